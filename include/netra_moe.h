@@ -1,0 +1,63 @@
+// FP8 E4M3 block-scaled routed-MoE for gfx950: kernel ABI of the engine
+// operations and the direct C entry points of libnetra_moe.so.
+//
+// Engine operations (code object netra_moe_gfx950.hsaco, launched through
+// netra_engine_* from include/netra_engine.h). Each kernel takes pointers
+// first, then u32 shape constants, in the order listed. They replace, in
+// order, the reference's router GEMV (kernels/gfx950/templates/routing/
+// bf16_gemv.inc:16-150), the external SGLang top-k + the shared-gate append
+// (runtime/gfx950/routing/decode/qwen36_shared_gate_append_bridge.hip:76-112),
+// the external AITER moe_sorting whose output format the reference consumes
+// (kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112),
+// the decode gate/up + SiLU-quant pair (moe/decode/gate_up_mfma.inc:12-161,
+// moe/decode/silu_quant.inc:16-236), the down GEMM (moe/decode/
+// down_reduce_mfma_2wave.inc:14-291) and the route reducer
+// (moe/prefill/route_reduce_splitk2_f16.inc:6-117):
+//
+//   netra_moe_router_logits_gfx950(x bf16[T,H], w bf16[E+S,H], logits bf16[T,E+S],
+//       mask u64[(E+S)*W]; T, H, rows=E+S, mask_words=(E+S)*W)
+//       grid (ceil(rows/16), T), block 256
+//   netra_moe_topk_quant_gfx950(logits, bias f32[E], x, ids i32[T,Ktot],
+//       weights f32[T,Ktot], xq e4m3[T,H], xs f32[T,H/128], mask; T, H, E, K, S, W)
+//       grid ceil(T/4), block 256
+//   netra_moe_sort_gfx950(ids, mask, sorted_ids i32[CAP*64], sorted_expert i32[CAP],
+//       num_valid i32[2], counts i32[E+S]; T, Ktot, Etot, W, CAP)
+//       grid 1, block 1024, dynamic LDS 4*(Etot*W + 2*Etot + 1)
+//   netra_moe_gate_up_gfx950(xq, xs, w13 e4m3[Etot,2I,H], w13s f32[Etot,2I/128,H/128],
+//       sorted_ids, sorted_expert, num_valid, hq e4m3[CAP*64,I], hs f32[CAP*64,I/128];
+//       T, H, I, Ktot, Etot)   grid (CAP, I/128), block 256
+//   netra_moe_down_gfx950(hq, hs, w2 e4m3[Etot,H,I], w2s f32[Etot,H/128,I/128],
+//       sorted_ids, sorted_expert, num_valid, partial f32[T*Ktot,H]; T, H, I, Ktot, Etot)
+//       grid (CAP, H/256), block 256
+//   netra_moe_combine_gfx950(partial, weights, out bf16[T,H]; T, H, Ktot)
+//       grid (ceil(H/1024), T), block 256
+//
+// with Ktot = K + S, Etot = E + S (the shared expert is expert E), W =
+// ceil(T/64) mask words per expert, CAP = ceil(T*Ktot/64) + Etot blocks.
+// Sorted ids are (slot << 24) | token; padding rows hold (Ktot << 24) | T.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// Weight preparation: fp32 w[groups, n, k] -> e4m3 q[groups, n, k] plus fp32
+// 128x128 block scales s[groups, n/128, k/128] (scale = max(amax, 1e-10) *
+// 0x3b124925, q = e4m3_rne(w * (1/scale))). n and k must be multiples of 128.
+// Replaces the checkpoint re-quantisation recipe the reference plans in
+// compiler/netra_compiler/layouts.py:175-206 and delegates to its loader.
+// Returns 0 or a hipError_t value (-1 for invalid shapes); the message is
+// available from netra_moe_last_error() on the calling thread, following the
+// reference bridges (runtime/gfx950/fp8/moe/qwen36_moe_silu_mul_quant_bridge.h:18-59).
+int netra_moe_quant_blocks(const float* w, uint8_t* q, float* s, uint32_t groups, uint32_t n,
+                           uint32_t k, hipStream_t stream);
+
+const char* netra_moe_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif

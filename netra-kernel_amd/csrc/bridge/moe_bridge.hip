@@ -1,0 +1,35 @@
+// Direct C entry points of libnetra_moe.so (weight preparation). The MoE
+// layer itself runs through the engine ABI; this library carries the kernels
+// that run once at weight-load time.
+#include "../../../include/netra_moe.h"
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "../kernels/moe_kernels.hip"
+
+namespace {
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& message) {
+  g_last_error = message;
+  return code;
+}
+}  // namespace
+
+extern "C" int netra_moe_quant_blocks(const float* w, uint8_t* q, float* s, uint32_t groups,
+                                      uint32_t n, uint32_t k, hipStream_t stream) {
+  if (!w || !q || !s || groups == 0 || n == 0 || k == 0 || n % 128u || k % 128u)
+    return fail(-1, "netra_moe_quant_blocks: null pointer or n/k not a positive multiple of 128");
+  const uint64_t blocks = static_cast<uint64_t>(groups) * (n / 128u) * (k / 128u);
+  if (blocks > 0x7fffffffull) return fail(-1, "netra_moe_quant_blocks: too many blocks");
+  hipLaunchKernelGGL(netra_moe_quant_blocks_gfx950, dim3(static_cast<uint32_t>(blocks)), dim3(256),
+                     0, stream, w, q, s, groups, n, k);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(static_cast<int>(err), hipGetErrorString(err));
+  g_last_error.clear();
+  return 0;
+}
+
+extern "C" const char* netra_moe_last_error(void) { return g_last_error.c_str(); }

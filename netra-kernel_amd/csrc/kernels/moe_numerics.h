@@ -1,0 +1,95 @@
+// Device numerics shared by the MoE kernels (gfx950, wave64).
+//
+// Every helper here is part of the layer's numeric contract: the same
+// operation sequence is evaluated on the CPU by the test oracle, so the results
+// are bit-identical. The kernels are compiled with -ffp-contract=off; every
+// fused multiply-add below is an explicit fmaf().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nk {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// 1/448 rounded to fp32 (0x3b124925): the FP8 scale constant of the
+// reference's quantisers (harness/gfx950/fp8/moe/decode/
+// qwen36_moe_silu_mul_quant_fp8_gfx950.hip:35, silu_quant.inc:40).
+__device__ __forceinline__ float inv_e4m3_max() { return __uint_as_float(0x3b124925u); }
+constexpr float kAmaxFloor = 1.0e-10f;
+
+__device__ __forceinline__ uint16_t bf16_rne(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
+__device__ __forceinline__ float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
+
+// OCP E4M3 (e4m3fn), round to nearest even, magnitudes >= 448 saturate,
+// NaN -> 0x7f. Integer re-rounding of the fp32 mantissa; no table.
+__device__ __forceinline__ uint32_t e4m3_rne(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;
+  const float fa = __uint_as_float(a);
+  if (fa >= 448.0f) return sign | 0x7eu;
+  if (fa < 0.015625f) return sign | (uint32_t)rintf(fa * 512.0f);
+  const uint32_t e = (a >> 23) - 127u + 7u;
+  const uint32_t mant = a & 0x7fffffu;
+  const uint32_t rounded = mant + 0x7ffffu + ((mant >> 20) & 1u);
+  uint32_t code = (e << 3) + (rounded >> 20);
+  code = code > 0x7eu ? 0x7eu : code;
+  return sign | code;
+}
+
+// Contract exp: Cody-Waite reduction with n = rint(x log2 e), ln2 split into
+// 0x3f317200 + 0x35bfbe8e, degree-7 Taylor polynomial of e^r in Horner form,
+// scaled by 2^n through the exponent field; x < -87 -> 0, x > 88 -> +inf.
+__device__ __forceinline__ float nexp(float x) {
+  if (x != x) return x;
+  if (x < -87.0f) return 0.0f;
+  if (x > 88.0f) return __uint_as_float(0x7f800000u);
+  const float n = rintf(x * 1.44269502162933349609375f);
+  float r = fmaf(-n, 0.693145751953125f, x);
+  r = fmaf(-n, 1.428606765330187045037746429443359375e-06f, r);
+  float p = 1.98412701138295233249664306640625e-04f;
+  p = fmaf(p, r, 1.388888922519981861114501953125e-03f);
+  p = fmaf(p, r, 8.333333767950534820556640625e-03f);
+  p = fmaf(p, r, 4.1666667163372039794921875e-02f);
+  p = fmaf(p, r, 1.6666667163372039794921875e-01f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int ni = (int)n;
+  return p * __uint_as_float((uint32_t)(ni + 127) << 23);
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + nexp(-g)); }
+__device__ __forceinline__ float sigmoid(float z) { return 1.0f / (1.0f + nexp(-z)); }
+
+// 32 contiguous FP8 bytes as one MFMA operand (two 16-byte loads).
+__device__ __forceinline__ v8i load_fp8x32(const uint8_t* p) {
+  const uint4 lo = *reinterpret_cast<const uint4*>(p);
+  const uint4 hi = *reinterpret_cast<const uint4*>(p + 16);
+  v8i r;
+  r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
+  r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
+  return r;
+}
+
+// D = A(16x128 e4m3) * B(128x16 e4m3), fp32 accumulate. Lane l supplies row
+// (l & 15) of A / column (l & 15) of B over K bytes [(l >> 4) * 32, +32); it
+// receives D rows (l >> 4) * 4 + j, column (l & 15), j = 0..3.
+__device__ __forceinline__ v4f mfma_e4m3_16x16x128(v8i a, v8i b) {
+  v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, zero, 0, 0, 0, 0, 0, 0);
+}
+
+}  // namespace nk

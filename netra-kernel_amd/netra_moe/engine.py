@@ -1,0 +1,232 @@
+"""Emit a netra-engine-1 directory for one fixed-shape MoE layer.
+
+The directory layout and engine.json fields are the ones the reference
+runtime reads (runtime/gfx950/engine/netra_engine.hip:273-383; emitted by
+compiler/netra_compiler/engine.py:373-504):
+
+  engine.json        format_version, target, wave_size, required_rocm,
+                     workspace_bytes, profiles[].guards, operations[] with
+                     launch/hsaco/kernel_symbol/typed arguments
+  contracts.json     one HIP kernel contract (stable nk_ id) per operation
+  graph_recipe.json  tensors, binding slots (profile, op, arg) per tensor and the
+                     RAW/WAR/WAW operation dependencies
+  memory_plan.json   workspace offsets of the engine-owned tensors
+  hsaco/             the code object
+
+Caller-owned tensors (inputs, weights, output and any intermediate the caller
+asks to see) are bound pointer slots; every other intermediate lives in the
+engine workspace.
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+import shutil
+from dataclasses import dataclass
+from pathlib import Path
+
+from .config import BLOCK_M, MoEConfig
+from .contracts import HipKernelContract, Launch, canonical_json
+from .profiles import profile_for
+from . import paths
+
+DTYPE_BYTES = {"bf16": 2, "f32": 4, "e4m3": 1, "i32": 4, "u64": 8}
+ALIGN = 256
+
+
+@dataclass(frozen=True)
+class TensorSpec:
+    name: str
+    dtype: str
+    shape: tuple[int, ...]
+    role: str  # input | weight | output | temporary
+
+    @property
+    def nbytes(self) -> int:
+        n = DTYPE_BYTES[self.dtype]
+        for d in self.shape:
+            n *= d
+        return n
+
+
+def tensor_table(cfg: MoEConfig) -> dict[str, TensorSpec]:
+    T, H, I = cfg.T, cfg.H, cfg.I
+    specs = [
+        TensorSpec("x", "bf16", (T, H), "input"),
+        TensorSpec("router_w", "bf16", (cfg.router_rows, H), "weight"),
+        TensorSpec("router_bias", "f32", (cfg.E,), "weight"),
+        TensorSpec("w13", "e4m3", (cfg.Etot, 2 * I, H), "weight"),
+        TensorSpec("w13_scale", "f32", (cfg.Etot, 2 * I // 128, H // 128), "weight"),
+        TensorSpec("w2", "e4m3", (cfg.Etot, H, I), "weight"),
+        TensorSpec("w2_scale", "f32", (cfg.Etot, H // 128, I // 128), "weight"),
+        TensorSpec("out", "bf16", (T, H), "output"),
+        TensorSpec("logits", "bf16", (T, cfg.router_rows), "temporary"),
+        TensorSpec("mask", "u64", (cfg.Etot, cfg.mask_words_per_expert), "temporary"),
+        TensorSpec("topk_ids", "i32", (T, cfg.Ktot), "temporary"),
+        TensorSpec("topk_weights", "f32", (T, cfg.Ktot), "temporary"),
+        TensorSpec("x_q", "e4m3", (T, H), "temporary"),
+        TensorSpec("x_scale", "f32", (T, H // 128), "temporary"),
+        TensorSpec("sorted_ids", "i32", (cfg.cap_rows,), "temporary"),
+        TensorSpec("sorted_expert", "i32", (cfg.cap_blocks,), "temporary"),
+        TensorSpec("num_valid", "i32", (2,), "temporary"),
+        TensorSpec("expert_counts", "i32", (cfg.Etot,), "temporary"),
+        TensorSpec("h_q", "e4m3", (cfg.cap_rows, I), "temporary"),
+        TensorSpec("h_scale", "f32", (cfg.cap_rows, I // 128), "temporary"),
+        TensorSpec("partial", "f32", (cfg.routes, H), "temporary"),
+    ]
+    return {s.name: s for s in specs}
+
+
+def operations(cfg: MoEConfig) -> list[dict]:
+    """The six launches of one layer call, in stream order."""
+    T, H, I = cfg.T, cfg.H, cfg.I
+    W = cfg.mask_words_per_expert
+    u = lambda v: ("u32", int(v))  # noqa: E731
+    return [
+        dict(name="moe.router_logits", symbol="netra_moe_router_logits_gfx950",
+             grid=((cfg.router_rows + 15) // 16, T, 1), block=(256, 1, 1), lds=0, dyn=0,
+             args=["x", "router_w", "logits", "mask", u(T), u(H), u(cfg.router_rows), u(cfg.Etot * W)],
+             reads=["x", "router_w"], writes=["logits", "mask"],
+             refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150"]),
+        dict(name="moe.topk_quant", symbol="netra_moe_topk_quant_gfx950",
+             grid=((T + 3) // 4, 1, 1), block=(256, 1, 1), lds=0, dyn=0,
+             args=["logits", "router_bias", "x", "topk_ids", "topk_weights", "x_q", "x_scale", "mask",
+                   u(T), u(H), u(cfg.E), u(cfg.K), u(cfg.S), u(W)],
+             reads=["logits", "router_bias", "x", "mask"],
+             writes=["topk_ids", "topk_weights", "x_q", "x_scale", "mask"],
+             refs=["runtime/gfx950/routing/decode/qwen36_shared_gate_append_bridge.hip:76-112"]),
+        dict(name="moe.sort", symbol="netra_moe_sort_gfx950",
+             grid=(1, 1, 1), block=(1024, 1, 1), lds=0, dyn=cfg.sort_lds_bytes,
+             args=["topk_ids", "mask", "sorted_ids", "sorted_expert", "num_valid", "expert_counts",
+                   u(T), u(cfg.Ktot), u(cfg.Etot), u(W), u(cfg.cap_blocks)],
+             reads=["topk_ids", "mask"],
+             writes=["sorted_ids", "sorted_expert", "num_valid", "expert_counts"],
+             refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]),
+        dict(name="moe.gate_up", symbol="netra_moe_gate_up_gfx950",
+             grid=(cfg.cap_blocks, I // 128, 1), block=(256, 1, 1), lds=1536, dyn=0,
+             args=["x_q", "x_scale", "w13", "w13_scale", "sorted_ids", "sorted_expert", "num_valid",
+                   "h_q", "h_scale", u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
+             reads=["x_q", "x_scale", "w13", "w13_scale", "sorted_ids", "sorted_expert", "num_valid"],
+             writes=["h_q", "h_scale"],
+             refs=["kernels/gfx950/templates/moe/decode/gate_up_mfma.inc:12-161",
+                   "kernels/gfx950/templates/moe/decode/silu_quant.inc:16-236"]),
+        dict(name="moe.down", symbol="netra_moe_down_gfx950",
+             grid=(cfg.cap_blocks, H // 256, 1), block=(256, 1, 1), lds=256, dyn=0,
+             args=["h_q", "h_scale", "w2", "w2_scale", "sorted_ids", "sorted_expert", "num_valid",
+                   "partial", u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
+             reads=["h_q", "h_scale", "w2", "w2_scale", "sorted_ids", "sorted_expert", "num_valid"],
+             writes=["partial"],
+             refs=["kernels/gfx950/templates/moe/decode/down_reduce_mfma_2wave.inc:14-291"]),
+        dict(name="moe.combine", symbol="netra_moe_combine_gfx950",
+             grid=((H + 1023) // 1024, T, 1), block=(256, 1, 1), lds=0, dyn=0,
+             args=["partial", "topk_weights", "out", u(T), u(H), u(cfg.Ktot)],
+             reads=["partial", "topk_weights"], writes=["out"],
+             refs=["kernels/gfx950/templates/moe/prefill/route_reduce_splitk2_f16.inc:6-117"]),
+    ]
+
+
+def _dependencies(ops: list[dict]) -> list[list[int]]:
+    deps = []
+    for i, op in enumerate(ops):
+        mine = set()
+        for j in range(i):
+            prev = ops[j]
+            raw = set(op["reads"]) & set(prev["writes"])
+            war = set(op["writes"]) & set(prev["reads"])
+            waw = set(op["writes"]) & set(prev["writes"])
+            if raw or war or waw:
+                mine.add(j)
+        deps.append(sorted(mine))
+    return deps
+
+
+def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ...] = (),
+                       hsaco: Path | None = None) -> dict:
+    """Write the engine directory; returns the graph recipe (also on disk)."""
+    directory = Path(directory)
+    hsaco = Path(hsaco) if hsaco else paths.hsaco_path()
+    if not hsaco.is_file():
+        raise FileNotFoundError(f"code object {hsaco} is missing; run the build first")
+    tensors = tensor_table(cfg)
+    unknown = set(expose) - set(tensors)
+    if unknown:
+        raise ValueError(f"cannot expose unknown tensors {sorted(unknown)}")
+    ops = operations(cfg)
+    code = hsaco.read_bytes()
+    sha = hashlib.sha256(code).hexdigest()
+
+    # Workspace: engine-owned temporaries, 256-byte aligned, no reuse.
+    offsets: dict[str, int] = {}
+    cursor = 0
+    for name, spec in tensors.items():
+        if spec.role == "temporary" and name not in expose:
+            offsets[name] = cursor
+            cursor += (spec.nbytes + ALIGN - 1) // ALIGN * ALIGN
+    workspace_bytes = cursor
+
+    bindings: dict[str, list[list[int]]] = {}
+    op_records, contracts = [], []
+    for oi, op in enumerate(ops):
+        arguments = []
+        for ai, a in enumerate(op["args"]):
+            if isinstance(a, tuple):
+                arguments.append({"kind": "u32_constant", "value": a[1]})
+            elif a in offsets:
+                arguments.append({"kind": "pointer", "source": "workspace", "tensor": a,
+                                  "workspace_offset": offsets[a]})
+            else:
+                arguments.append({"kind": "pointer", "source": "binding", "tensor": a})
+                bindings.setdefault(a, []).append([0, oi, ai])
+        launch = Launch(tuple(op["grid"]), tuple(op["block"]), op["lds"], op["dyn"])
+        kernarg = sum(4 if isinstance(a, tuple) else 8 for a in op["args"])
+        kernarg = (kernarg + 7) // 8 * 8
+        contract = HipKernelContract(
+            operation=op["name"], family="moe.fp8_block128.gfx950_hip", symbol=op["symbol"],
+            constants=(("T", cfg.T), ("H", cfg.H), ("I", cfg.I), ("E", cfg.E), ("K", cfg.K),
+                       ("S", cfg.S), ("BLOCK_M", BLOCK_M), ("SCALE_BLOCK", 128)),
+            semantics=(("abi", f"{op['symbol']}.ptr_then_u32.v1"),
+                       ("quantization", "fp8e4m3fn_block128x128_weights_1x128_activations.v1"),
+                       ("layouts", "row_major_expert_nk.sorted_m64_slot24.v1"),
+                       ("numerical", "router_16slice_fma_tree.topk_lowidx.exp_cw7.v1")),
+            launch=launch, kernarg_size=kernarg, code_object_sha256=sha,
+            source_refs=tuple(op["refs"]))
+        contracts.append(contract.to_dict())
+        op_records.append({
+            "name": op["name"], "execution": "kernel", "contract_id": contract.stable_id,
+            "launch": launch.to_dict(), "hsaco": "hsaco/" + hsaco.name,
+            "kernel_symbol": op["symbol"], "arguments": arguments,
+        })
+
+    profile = profile_for(cfg)
+    engine = {
+        "format_version": "netra-engine-1",
+        "target": "gfx950",
+        "wave_size": 64,
+        "required_rocm": {"minimum": "7.0", "code_object_version": 6},
+        "name": f"netra-moe-{cfg.name}",
+        "configuration": cfg.to_dict(),
+        "workspace_bytes": workspace_bytes,
+        "profiles": [{"name": profile.name, "guards": profile.to_dict()["guards"],
+                      "tensor_parallel": profile.tensor_parallel}],
+        "operations": op_records,
+    }
+    recipe = {
+        "format": "netra-graph-recipe-1",
+        "tensors": {n: {"dtype": s.dtype, "shape": list(s.shape), "role": s.role,
+                        "bytes": s.nbytes, "storage": "workspace" if n in offsets else "binding"}
+                    for n, s in tensors.items()},
+        "bindings": bindings,
+        "dependencies": _dependencies(ops),
+    }
+    memory_plan = {"workspace_bytes": workspace_bytes, "alignment": ALIGN,
+                   "offsets": offsets}
+
+    directory.mkdir(parents=True, exist_ok=True)
+    (directory / "hsaco").mkdir(exist_ok=True)
+    target = directory / "hsaco" / hsaco.name
+    if not target.exists() or target.read_bytes() != code:
+        shutil.copyfile(hsaco, target)
+    for fname, doc in (("engine.json", engine), ("contracts.json", {"contracts": contracts}),
+                       ("graph_recipe.json", recipe), ("memory_plan.json", memory_plan)):
+        (directory / fname).write_text(canonical_json(doc))
+    return recipe

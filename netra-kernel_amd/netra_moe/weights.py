@@ -1,0 +1,108 @@
+"""Weight preparation and synthetic layer inputs.
+
+quantize_blocks() runs the gfx950 weight-prep kernel (libnetra_moe.so,
+include/netra_moe.h) that turns fp32 expert weights into E4M3 with 128x128
+fp32 block scales. synthetic_* build the seeded inputs of the benchmark
+configurations: activations bf16 ~ N(0, 1), router and shared-gate weights
+bf16 ~ N(0, 0.02), expert weights ~ N(0, 0.02) quantised at setup, and for the
+speculative-verification config an expert bias log(Zipf(1.1)) over a seeded
+permutation of the routed experts.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import torch
+
+from . import paths
+from .config import MoEConfig
+
+_bridge = None
+
+
+def bridge_library() -> ctypes.CDLL:
+    global _bridge
+    if _bridge is None:
+        path = paths.bridge_library()
+        if not path.is_file():
+            raise FileNotFoundError(f"{path} is missing: build the native library first")
+        lib = ctypes.CDLL(str(path))
+        lib.netra_moe_quant_blocks.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_uint32] * 3 + [ctypes.c_void_p]
+        lib.netra_moe_quant_blocks.restype = ctypes.c_int
+        lib.netra_moe_last_error.argtypes = []
+        lib.netra_moe_last_error.restype = ctypes.c_char_p
+        _bridge = lib
+    return _bridge
+
+
+def quantize_blocks(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp32 [G, N, K] on the GPU -> (e4m3 bytes [G, N, K], fp32 scales [G, N/128, K/128])."""
+    if w.dim() != 3 or w.dtype != torch.float32 or not w.is_cuda or not w.is_contiguous():
+        raise ValueError("quantize_blocks needs a contiguous fp32 [G, N, K] GPU tensor")
+    g, n, k = w.shape
+    if n % 128 or k % 128:
+        raise ValueError("N and K must be multiples of 128")
+    q = torch.empty((g, n, k), dtype=torch.uint8, device=w.device)
+    s = torch.empty((g, n // 128, k // 128), dtype=torch.float32, device=w.device)
+    stream = torch.cuda.current_stream(w.device).cuda_stream
+    lib = bridge_library()
+    rc = lib.netra_moe_quant_blocks(w.data_ptr(), q.data_ptr(), s.data_ptr(), g, n, k, stream)
+    if rc != 0:
+        raise RuntimeError(f"netra_moe_quant_blocks failed ({rc}): {lib.netra_moe_last_error().decode()}")
+    return q, s
+
+
+def zipf_bias(E: int, seed: int, s: float = 1.1) -> np.ndarray:
+    """bias[e] = log p(rank(e)), p(r) proportional to r^-s over r = 1..E."""
+    ranks = np.arange(1, E + 1, dtype=np.float64)
+    p = ranks ** (-s)
+    p /= p.sum()
+    perm = np.random.default_rng(seed).permutation(E)
+    bias = np.empty(E, dtype=np.float32)
+    bias[perm] = np.log(p).astype(np.float32)
+    return bias
+
+
+def synthetic_activations(cfg: MoEConfig, device: torch.device | str = "cpu") -> dict[str, torch.Tensor]:
+    """x, router_w (router rows + shared-gate row), router_bias; generated on the CPU."""
+    g = torch.Generator().manual_seed(cfg.seed)
+    x = torch.randn((cfg.T, cfg.H), generator=g, dtype=torch.float32).to(torch.bfloat16)
+    router_w = (torch.randn((cfg.router_rows, cfg.H), generator=g, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+    if cfg.router_bias == "zipf1.1":
+        bias = torch.from_numpy(zipf_bias(cfg.E, cfg.seed))
+    else:
+        bias = torch.zeros(cfg.E, dtype=torch.float32)
+    return {"x": x.to(device), "router_w": router_w.to(device), "router_bias": bias.to(device)}
+
+
+def synthetic_expert_weights_f32(cfg: MoEConfig, seed: int, device: torch.device | str) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp32 W13 [Etot, 2I, H] and W2 [Etot, H, I] ~ N(0, 0.02)."""
+    dev = torch.device(device)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    w13 = torch.randn((cfg.Etot, 2 * cfg.I, cfg.H), generator=g, device=dev, dtype=torch.float32)
+    w13.mul_(0.02)
+    w2 = torch.randn((cfg.Etot, cfg.H, cfg.I), generator=g, device=dev, dtype=torch.float32)
+    w2.mul_(0.02)
+    return w13, w2
+
+
+def synthetic_expert_weights(cfg: MoEConfig, seed: int, device: torch.device | str) -> dict[str, torch.Tensor]:
+    """Quantised expert weights generated and prepared on the GPU."""
+    w13, w2 = synthetic_expert_weights_f32(cfg, seed, device)
+    q13, s13 = quantize_blocks(w13)
+    del w13
+    q2, s2 = quantize_blocks(w2)
+    del w2
+    return {"w13": q13, "w13_scale": s13, "w2": q2, "w2_scale": s2}
+
+
+def expert_bytes_touched(cfg: MoEConfig, topk_ids: np.ndarray) -> tuple[int, int]:
+    """(distinct experts touched, their weight+scale bytes) for one call's routing."""
+    touched = int(np.unique(topk_ids.reshape(-1)).size)
+    return touched, touched * cfg.expert_bytes()
+
+
+def flops_to_tflops(flops: int, seconds: float) -> float:
+    return flops / seconds / 1e12 if seconds > 0 else math.nan

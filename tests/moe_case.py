@@ -1,0 +1,83 @@
+"""Shared set-up for GPU parity tests, smoke() and the CPU baseline: seeded
+inputs for one configuration, the engine run with every intermediate exposed,
+and the oracle's answer on the same bytes."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import oracle
+from netra_moe.config import MoEConfig
+from netra_moe.engine import tensor_table
+from netra_moe.layer import MoELayer
+from netra_moe import weights as W
+
+ALL_INTERMEDIATES = ("logits", "mask", "topk_ids", "topk_weights", "x_q", "x_scale", "sorted_ids",
+                     "sorted_expert", "num_valid", "expert_counts", "h_q", "h_scale", "partial")
+WEIGHT_SEED = 77
+
+
+def bf16_bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def make_inputs(cfg: MoEConfig, device: torch.device, weights_on_gpu: bool | None = None):
+    """Activations from the CPU generator; expert weights quantised by the
+    oracle (small shapes) or by the GPU weight-prep kernel (full shapes)."""
+    act = W.synthetic_activations(cfg, "cpu")
+    if weights_on_gpu is None:
+        weights_on_gpu = cfg.Etot * cfg.I * cfg.H > (1 << 24)
+    if weights_on_gpu:
+        wq = W.synthetic_expert_weights(cfg, WEIGHT_SEED, device)
+        torch.cuda.synchronize(device)
+    else:
+        w13, w2 = W.synthetic_expert_weights_f32(cfg, WEIGHT_SEED, "cpu")
+        q13, s13 = oracle.quant_blocks_f32(w13.numpy())
+        q2, s2 = oracle.quant_blocks_f32(w2.numpy())
+        wq = {"w13": torch.from_numpy(q13).to(device), "w13_scale": torch.from_numpy(s13).to(device),
+              "w2": torch.from_numpy(q2).to(device), "w2_scale": torch.from_numpy(s2).to(device)}
+    gpu = {"router_w": act["router_w"].to(device), "router_bias": act["router_bias"].to(device), **wq}
+    host = {
+        "x": bf16_bits(act["x"]),
+        "router_w": bf16_bits(act["router_w"]),
+        "router_bias": act["router_bias"].numpy(),
+        "w13": wq["w13"].cpu().numpy(), "w13_scale": wq["w13_scale"].cpu().numpy(),
+        "w2": wq["w2"].cpu().numpy(), "w2_scale": wq["w2_scale"].cpu().numpy(),
+    }
+    return act["x"].to(device), gpu, host
+
+
+def run_gpu(cfg: MoEConfig, x: torch.Tensor, gpu_weights: dict, device: torch.device,
+            expose=ALL_INTERMEDIATES, graph: bool = False, repeats: int = 1):
+    layer = MoELayer(cfg, gpu_weights, device=device.index or 0, expose=expose, graph=graph)
+    outs = []
+    for _ in range(repeats):
+        layer.forward(x)
+        torch.cuda.synchronize(device)
+        outs.append(bf16_bits(layer.out))
+    res = {"out": outs[-1], "runs": outs}
+    for name in expose:
+        t = layer.buffer(name).detach().cpu()
+        if t.dtype == torch.bfloat16:
+            res[name] = bf16_bits(t)
+        else:
+            res[name] = t.numpy().copy()
+    layer.close()
+    return res
+
+
+def oracle_routing(cfg: MoEConfig, host: dict) -> dict:
+    logits = oracle.router_logits(host["x"], host["router_w"])
+    ids, wts = oracle.topk(logits, host["router_bias"], cfg.E, cfg.K, cfg.S)
+    x_q, x_s = oracle.quant_rows_bf16(host["x"])
+    sid, sexp, nv, counts = oracle.sort(ids, cfg.Etot, cfg.cap_blocks)
+    return dict(logits=logits, topk_ids=ids, topk_weights=wts, x_q=x_q, x_scale=x_s,
+                sorted_ids=sid, sorted_expert=sexp, num_valid=nv, expert_counts=counts)
+
+
+def sample_tokens(cfg: MoEConfig, n: int) -> np.ndarray:
+    if cfg.T <= n:
+        return np.arange(cfg.T, dtype=np.int64)
+    rng = np.random.default_rng(cfg.seed + 5)
+    picks = rng.choice(cfg.T, size=n, replace=False)
+    return np.unique(np.concatenate([[0, cfg.T - 1], picks]))[:n].astype(np.int64)

@@ -92,7 +92,11 @@ class MoELayer:
             self.x.copy_(x)
         stream = self._stream()
         if self.graph and not self._prepared:
-            self.engine.prepare(0, stream)
+            # Capture needs a non-legacy stream; the executable graph then
+            # replays on whatever stream the caller launches it on.
+            capture = torch.cuda.Stream(self.device)
+            self.engine.prepare(0, capture.cuda_stream)
+            self._capture_stream = capture
             self._prepared = True
         self.engine.launch(0, self.shape, stream)
         return self.out

@@ -4,8 +4,8 @@ Bars: router logits, top-k ids and weights, the 1x128 input quant, expert
 counts, the sorted permutation and the expert-block table are bit-exact; the
 layer output is within max|y - y_ref| / max|y_ref| <= 2e-2 of the fp64-
 accumulated oracle (checked on every token for T <= 64 and on a seeded sample
-of tokens above that). The FP8 intermediate h is compared with the same
-tolerance on the rows the oracle recomputes.
+of tokens above that). The FP8 intermediate h must agree code-for-code up to
+one E4M3 rounding step on the rows the oracle recomputes.
 """
 import numpy as np
 import pytest
@@ -58,6 +58,12 @@ def test_counts_sort_permutation_bit_exact(case):
 
 
 def test_gate_up_silu_quant_rows(case):
+    """FP8 h on the rows the oracle recomputes. h is bf16 before requant and the
+    fp32 accumulation order differs, so a group max may move by one bf16 step
+    (scale ratio within 2^-7) and an element by one E4M3 step (dequantised
+    difference within 1/8 relative + 1.5% for the scale); elements near zero,
+    where g or u cancel, may move by up to two subnormal steps (2^-9 * scale
+    each); fewer than 1% of codes may differ."""
     cfg, host, got, ref = case
     nv = int(ref["num_valid"][0])
     rows = min(nv, 1024)
@@ -65,12 +71,22 @@ def test_gate_up_silu_quant_rows(case):
                                  ref["sorted_ids"], ref["sorted_expert"], rows, cfg.T, cfg.H, cfg.I)
     t = ref["sorted_ids"][:rows] & 0xFFFFFF
     valid = t < cfg.T
-    table = oracle.e4m3_table()
-    h_ref = table[h_q[:rows][valid]].astype(np.float64) * np.repeat(h_s[:rows][valid], 128, axis=1)
-    h_got = table[got["h_q"][:rows][valid]].astype(np.float64) * np.repeat(got["h_scale"][:rows][valid], 128, axis=1)
-    err = oracle.max_abs_rel(h_got, h_ref)
-    print(f"[parity] {cfg.name} h max_abs_rel={err:.3e} rows={int(valid.sum())}")
-    assert err <= TOL
+    s_ref = h_s[:rows][valid].astype(np.float64)
+    s_got = got["h_scale"][:rows][valid].astype(np.float64)
+    q_ref, q_got = h_q[:rows][valid], got["h_q"][:rows][valid]
+    table = oracle.e4m3_table().astype(np.float64)
+    d_ref = table[q_ref] * np.repeat(s_ref, 128, axis=1)
+    d_got = table[q_got] * np.repeat(s_got, 128, axis=1)
+    scale_rel = float(np.max(np.abs(s_got - s_ref) / s_ref))
+    smax = np.repeat(np.maximum(s_ref, s_got), 128, axis=1)
+    bound = 0.14 * np.maximum(np.abs(d_ref), np.abs(d_got)) + smax * 2.0 ** -8 * 1.01
+    excess = float(np.max(np.abs(d_got - d_ref) - bound))
+    frac = float(np.mean(q_ref != q_got))
+    print(f"[parity] {cfg.name} h rows={int(valid.sum())} scale_rel={scale_rel:.2e} "
+          f"code_mismatch={frac:.2e} worst_excess={excess:.2e}")
+    assert scale_rel <= 2.0 ** -7
+    assert excess <= 0.0
+    assert frac < 1e-2
 
 
 def test_layer_output_within_tolerance(case):

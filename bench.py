@@ -133,6 +133,7 @@ def main() -> int:
 
     from netra_moe import weights as W
     from netra_moe.config import BASELINE_CONFIGS
+    from netra_moe.engine import OP_NAMES
     from netra_moe.layer import MoELayer
 
     if not torch.cuda.is_available():
@@ -142,7 +143,9 @@ def main() -> int:
     torch.cuda.set_device(dev)
     cfg = BASELINE_CONFIGS[args.config]
     log(f"[bench] weights: 2 copies of {cfg.Etot} experts ({2 * cfg.Etot * cfg.expert_bytes() / 1e9:.2f} GB)")
-    wsets = [W.synthetic_expert_weights(cfg, WEIGHT_SEED + i, dev) for i in range(2)]
+    # copy 0 also keeps its row-major bytes: the CPU baseline reads that layout
+    wsets = [W.synthetic_expert_weights(cfg, WEIGHT_SEED + i, dev, keep_row_major=(i == 0))
+             for i in range(2)]
     torch.cuda.synchronize()
 
     def run_config(c, steps, warmup, with_kernels):
@@ -172,7 +175,7 @@ def main() -> int:
                 lay.x.copy_(act["x"].to(dev))
                 dl.append(lay)
             kern = {}
-            for op in ("router_logits", "topk_quant", "sort", "gate_up", "down", "combine"):
+            for op in OP_NAMES:
                 kern[op] = time_operation(dl, op, max(20, steps // 2), torch) * 1e3  # us
             for lay in dl:
                 lay.close()
@@ -201,7 +204,10 @@ def main() -> int:
     if not args.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)
         log(f"[bench] cpu baseline on {threads} threads")
-        w_host = {k: v.cpu().numpy() for k, v in wsets[0].items()}
+        w_host = {"w13": wsets[0]["w13_row_major"].cpu().numpy(),
+                  "w13_scale": wsets[0]["w13_scale"].cpu().numpy(),
+                  "w2": wsets[0]["w2_row_major"].cpu().numpy(),
+                  "w2_scale": wsets[0]["w2_scale"].cpu().numpy()}
         cpu = cpu_baseline(cfg, act, w_host, threads, args.cpu_seconds)
 
     line = {

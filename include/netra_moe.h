@@ -14,26 +14,34 @@
 // down_reduce_mfma_2wave.inc:14-291) and the route reducer
 // (moe/prefill/route_reduce_splitk2_f16.inc:6-117):
 //
-//   netra_moe_router_logits_gfx950(x bf16[T,H], w bf16[E+S,H], logits bf16[T,E+S],
-//       mask u64[(E+S)*W]; T, H, rows=E+S, mask_words=(E+S)*W)
-//       grid (ceil(rows/16), T), block 256
-//   netra_moe_topk_quant_gfx950(logits, bias f32[E], x, ids i32[T,Ktot],
-//       weights f32[T,Ktot], xq e4m3[T,H], xs f32[T,H/128], mask; T, H, E, K, S, W)
-//       grid ceil(T/4), block 256
+//   netra_moe_router_h<H>_gfx950, H in {512,1024,2048,4096} (x bf16[T,H],
+//       w bf16[E+S,H], logits bf16[T,E+S], xq e4m3[T,H], xs f32[T,H/128],
+//       mask u64[(E+S)*W]; T, H, rows=E+S, (E+S)*W)
+//       grid (ceil(rows/16), ceil(T/4)), block 256
+//   netra_moe_topk_gfx950(logits, bias f32[E], ids i32[T,Ktot], weights f32[T,Ktot],
+//       mask; T, E, K, S, W)   grid ceil(T/4), block 256
 //   netra_moe_sort_gfx950(ids, mask, sorted_ids i32[CAP*64], sorted_expert i32[CAP],
-//       num_valid i32[2], counts i32[E+S]; T, Ktot, Etot, W, CAP)
-//       grid 1, block 1024, dynamic LDS 4*(Etot*W + 2*Etot + 1)
-//   netra_moe_gate_up_gfx950(xq, xs, w13 e4m3[Etot,2I,H], w13s f32[Etot,2I/128,H/128],
-//       sorted_ids, sorted_expert, num_valid, hq e4m3[CAP*64,I], hs f32[CAP*64,I/128];
-//       T, H, I, Ktot, Etot)   grid (CAP, I/128), block 256
-//   netra_moe_down_gfx950(hq, hs, w2 e4m3[Etot,H,I], w2s f32[Etot,H/128,I/128],
-//       sorted_ids, sorted_expert, num_valid, partial f32[T*Ktot,H]; T, H, I, Ktot, Etot)
-//       grid (CAP, H/256), block 256
+//       tile_map i32[CAPT], num_valid i32[4], counts i32[E+S]; T, Ktot, Etot, W, CAP)
+//       grid 1, block 1024, dynamic LDS 4*(Etot*W + 3*Etot + 2 + CAP)
+//   decode ("stream") GEMMs, H in {512,1024,2048,4096}, I in {256,512,1024,2048}:
+//   netra_moe_gate_up_stream_h<H>_gfx950(xq, xs, w13 e4m3[Etot,2I,H],
+//       w13s f32[Etot,2I/128,H/128], sorted_ids, sorted_expert, tile_map, num_valid,
+//       h bf16[CAP*64,I]; T, H, I, Ktot, Etot)   grid 512, block 256 (persistent)
+//   netra_moe_down_stream_i<I>_gfx950(h, w2 e4m3[Etot,H,I], w2s f32[Etot,H/128,I/128],
+//       sorted_ids, sorted_expert, tile_map, num_valid, partial f32[T*Ktot,H];
+//       T, H, I, Ktot, Etot)   grid 768, block 256 (persistent)
+//   prefill ("tile") GEMMs:
+//   netra_moe_gate_up_tile_gfx950(xq, xs, w13, w13s, sorted_ids, sorted_expert,
+//       num_valid, hq e4m3[CAP*64,I], hs f32[CAP*64,I/128]; T, H, I, Ktot, Etot)
+//       grid (CAP, I/128), block 256
+//   netra_moe_down_tile_gfx950(hq, hs, w2, w2s, sorted_ids, sorted_expert, num_valid,
+//       partial; T, H, I, Ktot, Etot)   grid (CAP, H/256), block 256
 //   netra_moe_combine_gfx950(partial, weights, out bf16[T,H]; T, H, Ktot)
 //       grid (ceil(H/1024), T), block 256
 //
 // with Ktot = K + S, Etot = E + S (the shared expert is expert E), W =
-// ceil(T/64) mask words per expert, CAP = ceil(T*Ktot/64) + Etot blocks.
+// ceil(T/64) mask words per expert, CAP = ceil(T*Ktot/64) + Etot blocks,
+// CAPT = ceil(T*Ktot/16) + Etot row tiles.
 // Sorted ids are (slot << 24) | token; padding rows hold (Ktot << 24) | T.
 #pragma once
 
@@ -55,6 +63,22 @@ extern "C" {
 // reference bridges (runtime/gfx950/fp8/moe/qwen36_moe_silu_mul_quant_bridge.h:18-59).
 int netra_moe_quant_blocks(const float* w, uint8_t* q, float* s, uint32_t groups, uint32_t n,
                            uint32_t k, hipStream_t stream);
+
+// Weight layout change for the GEMM kernels: row-major e4m3 src[groups, n, k]
+// -> dst in the tile16x128 layout (n/16 x k/128 tiles, row tiles outermost;
+// inside a tile lane l's 32 bytes are row l % 16, columns (l / 16) * 32 .. +31,
+// at byte l * 32). n % 16 == 0, k % 128 == 0, src and dst distinct. The
+// reference consumes AITER's own shuffled layout
+// (kernels/gfx950/templates/common/addressing.inc:22-27); this is the
+// layout of this build's kernels. Same error convention as above.
+int netra_moe_pack_tiles(const uint8_t* src, uint8_t* dst, uint32_t groups, uint32_t n,
+                         uint32_t k, hipStream_t stream);
+
+// Conversion self-check: writes the contract's integer E4M3 encoding (sw) and
+// the hardware conversion used by the hot kernels (hw) of n fp32 inputs.
+// No counterpart in the reference; tests use it to prove the two agree.
+int netra_moe_e4m3_check(const float* in, uint8_t* sw, uint8_t* hw, uint32_t n,
+                         hipStream_t stream);
 
 const char* netra_moe_last_error(void);
 

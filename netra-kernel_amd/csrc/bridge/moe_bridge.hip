@@ -32,4 +32,29 @@ extern "C" int netra_moe_quant_blocks(const float* w, uint8_t* q, float* s, uint
   return 0;
 }
 
+extern "C" int netra_moe_pack_tiles(const uint8_t* src, uint8_t* dst, uint32_t groups, uint32_t n,
+                                    uint32_t k, hipStream_t stream) {
+  if (!src || !dst || src == dst || groups == 0 || n == 0 || k == 0 || n % 16u || k % 128u)
+    return fail(-1, "netra_moe_pack_tiles: null/aliased pointers or n % 16, k % 128 != 0");
+  const uint64_t tiles = static_cast<uint64_t>(groups) * (n / 16u) * (k / 128u);
+  if (tiles > 0xfffffffcull) return fail(-1, "netra_moe_pack_tiles: too many tiles");
+  hipLaunchKernelGGL(netra_moe_pack_tiles_gfx950, dim3(static_cast<uint32_t>((tiles + 3u) / 4u)),
+                     dim3(256), 0, stream, src, dst, groups, n, k);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(static_cast<int>(err), hipGetErrorString(err));
+  g_last_error.clear();
+  return 0;
+}
+
+extern "C" int netra_moe_e4m3_check(const float* in, uint8_t* sw, uint8_t* hw, uint32_t n,
+                                    hipStream_t stream) {
+  if (!in || !sw || !hw || n == 0) return fail(-1, "netra_moe_e4m3_check: null pointer or n == 0");
+  const uint32_t grid = (n + 1023u) / 1024u;
+  hipLaunchKernelGGL(netra_moe_e4m3_check_gfx950, dim3(grid), dim3(256), 0, stream, in, sw, hw, n);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(static_cast<int>(err), hipGetErrorString(err));
+  g_last_error.clear();
+  return 0;
+}
+
 extern "C" const char* netra_moe_last_error(void) { return g_last_error.c_str(); }

@@ -1,0 +1,110 @@
+// Top-k weighted combine and the weight-preparation quantiser.
+#pragma once
+#include "moe_numerics.h"
+
+#define NK_KERNEL extern "C" __global__
+
+// ---------------------------------------------------------------------------
+// Top-k weighted combine (reference: kernels/gfx950/templates/moe/prefill/
+// route_reduce_splitk2_f16.inc:6-117 and down_reduce_mfma_2wave.inc:202-213:
+// slot-ordered weighted sum, then bf16). out[t, n] = bf16(sum over slots in
+// order of fmaf(w[t, s], partial[t * Ktot + s, n], acc)).
+NK_KERNEL __launch_bounds__(256) void netra_moe_combine_gfx950(
+    const float* __restrict__ partial, const float* __restrict__ weights,
+    uint16_t* __restrict__ out, uint32_t T, uint32_t H, uint32_t Ktot) {
+  const uint32_t t = blockIdx.y;
+  const uint32_t n = (blockIdx.x * 256u + threadIdx.x) * 4u;
+  if (t >= T || n >= H) return;
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  for (uint32_t s = 0; s < Ktot; ++s) {
+    const float w = weights[(size_t)t * Ktot + s];
+    const float4 p = *reinterpret_cast<const float4*>(partial + ((size_t)t * Ktot + s) * H + n);
+    a0 = fmaf(w, p.x, a0);
+    a1 = fmaf(w, p.y, a1);
+    a2 = fmaf(w, p.z, a2);
+    a3 = fmaf(w, p.w, a3);
+  }
+  uint2 o;
+  o.x = (uint32_t)nk::bf16_rne(a0) | ((uint32_t)nk::bf16_rne(a1) << 16);
+  o.y = (uint32_t)nk::bf16_rne(a2) | ((uint32_t)nk::bf16_rne(a3) << 16);
+  *reinterpret_cast<uint2*>(out + (size_t)t * H + n) = o;
+}
+
+// ---------------------------------------------------------------------------
+// Weight preparation: fp32 [groups, n, k] -> e4m3 + fp32 128x128 block scales
+// (scale = max(amax, 1e-10) * 0x3b124925, q = e4m3(w * (1 / scale))); one
+// workgroup per 128x128 block (reference recipe: compiler/netra_compiler/
+// layouts.py:175-206 plans the scale layout [groups, n/128, k/128]).
+NK_KERNEL __launch_bounds__(256) void netra_moe_quant_blocks_gfx950(
+    const float* __restrict__ w, uint8_t* __restrict__ q, float* __restrict__ s,
+    uint32_t groups, uint32_t n, uint32_t k) {
+  __shared__ float s_max[4];
+  const uint32_t nb = n / 128u, kb = k / 128u;
+  const uint32_t blk = blockIdx.x;
+  if (blk >= groups * nb * kb) return;
+  const uint32_t g = blk / (nb * kb), bn = (blk / kb) % nb, bk = blk % kb;
+  const size_t base = ((size_t)g * n + bn * 128u) * k + bk * 128u;
+  const uint32_t tid = threadIdx.x;
+  // thread owns column 4*(tid&31)..+3 of rows (tid>>5) + 8 i, i = 0..15
+  const uint32_t col = (tid & 31u) * 4u, row0 = tid >> 5;
+  float amax = nk::kAmaxFloor;
+  for (uint32_t i = 0; i < 16u; ++i) {
+    const float4 v = *reinterpret_cast<const float4*>(w + base + (size_t)(row0 + 8u * i) * k + col);
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+#pragma unroll
+  for (uint32_t off = 1; off < 64; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  if ((tid & 63u) == 0) s_max[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+  const float scale = amax * nk::inv_e4m3_max();
+  const float inv = 1.0f / scale;
+  if (tid == 0) s[blk] = scale;
+  for (uint32_t i = 0; i < 16u; ++i) {
+    const size_t off = base + (size_t)(row0 + 8u * i) * k + col;
+    const float4 v = *reinterpret_cast<const float4*>(w + off);
+    const uint32_t packed = nk::e4m3_rne(v.x * inv) | (nk::e4m3_rne(v.y * inv) << 8) |
+                            (nk::e4m3_rne(v.z * inv) << 16) | (nk::e4m3_rne(v.w * inv) << 24);
+    *reinterpret_cast<uint32_t*>(q + off) = packed;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Conversion self-check: the integer E4M3 encoder (the contract, shared with
+// the CPU oracle) next to the hardware conversion the hot kernels use.
+NK_KERNEL __launch_bounds__(256) void netra_moe_e4m3_check_gfx950(
+    const float* __restrict__ in, uint8_t* __restrict__ sw, uint8_t* __restrict__ hw, uint32_t n) {
+  const uint32_t i = (blockIdx.x * 256u + threadIdx.x) * 4u;
+  if (i >= n) return;
+  float v[4];
+#pragma unroll
+  for (uint32_t k = 0; k < 4; ++k) v[k] = (i + k < n) ? in[i + k] : 0.0f;
+  const uint32_t h = nk::e4m3x4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+  for (uint32_t k = 0; k < 4; ++k) {
+    if (i + k < n) {
+      sw[i + k] = (uint8_t)nk::e4m3_rne(v[k]);
+      hw[i + k] = (uint8_t)(h >> (8u * k));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Weight layout change: row-major e4m3 [groups, n, k] -> tile16x128 (see
+// nk::tile_operand). One wave per 16 x 128 tile; lane l moves row l & 15,
+// columns (l >> 4) * 32 .. +31 to tile offset l * 32.
+NK_KERNEL __launch_bounds__(256) void netra_moe_pack_tiles_gfx950(
+    const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t groups, uint32_t n,
+    uint32_t k) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t tile = blockIdx.x * 4u + (threadIdx.x >> 6);
+  const uint32_t nt = n / 16u, kb = k / 128u;
+  if (tile >= groups * nt * kb) return;
+  const uint32_t g = tile / (nt * kb), rt = (tile / kb) % nt, cb = tile % kb;
+  const uint8_t* s = src + ((size_t)g * n + rt * 16u + (lane & 15u)) * k + cb * 128u + (lane >> 4) * 32u;
+  const uint4 lo = *reinterpret_cast<const uint4*>(s);
+  const uint4 hi = *reinterpret_cast<const uint4*>(s + 16);
+  uint8_t* d = dst + (size_t)tile * 2048u + lane * 32u;
+  *reinterpret_cast<uint4*>(d) = lo;
+  *reinterpret_cast<uint4*>(d + 16) = hi;
+}

@@ -49,6 +49,21 @@ __device__ __forceinline__ uint32_t e4m3_rne(float x) {
   return sign | code;
 }
 
+// Four E4M3 encodings through the gfx950 conversion instruction
+// (v_cvt_pk_fp8_f32: OCP e4m3fn, round to nearest even). Inputs are clamped to
+// +-448 first, which reproduces the saturating rule of e4m3_rne for every
+// finite input (netra_moe_e4m3_check compares the two on the device); NaN
+// inputs, which the layer never produces from finite data, are outside the
+// contract. Byte i of the result encodes argument i.
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+  a = fminf(fmaxf(a, -448.0f), 448.0f);
+  b = fminf(fmaxf(b, -448.0f), 448.0f);
+  c = fminf(fmaxf(c, -448.0f), 448.0f);
+  d = fminf(fmaxf(d, -448.0f), 448.0f);
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+
 // Contract exp: Cody-Waite reduction with n = rint(x log2 e), ln2 split into
 // 0x3f317200 + 0x35bfbe8e, degree-7 Taylor polynomial of e^r in Horner form,
 // scaled by 2^n through the exponent field; x < -87 -> 0, x > 88 -> +inf.
@@ -82,6 +97,16 @@ __device__ __forceinline__ v8i load_fp8x32(const uint8_t* p) {
   r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
   r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
   return r;
+}
+
+// Packed expert-weight layout ("tile16x128"): a [N, K] e4m3 matrix is stored
+// as N/16 x K/128 tiles, row tiles outermost; inside a tile the 64 lanes' MFMA
+// operands lie back to back, lane l holding row l & 15, columns
+// (l >> 4) * 32 .. +31. One wave load of 32 bytes per lane therefore reads a
+// contiguous 2 KiB, and a 16-row tile's full K extent is contiguous.
+__device__ __forceinline__ const uint8_t* tile_operand(const uint8_t* matrix, uint32_t row_tile,
+                                                       uint32_t kb, uint32_t kblocks, uint32_t lane) {
+  return matrix + ((size_t)row_tile * kblocks + kb) * 2048u + lane * 32u;
 }
 
 // D = A(16x128 e4m3) * B(128x16 e4m3), fp32 accumulate. Lane l supplies row

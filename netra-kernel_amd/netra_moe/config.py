@@ -75,7 +75,12 @@ class MoEConfig:
 
     @property
     def sort_lds_bytes(self) -> int:
-        return 4 * (self.Etot * self.mask_words_per_expert + 2 * self.Etot + 1)
+        return 4 * (self.Etot * self.mask_words_per_expert + 3 * self.Etot + 2 + self.cap_blocks)
+
+    @property
+    def cap_tiles(self) -> int:
+        """Upper bound on non-empty 16-row tiles: sum over experts of ceil(rows / 16)."""
+        return (self.routes + 15) // 16 + self.Etot
 
     def flops(self) -> int:
         """Algorithmic FLOPs of one layer call: router + every routed/shared row."""

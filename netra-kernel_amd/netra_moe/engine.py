@@ -49,7 +49,28 @@ class TensorSpec:
         return n
 
 
-def tensor_table(cfg: MoEConfig) -> dict[str, TensorSpec]:
+GEMM_PATHS = ("stream", "tile")
+STREAM_H = (512, 1024, 2048, 4096)   # netra_moe_gate_up_stream_h<H>_gfx950
+STREAM_I = (256, 512, 1024, 2048)    # netra_moe_down_stream_i<I>_gfx950
+# Persistent stream kernels: 256 CUs x 4 SIMDs x resident waves per SIMD
+# (NK_GATE_UP_WAVES_PER_EU = 2, NK_DOWN_WAVES_PER_EU = 3) / 4 waves per group.
+STREAM_GRID_GATE_UP = 512
+STREAM_GRID_DOWN = 768
+
+
+def resolve_path(cfg: MoEConfig, path: str = "auto") -> str:
+    """stream: split-K weight streaming (decode-sized T); tile: 64-row block tiles."""
+    if path == "auto":
+        path = "stream" if cfg.T <= 256 else "tile"
+    if path not in GEMM_PATHS:
+        raise ValueError(f"unknown GEMM path {path!r}")
+    if path == "stream" and (cfg.H not in STREAM_H or cfg.I not in STREAM_I):
+        raise ValueError(f"stream path kernels exist for H in {STREAM_H} and I in {STREAM_I}")
+    return path
+
+
+def tensor_table(cfg: MoEConfig, path: str = "auto") -> dict[str, TensorSpec]:
+    path = resolve_path(cfg, path)
     T, H, I = cfg.T, cfg.H, cfg.I
     specs = [
         TensorSpec("x", "bf16", (T, H), "input"),
@@ -68,61 +89,99 @@ def tensor_table(cfg: MoEConfig) -> dict[str, TensorSpec]:
         TensorSpec("x_scale", "f32", (T, H // 128), "temporary"),
         TensorSpec("sorted_ids", "i32", (cfg.cap_rows,), "temporary"),
         TensorSpec("sorted_expert", "i32", (cfg.cap_blocks,), "temporary"),
-        TensorSpec("num_valid", "i32", (2,), "temporary"),
+        TensorSpec("tile_map", "i32", (cfg.cap_tiles,), "temporary"),
+        TensorSpec("num_valid", "i32", (4,), "temporary"),
         TensorSpec("expert_counts", "i32", (cfg.Etot,), "temporary"),
-        TensorSpec("h_q", "e4m3", (cfg.cap_rows, I), "temporary"),
-        TensorSpec("h_scale", "f32", (cfg.cap_rows, I // 128), "temporary"),
-        TensorSpec("partial", "f32", (cfg.routes, H), "temporary"),
     ]
+    if path == "stream":
+        specs.append(TensorSpec("h", "bf16", (cfg.cap_rows, I), "temporary"))
+    else:
+        specs += [TensorSpec("h_q", "e4m3", (cfg.cap_rows, I), "temporary"),
+                  TensorSpec("h_scale", "f32", (cfg.cap_rows, I // 128), "temporary")]
+    specs.append(TensorSpec("partial", "f32", (cfg.routes, H), "temporary"))
     return {s.name: s for s in specs}
 
 
-def operations(cfg: MoEConfig) -> list[dict]:
+OP_NAMES = ("router", "topk", "sort", "gate_up", "down", "combine")
+ROUTER_H = (512, 1024, 2048, 4096)   # netra_moe_router_h<H>_gfx950
+ROUTER_TOKENS = 4                     # tokens per router workgroup (kRouterTokens)
+
+
+def operations(cfg: MoEConfig, path: str = "auto") -> list[dict]:
     """The six launches of one layer call, in stream order."""
+    path = resolve_path(cfg, path)
     T, H, I = cfg.T, cfg.H, cfg.I
     W = cfg.mask_words_per_expert
+    if H not in ROUTER_H:
+        raise ValueError(f"router kernels exist for H in {ROUTER_H}")
     u = lambda v: ("u32", int(v))  # noqa: E731
-    return [
-        dict(name="moe.router_logits", symbol="netra_moe_router_logits_gfx950",
-             grid=((cfg.router_rows + 15) // 16, T, 1), block=(256, 1, 1), lds=0, dyn=0,
-             args=["x", "router_w", "logits", "mask", u(T), u(H), u(cfg.router_rows), u(cfg.Etot * W)],
-             reads=["x", "router_w"], writes=["logits", "mask"],
-             refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150"]),
-        dict(name="moe.topk_quant", symbol="netra_moe_topk_quant_gfx950",
-             grid=((T + 3) // 4, 1, 1), block=(256, 1, 1), lds=0, dyn=0,
-             args=["logits", "router_bias", "x", "topk_ids", "topk_weights", "x_q", "x_scale", "mask",
-                   u(T), u(H), u(cfg.E), u(cfg.K), u(cfg.S), u(W)],
-             reads=["logits", "router_bias", "x", "mask"],
-             writes=["topk_ids", "topk_weights", "x_q", "x_scale", "mask"],
-             refs=["runtime/gfx950/routing/decode/qwen36_shared_gate_append_bridge.hip:76-112"]),
+    ops = [
+        dict(name="moe.router", symbol=f"netra_moe_router_h{H}_gfx950",
+             grid=((cfg.router_rows + 15) // 16, (T + ROUTER_TOKENS - 1) // ROUTER_TOKENS, 1),
+             block=(256, 1, 1), lds=0, dyn=0,
+             args=["x", "router_w", "logits", "x_q", "x_scale", "mask",
+                   u(T), u(H), u(cfg.router_rows), u(cfg.Etot * W)],
+             reads=["x", "router_w"], writes=["logits", "x_q", "x_scale", "mask"],
+             refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150",
+                   "tools/benchmark/export_qwen36_router_bf16_capture.py:78"]),
+        dict(name="moe.topk", symbol="netra_moe_topk_gfx950",
+             grid=((T + 3) // 4, 1, 1), block=(256, 1, 1), lds=19712, dyn=0,
+             args=["logits", "router_bias", "topk_ids", "topk_weights", "mask",
+                   u(T), u(cfg.E), u(cfg.K), u(cfg.S), u(W)],
+             reads=["logits", "router_bias", "mask"], writes=["topk_ids", "topk_weights", "mask"],
+             refs=["runtime/gfx950/routing/decode/qwen36_shared_gate_append_bridge.hip:76-112",
+                   "tools/benchmark/export_qwen36_shared_gate_append_capture.py:97-107,134-139"]),
         dict(name="moe.sort", symbol="netra_moe_sort_gfx950",
              grid=(1, 1, 1), block=(1024, 1, 1), lds=0, dyn=cfg.sort_lds_bytes,
-             args=["topk_ids", "mask", "sorted_ids", "sorted_expert", "num_valid", "expert_counts",
+             args=["topk_ids", "mask", "sorted_ids", "sorted_expert", "tile_map", "num_valid",
+                   "expert_counts",
                    u(T), u(cfg.Ktot), u(cfg.Etot), u(W), u(cfg.cap_blocks)],
              reads=["topk_ids", "mask"],
-             writes=["sorted_ids", "sorted_expert", "num_valid", "expert_counts"],
+             writes=["sorted_ids", "sorted_expert", "tile_map", "num_valid", "expert_counts"],
              refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]),
-        dict(name="moe.gate_up", symbol="netra_moe_gate_up_gfx950",
-             grid=(cfg.cap_blocks, I // 128, 1), block=(256, 1, 1), lds=1536, dyn=0,
-             args=["x_q", "x_scale", "w13", "w13_scale", "sorted_ids", "sorted_expert", "num_valid",
-                   "h_q", "h_scale", u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
-             reads=["x_q", "x_scale", "w13", "w13_scale", "sorted_ids", "sorted_expert", "num_valid"],
-             writes=["h_q", "h_scale"],
-             refs=["kernels/gfx950/templates/moe/decode/gate_up_mfma.inc:12-161",
-                   "kernels/gfx950/templates/moe/decode/silu_quant.inc:16-236"]),
-        dict(name="moe.down", symbol="netra_moe_down_gfx950",
-             grid=(cfg.cap_blocks, H // 256, 1), block=(256, 1, 1), lds=256, dyn=0,
-             args=["h_q", "h_scale", "w2", "w2_scale", "sorted_ids", "sorted_expert", "num_valid",
-                   "partial", u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
-             reads=["h_q", "h_scale", "w2", "w2_scale", "sorted_ids", "sorted_expert", "num_valid"],
-             writes=["partial"],
-             refs=["kernels/gfx950/templates/moe/decode/down_reduce_mfma_2wave.inc:14-291"]),
+    ]
+    common = ["sorted_ids", "sorted_expert", "num_valid"]
+    if path == "stream":
+        ops += [
+            dict(name="moe.gate_up", symbol=f"netra_moe_gate_up_stream_h{H}_gfx950",
+                 grid=(STREAM_GRID_GATE_UP, 1, 1), block=(256, 1, 1), lds=0, dyn=0,
+                 args=["x_q", "x_scale", "w13", "w13_scale", "sorted_ids", "sorted_expert",
+                       "tile_map", "num_valid", "h",
+                       u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
+                 reads=["x_q", "x_scale", "w13", "w13_scale", *common, "tile_map"], writes=["h"],
+                 refs=["kernels/gfx950/templates/moe/decode/gate_up_mfma.inc:12-161"]),
+            dict(name="moe.down", symbol=f"netra_moe_down_stream_i{I}_gfx950",
+                 grid=(STREAM_GRID_DOWN, 1, 1), block=(256, 1, 1), lds=0, dyn=0,
+                 args=["h", "w2", "w2_scale", "sorted_ids", "sorted_expert", "tile_map",
+                       "num_valid", "partial",
+                       u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
+                 reads=["h", "w2", "w2_scale", *common, "tile_map"], writes=["partial"],
+                 refs=["kernels/gfx950/templates/moe/decode/silu_quant.inc:16-236",
+                       "kernels/gfx950/templates/moe/decode/down_reduce_mfma_2wave.inc:14-291"]),
+        ]
+    else:
+        ops += [
+            dict(name="moe.gate_up", symbol="netra_moe_gate_up_tile_gfx950",
+                 grid=(cfg.cap_blocks, I // 128, 1), block=(256, 1, 1), lds=1536, dyn=0,
+                 args=["x_q", "x_scale", "w13", "w13_scale", *common, "h_q", "h_scale",
+                       u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
+                 reads=["x_q", "x_scale", "w13", "w13_scale", *common], writes=["h_q", "h_scale"],
+                 refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/gate_up.inc",
+                       "kernels/gfx950/templates/moe/prefill/fused_splitk2/silu_quant.inc"]),
+            dict(name="moe.down", symbol="netra_moe_down_tile_gfx950",
+                 grid=(cfg.cap_blocks, H // 256, 1), block=(256, 1, 1), lds=256, dyn=0,
+                 args=["h_q", "h_scale", "w2", "w2_scale", *common, "partial",
+                       u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
+                 reads=["h_q", "h_scale", "w2", "w2_scale", *common], writes=["partial"],
+                 refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/down_partial.inc"]),
+        ]
+    ops.append(
         dict(name="moe.combine", symbol="netra_moe_combine_gfx950",
              grid=((H + 1023) // 1024, T, 1), block=(256, 1, 1), lds=0, dyn=0,
              args=["partial", "topk_weights", "out", u(T), u(H), u(cfg.Ktot)],
              reads=["partial", "topk_weights"], writes=["out"],
-             refs=["kernels/gfx950/templates/moe/prefill/route_reduce_splitk2_f16.inc:6-117"]),
-    ]
+             refs=["kernels/gfx950/templates/moe/prefill/route_reduce_splitk2_f16.inc:6-117"]))
+    return ops
 
 
 def _dependencies(ops: list[dict]) -> list[list[int]]:
@@ -141,17 +200,18 @@ def _dependencies(ops: list[dict]) -> list[list[int]]:
 
 
 def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ...] = (),
-                       hsaco: Path | None = None) -> dict:
+                       hsaco: Path | None = None, path: str = "auto") -> dict:
     """Write the engine directory; returns the graph recipe (also on disk)."""
+    path = resolve_path(cfg, path)
     directory = Path(directory)
     hsaco = Path(hsaco) if hsaco else paths.hsaco_path()
     if not hsaco.is_file():
         raise FileNotFoundError(f"code object {hsaco} is missing; run the build first")
-    tensors = tensor_table(cfg)
+    tensors = tensor_table(cfg, path)
     unknown = set(expose) - set(tensors)
     if unknown:
         raise ValueError(f"cannot expose unknown tensors {sorted(unknown)}")
-    ops = operations(cfg)
+    ops = operations(cfg, path)
     code = hsaco.read_bytes()
     sha = hashlib.sha256(code).hexdigest()
 
@@ -205,6 +265,7 @@ def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ..
         "required_rocm": {"minimum": "7.0", "code_object_version": 6},
         "name": f"netra-moe-{cfg.name}",
         "configuration": cfg.to_dict(),
+        "gemm_path": path,
         "workspace_bytes": workspace_bytes,
         "profiles": [{"name": profile.name, "guards": profile.to_dict()["guards"],
                       "tensor_parallel": profile.tensor_parallel}],
@@ -212,6 +273,8 @@ def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ..
     }
     recipe = {
         "format": "netra-graph-recipe-1",
+        "gemm_path": path,
+        "operations": [op["name"] for op in ops],
         "tensors": {n: {"dtype": s.dtype, "shape": list(s.shape), "role": s.role,
                         "bytes": s.nbytes, "storage": "workspace" if n in offsets else "binding"}
                     for n, s in tensors.items()},

@@ -6,7 +6,6 @@ native library or a GPU (no CPU fallback exists in the product path).
 """
 from __future__ import annotations
 
-import ctypes
 import hashlib
 import json
 import os
@@ -16,18 +15,17 @@ from pathlib import Path
 import torch
 
 from .config import MoEConfig
-from .engine import compile_moe_engine, tensor_table
+from .engine import OP_NAMES, compile_moe_engine, resolve_path, tensor_table
 from .runtime import Engine, LaunchShape
 
 TORCH_DTYPES = {"bf16": torch.bfloat16, "f32": torch.float32, "e4m3": torch.uint8,
                 "i32": torch.int32, "u64": torch.int64}
 WEIGHT_NAMES = ("router_w", "router_bias", "w13", "w13_scale", "w2", "w2_scale")
-OP_NAMES = ("router_logits", "topk_quant", "sort", "gate_up", "down", "combine")
 
 
-def _engine_cache_dir(cfg: MoEConfig, expose: tuple[str, ...]) -> Path:
+def _engine_cache_dir(cfg: MoEConfig, expose: tuple[str, ...], path: str) -> Path:
     root = Path(os.environ.get("NETRA_MOE_ENGINE_CACHE", Path(tempfile.gettempdir()) / "netra_moe_engines"))
-    key = hashlib.sha256(json.dumps([cfg.to_dict(), sorted(expose)], sort_keys=True).encode()).hexdigest()[:16]
+    key = hashlib.sha256(json.dumps([cfg.to_dict(), sorted(expose), path], sort_keys=True).encode()).hexdigest()[:16]
     return root / f"{cfg.name}-{key}"
 
 
@@ -40,15 +38,17 @@ def check_tensor(name: str, t: torch.Tensor, dtype: str, shape: tuple[int, ...],
 
 class MoELayer:
     def __init__(self, cfg: MoEConfig, weights: dict[str, torch.Tensor], *, device: int = 0,
-                 expose: tuple[str, ...] = (), graph: bool = True, engine_dir: Path | None = None):
+                 expose: tuple[str, ...] = (), graph: bool = True, engine_dir: Path | None = None,
+                 path: str = "auto"):
         if not torch.cuda.is_available():
             raise RuntimeError("MoELayer needs a ROCm GPU; there is no CPU fallback")
         self.cfg = cfg
         self.device = torch.device("cuda", device)
         self.expose = tuple(expose)
-        self.engine_dir = Path(engine_dir) if engine_dir else _engine_cache_dir(cfg, self.expose)
-        self.recipe = compile_moe_engine(cfg, self.engine_dir, expose=self.expose)
-        self.specs = tensor_table(cfg)
+        self.path = resolve_path(cfg, path)
+        self.engine_dir = Path(engine_dir) if engine_dir else _engine_cache_dir(cfg, self.expose, self.path)
+        self.recipe = compile_moe_engine(cfg, self.engine_dir, expose=self.expose, path=self.path)
+        self.specs = tensor_table(cfg, self.path)
         with torch.cuda.device(self.device):
             self.engine = Engine(self.engine_dir, device_id=device, graph_capture=graph)
         self.graph = graph

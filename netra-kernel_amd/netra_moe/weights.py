@@ -31,6 +31,10 @@ def bridge_library() -> ctypes.CDLL:
         lib = ctypes.CDLL(str(path))
         lib.netra_moe_quant_blocks.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_uint32] * 3 + [ctypes.c_void_p]
         lib.netra_moe_quant_blocks.restype = ctypes.c_int
+        lib.netra_moe_pack_tiles.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_uint32] * 3 + [ctypes.c_void_p]
+        lib.netra_moe_pack_tiles.restype = ctypes.c_int
+        lib.netra_moe_e4m3_check.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_uint32, ctypes.c_void_p]
+        lib.netra_moe_e4m3_check.restype = ctypes.c_int
         lib.netra_moe_last_error.argtypes = []
         lib.netra_moe_last_error.restype = ctypes.c_char_p
         _bridge = lib
@@ -52,6 +56,30 @@ def quantize_blocks(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     if rc != 0:
         raise RuntimeError(f"netra_moe_quant_blocks failed ({rc}): {lib.netra_moe_last_error().decode()}")
     return q, s
+
+
+def pack_tiles(q: torch.Tensor) -> torch.Tensor:
+    """Row-major e4m3 bytes [G, N, K] on the GPU -> the kernels' tile16x128 layout."""
+    if q.dim() != 3 or q.dtype != torch.uint8 or not q.is_cuda or not q.is_contiguous():
+        raise ValueError("pack_tiles needs a contiguous uint8 [G, N, K] GPU tensor")
+    g, n, k = q.shape
+    if n % 16 or k % 128:
+        raise ValueError("N must be a multiple of 16 and K of 128")
+    out = torch.empty_like(q)
+    lib = bridge_library()
+    rc = lib.netra_moe_pack_tiles(q.data_ptr(), out.data_ptr(), g, n, k,
+                                  torch.cuda.current_stream(q.device).cuda_stream)
+    if rc != 0:
+        raise RuntimeError(f"netra_moe_pack_tiles failed ({rc}): {lib.netra_moe_last_error().decode()}")
+    return out
+
+
+def pack_tiles_host(q: np.ndarray) -> np.ndarray:
+    """Host restatement of the tile16x128 layout: [G, N, K] -> [G, N/16, K/128, 64 lanes, 32]
+    with lane = (k % 128) // 32 * 16 + n % 16 (returned with the original shape)."""
+    g, n, k = q.shape
+    t = q.reshape(g, n // 16, 16, k // 128, 4, 32).transpose(0, 1, 3, 4, 2, 5)
+    return np.ascontiguousarray(t).reshape(g, n, k)
 
 
 def zipf_bias(E: int, seed: int, s: float = 1.1) -> np.ndarray:
@@ -88,14 +116,25 @@ def synthetic_expert_weights_f32(cfg: MoEConfig, seed: int, device: torch.device
     return w13, w2
 
 
-def synthetic_expert_weights(cfg: MoEConfig, seed: int, device: torch.device | str) -> dict[str, torch.Tensor]:
-    """Quantised expert weights generated and prepared on the GPU."""
-    w13, w2 = synthetic_expert_weights_f32(cfg, seed, device)
+def prepare_expert_weights(w13: torch.Tensor, w2: torch.Tensor, keep_row_major: bool = False):
+    """fp32 W13 [Etot, 2I, H], W2 [Etot, H, I] on the GPU -> the layer's weight
+    tensors (e4m3 in the tile16x128 layout + fp32 128x128 block scales). With
+    keep_row_major the row-major e4m3 bytes are returned as well."""
     q13, s13 = quantize_blocks(w13)
-    del w13
     q2, s2 = quantize_blocks(w2)
-    del w2
-    return {"w13": q13, "w13_scale": s13, "w2": q2, "w2_scale": s2}
+    out = {"w13": pack_tiles(q13), "w13_scale": s13, "w2": pack_tiles(q2), "w2_scale": s2}
+    if keep_row_major:
+        out["w13_row_major"], out["w2_row_major"] = q13, q2
+    return out
+
+
+def synthetic_expert_weights(cfg: MoEConfig, seed: int, device: torch.device | str,
+                             keep_row_major: bool = False) -> dict[str, torch.Tensor]:
+    """Quantised, packed expert weights generated and prepared on the GPU."""
+    w13, w2 = synthetic_expert_weights_f32(cfg, seed, device)
+    out = prepare_expert_weights(w13, w2, keep_row_major)
+    del w13, w2
+    return out
 
 
 def expert_bytes_touched(cfg: MoEConfig, topk_ids: np.ndarray) -> tuple[int, int]:

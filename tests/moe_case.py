@@ -12,8 +12,13 @@ from netra_moe.engine import tensor_table
 from netra_moe.layer import MoELayer
 from netra_moe import weights as W
 
-ALL_INTERMEDIATES = ("logits", "mask", "topk_ids", "topk_weights", "x_q", "x_scale", "sorted_ids",
-                     "sorted_expert", "num_valid", "expert_counts", "h_q", "h_scale", "partial")
+ROUTING = ("logits", "mask", "topk_ids", "topk_weights", "x_q", "x_scale", "sorted_ids",
+           "sorted_expert", "tile_map", "num_valid", "expert_counts", "partial")
+PATH_INTERMEDIATES = {"stream": ("h",), "tile": ("h_q", "h_scale")}
+
+
+def intermediates(path: str) -> tuple[str, ...]:
+    return ROUTING + PATH_INTERMEDIATES[path]
 WEIGHT_SEED = 77
 
 
@@ -28,28 +33,35 @@ def make_inputs(cfg: MoEConfig, device: torch.device, weights_on_gpu: bool | Non
     if weights_on_gpu is None:
         weights_on_gpu = cfg.Etot * cfg.I * cfg.H > (1 << 24)
     if weights_on_gpu:
-        wq = W.synthetic_expert_weights(cfg, WEIGHT_SEED, device)
+        wq = W.synthetic_expert_weights(cfg, WEIGHT_SEED, device, keep_row_major=True)
         torch.cuda.synchronize(device)
+        rm13 = wq.pop("w13_row_major").cpu().numpy()
+        rm2 = wq.pop("w2_row_major").cpu().numpy()
+        s13, s2 = wq["w13_scale"].cpu().numpy(), wq["w2_scale"].cpu().numpy()
     else:
         w13, w2 = W.synthetic_expert_weights_f32(cfg, WEIGHT_SEED, "cpu")
-        q13, s13 = oracle.quant_blocks_f32(w13.numpy())
-        q2, s2 = oracle.quant_blocks_f32(w2.numpy())
-        wq = {"w13": torch.from_numpy(q13).to(device), "w13_scale": torch.from_numpy(s13).to(device),
-              "w2": torch.from_numpy(q2).to(device), "w2_scale": torch.from_numpy(s2).to(device)}
+        rm13, s13 = oracle.quant_blocks_f32(w13.numpy())
+        rm2, s2 = oracle.quant_blocks_f32(w2.numpy())
+        wq = {"w13": torch.from_numpy(W.pack_tiles_host(rm13)).to(device),
+              "w13_scale": torch.from_numpy(s13).to(device),
+              "w2": torch.from_numpy(W.pack_tiles_host(rm2)).to(device),
+              "w2_scale": torch.from_numpy(s2).to(device)}
     gpu = {"router_w": act["router_w"].to(device), "router_bias": act["router_bias"].to(device), **wq}
     host = {
         "x": bf16_bits(act["x"]),
         "router_w": bf16_bits(act["router_w"]),
         "router_bias": act["router_bias"].numpy(),
-        "w13": wq["w13"].cpu().numpy(), "w13_scale": wq["w13_scale"].cpu().numpy(),
-        "w2": wq["w2"].cpu().numpy(), "w2_scale": wq["w2_scale"].cpu().numpy(),
+        "w13": rm13, "w13_scale": s13, "w2": rm2, "w2_scale": s2,
     }
     return act["x"].to(device), gpu, host
 
 
 def run_gpu(cfg: MoEConfig, x: torch.Tensor, gpu_weights: dict, device: torch.device,
-            expose=ALL_INTERMEDIATES, graph: bool = False, repeats: int = 1):
-    layer = MoELayer(cfg, gpu_weights, device=device.index or 0, expose=expose, graph=graph)
+            expose=None, graph: bool = False, repeats: int = 1, path: str = "auto"):
+    layer = MoELayer(cfg, gpu_weights, device=device.index or 0, expose=expose or intermediates(
+        __import__("netra_moe.engine", fromlist=["resolve_path"]).resolve_path(cfg, path)),
+        graph=graph, path=path)
+    expose = layer.expose
     outs = []
     for _ in range(repeats):
         layer.forward(x)
@@ -70,9 +82,10 @@ def oracle_routing(cfg: MoEConfig, host: dict) -> dict:
     logits = oracle.router_logits(host["x"], host["router_w"])
     ids, wts = oracle.topk(logits, host["router_bias"], cfg.E, cfg.K, cfg.S)
     x_q, x_s = oracle.quant_rows_bf16(host["x"])
-    sid, sexp, nv, counts = oracle.sort(ids, cfg.Etot, cfg.cap_blocks)
+    sid, sexp, nv, counts, tmap = oracle.sort(ids, cfg.Etot, cfg.cap_blocks, with_tiles=True)
     return dict(logits=logits, topk_ids=ids, topk_weights=wts, x_q=x_q, x_scale=x_s,
-                sorted_ids=sid, sorted_expert=sexp, num_valid=nv, expert_counts=counts)
+                sorted_ids=sid, sorted_expert=sexp, num_valid=nv, expert_counts=counts,
+                tile_map=tmap)
 
 
 def sample_tokens(cfg: MoEConfig, n: int) -> np.ndarray:

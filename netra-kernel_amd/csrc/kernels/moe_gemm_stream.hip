@@ -7,7 +7,8 @@
 // metadata of the next item and the activations and weights of the next step
 // are issued before the current step's MFMAs wait, in the order they will be
 // consumed, so the in-order load counter never drains the prefetched data.
-// Waves never synchronise with each other.
+// Waves never synchronise with each other; per-item values that every lane
+// needs (activation scales) go through the wave's own LDS slot.
 //
 // gate/up writes h = bf16(silu(g) * u) in sorted-row order; down requantises h
 // per 1x128 group as it consumes it (the SiLU-quant step of the reference's
@@ -24,7 +25,7 @@
 #define NK_GATE_UP_WAVES_PER_EU 2
 #endif
 #ifndef NK_DOWN_WAVES_PER_EU
-#define NK_DOWN_WAVES_PER_EU 3
+#define NK_DOWN_WAVES_PER_EU 4
 #endif
 
 namespace nkstream {
@@ -33,20 +34,25 @@ struct Range {
   uint32_t beg, end;
 };
 
-// Contiguous run of items owned by the calling wave.
+__device__ __forceinline__ uint32_t wave_id() {
+  return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
+
+// Contiguous run of items owned by the calling wave (uniform values).
 __device__ __forceinline__ Range wave_range(uint32_t items) {
   const uint32_t waves = gridDim.x * (blockDim.x >> 6);
-  const uint32_t gw = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const uint32_t gw = blockIdx.x * (blockDim.x >> 6) + wave_id();
   const uint32_t per = (items + waves - 1u) / waves;
   const uint32_t beg = gw * per;
   const uint32_t end = beg + per < items ? beg + per : items;
   return {beg, beg < items ? end : beg};
 }
 
-// Routing metadata of one 16-row tile. Lane l holds row (l & 15) of the tile:
-// its token (gate/up) or route t * Ktot + slot (down), -1 for padding rows.
+// Routing metadata of one 16-row tile. row0 and expert are uniform; lane l
+// holds row (l & 15): its token (gate/up) or route t * Ktot + slot (down),
+// -1 for padding rows.
 struct TileRows {
-  uint32_t row0 = 0;   // first sorted row of the tile (block * 64 + 16 * tile)
+  uint32_t row0 = 0;
   int32_t expert = 0;
   int32_t row = -1;
 };
@@ -79,7 +85,7 @@ constexpr uint32_t kGuChunk = 2;
 
 struct GateUpStep {
   nk::v8i g[kGuChunk], u[kGuChunk], a[kGuChunk];
-  float sg[kGuChunk], su[kGuChunk], as[kGuChunk][4];
+  float sg[kGuChunk], su[kGuChunk];
 };
 
 template <uint32_t KB>
@@ -92,16 +98,31 @@ __device__ __forceinline__ void gate_up_stream(
   using namespace nkstream;
   constexpr uint32_t H = 128 * KB;
   constexpr uint32_t NCH = KB / kGuChunk;
+  constexpr uint32_t SPL = (KB + 3) / 4;  // activation scales per lane per item
   static_assert(KB % (2 * kGuChunk) == 0, "H must be a multiple of 512");
+  // Activation scales of the current and next item: [wave][slot][row * KB + kb].
+  __shared__ float s_xs[4][2][16 * KB];
   const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = wave_id();
   const uint32_t kofs = (lane >> 4) * 32u;
   const uint32_t cols = I / 16u;
   const Range r = wave_range((uint32_t)num_valid[2] * cols);
   const uint32_t steps = (r.end - r.beg) * NCH;
   if (steps == 0) return;
 
-  auto fetch_meta = [&](TileRows& m, uint32_t s) {
-    load_tile(m, tile_map, sorted_ids, sorted_expert, (r.beg + s / NCH) / cols, T, Ktot, Etot, false);
+  // Lane l fetches row l & 15's scales for K blocks [(l >> 4) * SPL, +SPL).
+  auto fetch_meta = [&](TileRows& m, float (&xsv)[SPL], uint32_t item) {
+    load_tile(m, tile_map, sorted_ids, sorted_expert, item / cols, T, Ktot, Etot, false);
+    const int32_t t = m.row < 0 ? 0 : m.row;
+    const uint32_t k0 = (lane >> 4) * SPL;
+#pragma unroll
+    for (uint32_t i = 0; i < SPL; ++i) xsv[i] = (k0 + i < KB) ? xs[(size_t)t * KB + k0 + i] : 0.0f;
+  };
+  auto store_scales = [&](const float (&xsv)[SPL], uint32_t slot) {
+    const uint32_t k0 = (lane >> 4) * SPL;
+#pragma unroll
+    for (uint32_t i = 0; i < SPL; ++i)
+      if (k0 + i < KB) s_xs[wave][slot][(lane & 15u) * KB + k0 + i] = xsv[i];
   };
   auto issue = [&](GateUpStep& st, const TileRows& m, uint32_t s) {
     const uint32_t item = r.beg + s / NCH, ch = s % NCH;
@@ -110,72 +131,77 @@ __device__ __forceinline__ void gate_up_stream(
     const uint8_t* arow = xq + (size_t)(ta < 0 ? 0 : ta) * H + kofs;
 #pragma unroll
     for (uint32_t i = 0; i < kGuChunk; ++i) st.a[i] = nk::load_fp8x32(arow + (ch * kGuChunk + i) * 128u);
-#pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) {
-      const int32_t tk = __shfl(m.row, (lane >> 4) * 4u + j);
-      const float* srow = xs + (size_t)(tk < 0 ? 0 : tk) * KB + ch * kGuChunk;
-#pragma unroll
-      for (uint32_t i = 0; i < kGuChunk; ++i) st.as[i][j] = srow[i];
-    }
-    const uint32_t ng = c * 16u + (lane & 15u), nu = I + ng;
     const uint8_t* we = w13 + (size_t)m.expert * 2u * I * H;
     const float* wse = w13s + (size_t)m.expert * (2u * I / 128u) * KB;
 #pragma unroll
     for (uint32_t i = 0; i < kGuChunk; ++i) {
       const uint32_t kb = ch * kGuChunk + i;
-      st.g[i] = nk::load_fp8x32(nk::tile_operand(we, c, kb, KB, lane));
-      st.u[i] = nk::load_fp8x32(nk::tile_operand(we, I / 16u + c, kb, KB, lane));
-      st.sg[i] = wse[(ng >> 7) * KB + kb];
-      st.su[i] = wse[(nu >> 7) * KB + kb];
+      st.g[i] = nk::load_tile_operand(nk::tile_base(we, c, kb, KB), lane);
+      st.u[i] = nk::load_tile_operand(nk::tile_base(we, I / 16u + c, kb, KB), lane);
+      st.sg[i] = wse[(c >> 3) * KB + kb];                 // 128-row scale block of rows 16c..
+      st.su[i] = wse[((I / 16u + c) >> 3) * KB + kb];
     }
   };
   nk::v4f ag = {0.0f, 0.0f, 0.0f, 0.0f}, au = {0.0f, 0.0f, 0.0f, 0.0f};
-  auto compute = [&](const GateUpStep& st, const TileRows& m, uint32_t s) {
+  auto compute = [&](const GateUpStep& st, const TileRows& m, uint32_t slot, uint32_t s) {
+    const uint32_t ch = s % NCH;
 #pragma unroll
     for (uint32_t i = 0; i < kGuChunk; ++i) {
+      const uint32_t kb = ch * kGuChunk + i;
       const nk::v4f dg = nk::mfma_e4m3_16x16x128(st.a[i], st.g[i]);
       const nk::v4f du = nk::mfma_e4m3_16x16x128(st.a[i], st.u[i]);
 #pragma unroll
       for (uint32_t j = 0; j < 4; ++j) {
-        ag[j] = ag[j] + st.sg[i] * (st.as[i][j] * dg[j]);
-        au[j] = au[j] + st.su[i] * (st.as[i][j] * du[j]);
+        const float as = s_xs[wave][slot][((lane >> 4) * 4u + j) * KB + kb];
+        ag[j] = ag[j] + st.sg[i] * (as * dg[j]);
+        au[j] = au[j] + st.su[i] * (as * du[j]);
       }
     }
-    if (s % NCH == NCH - 1u) {
+    if (ch == NCH - 1u) {
       const uint32_t c = (r.beg + s / NCH) % cols;
 #pragma unroll
       for (uint32_t j = 0; j < 4; ++j) {
         const uint32_t row = (lane >> 4) * 4u + j;
         if (__shfl(m.row, row) >= 0)
-          h[(size_t)(m.row0 + row) * I + c * 16u + (lane & 15u)] = nk::bf16_rne(nk::silu(ag[j]) * au[j]);
+          h[nk::h_tile_index(m.row0 + row, c * 16u + (lane & 15u), I / 128u)] =
+              nk::bf16_rne(nk::silu(ag[j]) * au[j]);
       }
       ag = nk::v4f{0.0f, 0.0f, 0.0f, 0.0f};
       au = nk::v4f{0.0f, 0.0f, 0.0f, 0.0f};
     }
   };
 
-  // Item k: its metadata was fetched at the start of item k - 1 and its first
-  // step issued during the last step of item k - 1; inside the item, step
-  // ch + 1 is issued before step ch computes.
+  // Item k (slot k & 1): its metadata and scales were fetched at the start of
+  // item k - 1, its scales stored and its first step issued during the last
+  // step of item k - 1; inside the item step ch + 1 is issued before step ch
+  // computes.
   GateUpStep sx, sy;
   TileRows ma, mb;
-  auto item_body = [&](uint32_t k, const TileRows& cur, TileRows& nxt) {
-    if (k + 1u < r.end) fetch_meta(nxt, (k + 1u - r.beg) * NCH);
+  float xa[SPL], xb[SPL];
+  auto item_body = [&](uint32_t k, const TileRows& cur, uint32_t slot, TileRows& nxt,
+                       float (&xnxt)[SPL]) {
+    const bool more = k + 1u < r.end;
+    if (more) fetch_meta(nxt, xnxt, k + 1u);
 #pragma unroll 1
     for (uint32_t ch = 0; ch < NCH; ch += 2u) {
       const uint32_t s = (k - r.beg) * NCH + ch;
       issue(sy, cur, s + 1u);
-      compute(sx, cur, s);
-      if (ch + 2u < NCH) issue(sx, cur, s + 2u);
-      else if (k + 1u < r.end) issue(sx, nxt, s + 2u);
-      compute(sy, cur, s + 1u);
+      compute(sx, cur, slot, s);
+      if (ch + 2u < NCH) {
+        issue(sx, cur, s + 2u);
+      } else if (more) {
+        store_scales(xnxt, slot ^ 1u);
+        issue(sx, nxt, s + 2u);
+      }
+      compute(sy, cur, slot, s + 1u);
     }
   };
-  fetch_meta(ma, 0);
+  fetch_meta(ma, xa, r.beg);
+  store_scales(xa, 0u);
   issue(sx, ma, 0);
   for (uint32_t k = r.beg; k < r.end; k += 2u) {
-    item_body(k, ma, mb);
-    if (k + 1u < r.end) item_body(k + 1u, mb, ma);
+    item_body(k, ma, 0u, mb, xb);
+    if (k + 1u < r.end) item_body(k + 1u, mb, 1u, ma, xa);
   }
 }
 
@@ -232,22 +258,22 @@ __device__ __forceinline__ void down_stream(
   const uint32_t steps = (r.end - r.beg) * NCH;
   if (steps == 0) return;
 
-  auto fetch_meta = [&](TileRows& m, uint32_t s) {
-    load_tile(m, tile_map, sorted_ids, sorted_expert, (r.beg + s / NCH) / cols, T, Ktot, Etot, true);
+  auto fetch_meta = [&](TileRows& m, uint32_t item) {
+    load_tile(m, tile_map, sorted_ids, sorted_expert, item / cols, T, Ktot, Etot, true);
   };
   auto issue = [&](DownStep& st, const TileRows& m, uint32_t s) {
     const uint32_t item = r.beg + s / NCH, kb = s % NCH;
     const uint32_t c = item % cols;
-    const uint4* src = reinterpret_cast<const uint4*>(h + (size_t)(m.row0 + (lane & 15u)) * I + kb * 128u + kofs);
+    // h tile layout: four 1 KiB pieces per (tile, K block), lane l at l * 16.
+    const uint4* src = reinterpret_cast<const uint4*>(h + ((size_t)(m.row0 >> 4) * KB + kb) * 2048u) + lane;
 #pragma unroll
-    for (uint32_t q = 0; q < 4; ++q) st.hraw[q] = src[q];
+    for (uint32_t q = 0; q < 4; ++q) st.hraw[q] = src[q * 64u];
     const uint8_t* we = w2 + (size_t)m.expert * H * I;
     const float* wse = w2s + (size_t)m.expert * (H / 128u) * KB;
 #pragma unroll
     for (uint32_t t2 = 0; t2 < 2; ++t2) {
-      const uint32_t n = c * 32u + t2 * 16u + (lane & 15u);
-      st.w[t2] = nk::load_fp8x32(nk::tile_operand(we, c * 2u + t2, kb, KB, lane));
-      st.s[t2] = wse[(n >> 7) * KB + kb];
+      st.w[t2] = nk::load_tile_operand(nk::tile_base(we, c * 2u + t2, kb, KB), lane);
+      st.s[t2] = wse[((c * 2u + t2) >> 3) * KB + kb];   // 128-row scale block of the tile
     }
   };
   nk::v4f acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -300,7 +326,7 @@ __device__ __forceinline__ void down_stream(
   DownStep sx, sy;
   TileRows ma, mb;
   auto item_body = [&](uint32_t k, const TileRows& cur, TileRows& nxt) {
-    if (k + 1u < r.end) fetch_meta(nxt, (k + 1u - r.beg) * NCH);
+    if (k + 1u < r.end) fetch_meta(nxt, k + 1u);
 #pragma unroll 1
     for (uint32_t ch = 0; ch < NCH; ch += 2u) {
       const uint32_t s = (k - r.beg) * NCH + ch;
@@ -311,7 +337,7 @@ __device__ __forceinline__ void down_stream(
       compute(sy, cur, s + 1u);
     }
   };
-  fetch_meta(ma, 0);
+  fetch_meta(ma, r.beg);
   issue(sx, ma, 0);
   for (uint32_t k = r.beg; k < r.end; k += 2u) {
     item_body(k, ma, mb);

@@ -77,7 +77,7 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_gate_up_tile_gfx950(
     float wsc[4];
 #pragma unroll
     for (uint32_t c = 0; c < 4; ++c) {
-      bf[c] = nk::load_fp8x32(nk::tile_operand(we, nrow[c] >> 4, kb, KB, lane));
+      bf[c] = nk::load_tile_operand(nk::tile_base(we, nrow[c] >> 4, kb, KB), lane);
       wsc[c] = wse[(nrow[c] >> 7) * KB + kb];
     }
 #pragma unroll
@@ -190,7 +190,7 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_down_tile_gfx950(
 #pragma unroll
     for (uint32_t c = 0; c < 4; ++c) {
       const uint32_t n = ncol0 + 16u * c;
-      bf[c] = nk::load_fp8x32(nk::tile_operand(we, n >> 4, kb, KB, lane));
+      bf[c] = nk::load_tile_operand(nk::tile_base(we, n >> 4, kb, KB), lane);
       wsc[c] = wse[(n >> 7) * KB + kb];
     }
 #pragma unroll

@@ -91,8 +91,9 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_e4m3_check_gfx950(
 
 // ---------------------------------------------------------------------------
 // Weight layout change: row-major e4m3 [groups, n, k] -> tile16x128 (see
-// nk::tile_operand). One wave per 16 x 128 tile; lane l moves row l & 15,
-// columns (l >> 4) * 32 .. +31 to tile offset l * 32.
+// nk::tile_base). One wave per 16 x 128 tile; lane l moves row l & 15,
+// columns (l >> 4) * 32 .. +15 to tile offset l * 16 and columns +16 .. +31
+// to 1024 + l * 16.
 NK_KERNEL __launch_bounds__(256) void netra_moe_pack_tiles_gfx950(
     const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t groups, uint32_t n,
     uint32_t k) {
@@ -104,7 +105,7 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_pack_tiles_gfx950(
   const uint8_t* s = src + ((size_t)g * n + rt * 16u + (lane & 15u)) * k + cb * 128u + (lane >> 4) * 32u;
   const uint4 lo = *reinterpret_cast<const uint4*>(s);
   const uint4 hi = *reinterpret_cast<const uint4*>(s + 16);
-  uint8_t* d = dst + (size_t)tile * 2048u + lane * 32u;
+  uint8_t* d = dst + (size_t)tile * 2048u + lane * 16u;
   *reinterpret_cast<uint4*>(d) = lo;
-  *reinterpret_cast<uint4*>(d + 16) = hi;
+  *reinterpret_cast<uint4*>(d + 1024) = hi;
 }

@@ -100,13 +100,33 @@ __device__ __forceinline__ v8i load_fp8x32(const uint8_t* p) {
 }
 
 // Packed expert-weight layout ("tile16x128"): a [N, K] e4m3 matrix is stored
-// as N/16 x K/128 tiles, row tiles outermost; inside a tile the 64 lanes' MFMA
-// operands lie back to back, lane l holding row l & 15, columns
-// (l >> 4) * 32 .. +31. One wave load of 32 bytes per lane therefore reads a
-// contiguous 2 KiB, and a 16-row tile's full K extent is contiguous.
-__device__ __forceinline__ const uint8_t* tile_operand(const uint8_t* matrix, uint32_t row_tile,
-                                                       uint32_t kb, uint32_t kblocks, uint32_t lane) {
-  return matrix + ((size_t)row_tile * kblocks + kb) * 2048u + lane * 32u;
+// as N/16 x K/128 tiles of 2 KiB, row tiles outermost, so a 16-row tile's full
+// K extent is contiguous. Lane l's MFMA operand (row l & 15, columns
+// (l >> 4) * 32 .. +31) is split in two 16-byte halves stored at l * 16 and
+// 1024 + l * 16: each of the wave's two 16-byte loads reads 1 KiB contiguous.
+__device__ __forceinline__ const uint8_t* tile_base(const uint8_t* matrix, uint32_t row_tile,
+                                                    uint32_t kb, uint32_t kblocks) {
+  return matrix + ((size_t)row_tile * kblocks + kb) * 2048u;
+}
+
+__device__ __forceinline__ v8i load_tile_operand(const uint8_t* tile, uint32_t lane) {
+  const uint4 lo = *reinterpret_cast<const uint4*>(tile + lane * 16u);
+  const uint4 hi = *reinterpret_cast<const uint4*>(tile + 1024u + lane * 16u);
+  v8i r;
+  r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
+  r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
+  return r;
+}
+
+// Tiled activation layout for h (bf16, [rows, I]) between the decode GEMMs:
+// per 16-row tile and 128-column block, lane l's 32 values (row l & 15,
+// columns (l >> 4) * 32 .. +31) form four 16-byte pieces; piece q of every
+// lane lies at ((tile * kblocks + kb) * 4 + q) * 1024 + l * 16 bytes, so the
+// consumer's four loads each read 1 KiB contiguous.
+__device__ __forceinline__ size_t h_tile_index(uint32_t row, uint32_t col, uint32_t kblocks) {
+  const uint32_t kb = col >> 7, cc = col & 127u, e = cc & 31u;
+  const uint32_t lane = (cc >> 5) * 16u + (row & 15u);
+  return ((((size_t)(row >> 4) * kblocks + kb) * 4u + (e >> 3)) * 64u + lane) * 8u + (e & 7u);
 }
 
 // D = A(16x128 e4m3) * B(128x16 e4m3), fp32 accumulate. Lane l supplies row

@@ -53,9 +53,9 @@ GEMM_PATHS = ("stream", "tile")
 STREAM_H = (512, 1024, 2048, 4096)   # netra_moe_gate_up_stream_h<H>_gfx950
 STREAM_I = (256, 512, 1024, 2048)    # netra_moe_down_stream_i<I>_gfx950
 # Persistent stream kernels: 256 CUs x 4 SIMDs x resident waves per SIMD
-# (NK_GATE_UP_WAVES_PER_EU = 2, NK_DOWN_WAVES_PER_EU = 3) / 4 waves per group.
+# (NK_GATE_UP_WAVES_PER_EU = 2, NK_DOWN_WAVES_PER_EU = 4) / 4 waves per group.
 STREAM_GRID_GATE_UP = 512
-STREAM_GRID_DOWN = 768
+STREAM_GRID_DOWN = 1024
 
 
 def resolve_path(cfg: MoEConfig, path: str = "auto") -> str:

@@ -75,11 +75,21 @@ def pack_tiles(q: torch.Tensor) -> torch.Tensor:
 
 
 def pack_tiles_host(q: np.ndarray) -> np.ndarray:
-    """Host restatement of the tile16x128 layout: [G, N, K] -> [G, N/16, K/128, 64 lanes, 32]
-    with lane = (k % 128) // 32 * 16 + n % 16 (returned with the original shape)."""
+    """Host restatement of the tile16x128 layout: [G, N, K] ->
+    [G, N/16, K/128, half, lane, 16 bytes] with lane = (k % 128) // 32 * 16 + n % 16
+    and half = (k % 32) // 16 (returned with the original shape)."""
     g, n, k = q.shape
-    t = q.reshape(g, n // 16, 16, k // 128, 4, 32).transpose(0, 1, 3, 4, 2, 5)
+    t = q.reshape(g, n // 16, 16, k // 128, 4, 2, 16).transpose(0, 1, 3, 5, 4, 2, 6)
     return np.ascontiguousarray(t).reshape(g, n, k)
+
+
+def unpack_h_tiles_host(h: np.ndarray, cols: int) -> np.ndarray:
+    """Inverse of the decode GEMMs' tiled h layout: flat bf16 bits -> [rows, cols].
+    Stored order is [row tile, K block, piece q, lane group g, row r, 8 values]
+    for row = tile * 16 + r and column = block * 128 + g * 32 + q * 8 + value."""
+    rows = h.size // cols
+    t = h.reshape(rows // 16, cols // 128, 4, 4, 16, 8).transpose(0, 4, 1, 3, 2, 5)
+    return np.ascontiguousarray(t).reshape(rows, cols)
 
 
 def zipf_bias(E: int, seed: int, s: float = 1.1) -> np.ndarray:

@@ -14,6 +14,7 @@ import torch
 import oracle
 from conftest import gpu_available
 from moe_case import make_inputs, oracle_routing, run_gpu, sample_tokens
+from netra_moe import weights as W
 from netra_moe.config import BASELINE_CONFIGS
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a GPU")]
@@ -114,7 +115,8 @@ def test_gate_up_h_bf16_rows(case):
     t = ref["sorted_ids"][:rows] & 0xFFFFFF
     valid = t < cfg.T
     h_ref = oracle.f32_from_bf16(h_b[:rows][valid]).astype(np.float64)
-    h_got = oracle.f32_from_bf16(got["h"][:rows][valid]).astype(np.float64)
+    h_rows = W.unpack_h_tiles_host(got["h"].reshape(-1), cfg.I)
+    h_got = oracle.f32_from_bf16(h_rows[:rows][valid]).astype(np.float64)
     row_max = np.max(np.abs(h_ref), axis=1, keepdims=True)
     excess = float(np.max(np.abs(h_got - h_ref) - 2.0 ** -7 * np.abs(h_ref) - 2.0 ** -12 * row_max))
     frac = float(np.mean(h_got != h_ref))

@@ -1,0 +1,40 @@
+"""Host restatements of the kernels' data layouts (CPU).
+
+The packed weight layout and the tiled h layout are pure permutations; these
+tests pin the host restatements against element-by-element definitions
+(independent index arithmetic) so the GPU tests that rely on them compare like
+with like.
+"""
+import numpy as np
+
+from netra_moe import weights as W
+
+
+def test_pack_tiles_host_is_the_documented_permutation():
+    rng = np.random.default_rng(0)
+    G, N, K = 2, 32, 256
+    q = rng.integers(0, 256, size=(G, N, K), dtype=np.uint8)
+    p = W.pack_tiles_host(q).reshape(-1)
+    for g in range(G):
+        for n in range(0, N, 5):
+            for k in range(0, K, 7):
+                tile = (g * (N // 16) + n // 16) * (K // 128) + k // 128
+                lane = ((k % 128) // 32) * 16 + n % 16
+                half = (k % 32) // 16
+                off = tile * 2048 + half * 1024 + lane * 16 + k % 16
+                assert p[off] == q[g, n, k]
+    assert sorted(p.tolist()) == sorted(q.reshape(-1).tolist())
+
+
+def test_unpack_h_tiles_inverts_the_device_index():
+    rows, cols = 32, 256
+    flat = np.arange(rows * cols, dtype=np.int64)
+    out = W.unpack_h_tiles_host(flat, cols)
+    for r in range(0, rows, 3):
+        for c in range(0, cols, 5):
+            kb, cc = c >> 7, c & 127
+            e = cc & 31
+            lane = (cc >> 5) * 16 + (r & 15)
+            idx = ((((r >> 4) * (cols // 128) + kb) * 4 + (e >> 3)) * 64 + lane) * 8 + (e & 7)
+            assert out[r, c] == idx
+    assert np.array_equal(np.sort(out.reshape(-1)), flat)

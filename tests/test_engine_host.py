@@ -1,0 +1,175 @@
+"""Host-side boundary tests (no GPU): the C-ABI libraries load and export every
+declared entry point, the ctypes structs match the C header's layout, the
+engine manifest contract is enforced by the native parser, engine emission is
+deterministic, and profiles select/refuse shapes the way the reference's
+planner does (compiler/netra_compiler/profiles.py:70-77)."""
+import ctypes
+import json
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import netra_moe as nm
+from netra_moe import paths, runtime
+from netra_moe.engine import OP_NAMES, operations
+
+REPO = Path(__file__).resolve().parent.parent
+
+
+def declared(header: Path) -> list[str]:
+    text = header.read_text()
+    return sorted(set(re.findall(r"^[A-Za-z_][\w \*]*?\b(netra_\w+)\(", text, flags=re.M)))
+
+
+def test_headers_declare_the_reference_engine_abi():
+    names = declared(REPO / "include" / "netra_engine.h")
+    ref = ["netra_engine_create", "netra_engine_profile_count", "netra_engine_query_profile",
+           "netra_engine_bind", "netra_engine_finalize_bindings", "netra_engine_prepare_profile",
+           "netra_engine_launch", "netra_engine_launch_operation", "netra_engine_launch_operation_bound",
+           "netra_engine_last_error", "netra_engine_destroy"]
+    assert set(ref) <= set(names)
+    assert set(names) == set(runtime.ENGINE_SYMBOLS)
+
+
+@pytest.mark.parametrize("header,lib", [("netra_engine.h", "engine"), ("netra_moe.h", "bridge")])
+def test_libraries_load_and_export_every_declared_symbol(header, lib):
+    path = paths.engine_library() if lib == "engine" else paths.bridge_library()
+    dll = ctypes.CDLL(str(path))
+    for name in declared(REPO / "include" / header):
+        assert hasattr(dll, name), f"{path.name} does not export {name}"
+
+
+def test_ctypes_structs_match_the_c_header(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text(r"""
+#include <stdio.h>
+#include <stddef.h>
+#include "netra_engine.h"
+int main(void) {
+  printf("%zu %zu %zu %zu\n", sizeof(netra_engine_options_t), sizeof(netra_profile_info_t),
+         sizeof(netra_launch_shape_t), sizeof(netra_pointer_binding_t));
+  printf("%zu %zu %zu\n", offsetof(netra_profile_info_t, min_sequence),
+         offsetof(netra_profile_info_t, workspace_bytes), offsetof(netra_profile_info_t, requires_fallback));
+  printf("%d %d %d\n", NETRA_STATUS_BINDING, NETRA_STATUS_BUSY, NETRA_STATUS_FALLBACK_REQUIRED);
+  return 0;
+}
+""")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-D__HIP_PLATFORM_AMD__", f"-I{REPO / 'include'}", "-I/opt/rocm/include",
+                    str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    sizes = [int(v) for v in out[0].split()]
+    assert sizes == [ctypes.sizeof(runtime.EngineOptions), ctypes.sizeof(runtime.ProfileInfo),
+                     ctypes.sizeof(runtime.LaunchShape), ctypes.sizeof(runtime.PointerBinding)]
+    offs = [int(v) for v in out[1].split()]
+    assert offs == [runtime.ProfileInfo.min_sequence.offset, runtime.ProfileInfo.workspace_bytes.offset,
+                    runtime.ProfileInfo.requires_fallback.offset]
+    assert [int(v) for v in out[2].split()] == [runtime.Status.BINDING, runtime.Status.BUSY,
+                                               runtime.Status.FALLBACK_REQUIRED]
+
+
+@pytest.fixture()
+def engine_dir(tmp_path):
+    cfg = nm.BASELINE_CONFIGS["decode_t64"]
+    d = tmp_path / "eng"
+    nm.compile_moe_engine(cfg, d)
+    return d
+
+
+def test_emitted_engine_passes_the_native_manifest_check(engine_dir):
+    st, msg = nm.manifest_check(engine_dir)
+    assert st == nm.Status.OK, msg
+    doc = json.loads((engine_dir / "engine.json").read_text())
+    assert [op["name"] for op in doc["operations"]] == [f"moe.{n}" for n in OP_NAMES]
+
+
+def _corrupt(engine_dir: Path, mutate) -> tuple:
+    doc = json.loads((engine_dir / "engine.json").read_text())
+    mutate(doc)
+    (engine_dir / "engine.json").write_text(json.dumps(doc))
+    return nm.manifest_check(engine_dir)
+
+
+@pytest.mark.parametrize("mutate,needle", [
+    (lambda d: d.update(format_version="netra-engine-0"), "format_version"),
+    (lambda d: d.update(target="gfx942"), "target"),
+    (lambda d: d.update(wave_size=32), "wave_size"),
+    (lambda d: d["required_rocm"].update(code_object_version=5), "code object"),
+    (lambda d: d["required_rocm"].update(minimum="7"), "MAJOR.MINOR"),
+    (lambda d: d["operations"][0].update(hsaco="hsaco/../engine.json"), "hsaco"),
+    (lambda d: d["operations"][0].update(hsaco="/abs/x.hsaco"), "hsaco"),
+    (lambda d: d["operations"][0]["launch"].update(grid=[0, 1, 1]), "nonzero"),
+    (lambda d: d["operations"][0]["launch"].update(block=[2048, 1, 1]), "1024"),
+    (lambda d: d["operations"][2].update(launch={**d["operations"][2]["launch"], "dynamic_lds_bytes": 200000}), "LDS"),
+    (lambda d: d["operations"][0]["arguments"].append({"kind": "pointer", "source": "workspace",
+                                                       "workspace_offset": d["workspace_bytes"]}), "workspace"),
+    (lambda d: d["operations"][0]["arguments"].extend([{"kind": "u32_constant", "value": 1}] * 40), "32"),
+    (lambda d: d["operations"][0]["arguments"].append({"kind": "f64_constant", "value": 1}), "kind"),
+    (lambda d: d["profiles"][0]["guards"]["m"].update(min=9, max=3), "min > max"),
+])
+def test_manifest_violations_are_refused(engine_dir, mutate, needle):
+    st, msg = _corrupt(engine_dir, mutate)
+    assert st == nm.Status.MANIFEST
+    assert needle.lower() in msg.lower(), msg
+
+
+def test_manifest_parser_rejects_malformed_json(engine_dir):
+    (engine_dir / "engine.json").write_text('{"a": 1, "a": 2}')
+    st, msg = nm.manifest_check(engine_dir)
+    assert st == nm.Status.MANIFEST and "duplicate" in msg
+    (engine_dir / "engine.json").write_text('{"a": [1, 2')
+    assert nm.manifest_check(engine_dir)[0] == nm.Status.MANIFEST
+    shutil.rmtree(engine_dir)
+    assert nm.manifest_check(engine_dir)[0] == nm.Status.IO
+
+
+def test_engine_emission_is_deterministic_and_contract_ids_track_shape(tmp_path):
+    cfg = nm.BASELINE_CONFIGS["verify_t512"]
+    a, b = tmp_path / "a", tmp_path / "b"
+    nm.compile_moe_engine(cfg, a)
+    nm.compile_moe_engine(cfg, b)
+    for f in ("engine.json", "contracts.json", "graph_recipe.json", "memory_plan.json"):
+        assert (a / f).read_bytes() == (b / f).read_bytes()
+    ids_a = [c["id"] for c in json.loads((a / "contracts.json").read_text())["contracts"]]
+    c2 = nm.BASELINE_CONFIGS["prefill_t4096"]
+    nm.compile_moe_engine(c2, tmp_path / "c")
+    ids_c = [c["id"] for c in json.loads((tmp_path / "c" / "contracts.json").read_text())["contracts"]]
+    assert all(i.startswith("nk_") and len(i) == 27 for i in ids_a)
+    assert len(set(ids_a) & set(ids_c)) == 0
+
+
+def test_every_emitted_kernel_symbol_is_in_the_code_object():
+    blob = paths.hsaco_path().read_bytes()
+    for cfg in nm.BASELINE_CONFIGS.values():
+        for path in ("stream", "tile"):
+            for op in operations(cfg, path):
+                assert op["symbol"].encode() in blob, op["symbol"]
+
+
+def test_profiles_select_exact_shapes_and_refuse_neighbours():
+    p64 = nm.profile_for(nm.BASELINE_CONFIGS["decode_t64"])
+    p1 = nm.profile_for(nm.BASELINE_CONFIGS["decode_t1"])
+    sel = nm.select_profile((p64, p1), {"m": 64, "batch": 1, "sequence": 0})
+    assert sel.supported and sel.profile is p64
+    miss = nm.select_profile((p64, p1), {"m": 63, "batch": 1, "sequence": 0})
+    assert not miss.supported and "fallback" in miss.reason
+    assert not nm.select_profile((p64,), {"m": 64, "batch": 1, "sequence": 0}, tensor_parallel=2).supported
+    # netra-profile-1 JSON round trip, as in manifests/gfx950/profiles/decode_m1.json
+    doc = {"format": "netra-profile-1", "name": "decode_m1", "guards": {"m": {"min": 1, "max": 1},
+           "batch": {"min": 1, "max": 64}, "sequence": {"min": 0, "max": 1048576}},
+           "quantization": "fp8_block128", "tensor_parallel": "deployment", "priority": 30}
+    prof = nm.ShapeProfile.from_dict(doc)
+    assert prof.guard("m").matches(1) and not prof.guard("m").matches(2) and prof.priority == 30
+
+
+def test_engine_create_without_a_gpu_reports_a_status():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("host-only behaviour")
+    d = Path(paths.PKG_ROOT) / "lib"
+    with pytest.raises(nm.NetraError) as err:
+        nm.Engine(d)
+    assert err.value.status in (nm.Status.HIP, nm.Status.UNSUPPORTED_TARGET)

@@ -35,16 +35,24 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def gate_up_bytes(cfg, touched: int) -> int:
+def gate_up_bytes(cfg, touched: int, path: str) -> int:
+    """Algorithmic HBM bytes of one gate/up launch: touched experts' W13 + scales,
+    x_q + x scales, and h (bf16 on the decode path; e4m3 + 1x128 scales on the
+    prefill path) for every route row."""
     w = touched * (2 * cfg.I * cfg.H + 4 * (2 * cfg.I // 128) * (cfg.H // 128))
     acts = cfg.T * cfg.H + 4 * cfg.T * (cfg.H // 128)
-    outs = cfg.routes * cfg.I + 4 * cfg.routes * (cfg.I // 128)
+    if path == "stream":
+        outs = 2 * cfg.routes * cfg.I
+    else:
+        outs = cfg.routes * cfg.I + 4 * cfg.routes * (cfg.I // 128)
     return w + acts + outs
 
 
-def down_bytes(cfg, touched: int) -> int:
+def down_bytes(cfg, touched: int, path: str) -> int:
+    """Touched experts' W2 + scales, h in, fp32 partial rows out."""
     w = touched * (cfg.H * cfg.I + 4 * (cfg.H // 128) * (cfg.I // 128))
-    return w + cfg.routes * cfg.I + 4 * cfg.routes * (cfg.I // 128) + 4 * cfg.routes * cfg.H
+    h = 2 * cfg.routes * cfg.I if path == "stream" else cfg.routes * cfg.I + 4 * cfg.routes * (cfg.I // 128)
+    return w + h + 4 * cfg.routes * cfg.H
 
 
 def time_graph(layers, steps: int, warmup: int, torch):
@@ -111,6 +119,111 @@ def cpu_baseline(cfg, act_cpu, w_host, threads: int, min_seconds: float):
                       f"fp64-accumulated C oracle, OpenMP), median of {len(runs)} runs, {med * 1e3:.1f} ms each"}
 
 
+COPY_BYTES = 1 << 30
+PMC_REPS = 6
+
+
+def copy_probe(W, torch, dev, reps: int = 10) -> float:
+    """GB/s of the library's plain copy kernel over 1 GiB (read + write bytes)."""
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    W.device_copy(src, dst)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        W.device_copy(src, dst)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    del src, dst
+    return 2 * COPY_BYTES / (ms / 1e3) / 1e9
+
+
+def pmc_workload(cfg_name: str) -> int:
+    """Run under rocprofv3 --pmc: three calibration copies of COPY_BYTES, then
+    PMC_REPS direct (non-graph) layer calls, each operation a dispatch of its own."""
+    import torch
+
+    from netra_moe import weights as W
+    from netra_moe.config import BASELINE_CONFIGS
+    from netra_moe.layer import MoELayer
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    cfg = BASELINE_CONFIGS[cfg_name]
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        W.device_copy(src, dst)
+    torch.cuda.synchronize()
+    del src, dst
+    ws = W.synthetic_expert_weights(cfg, WEIGHT_SEED, dev)
+    act = W.synthetic_activations(cfg, dev)
+    lay = MoELayer(cfg, {"router_w": act["router_w"], "router_bias": act["router_bias"], **ws}, graph=False)
+    lay.x.copy_(act["x"])
+    for _ in range(PMC_REPS):
+        lay.forward()
+    torch.cuda.synchronize()
+    lay.close()
+    log(f"[pmc-workload] {cfg_name}: done")
+    return 0
+
+
+def read_counter_csv(directory: Path, counter: str) -> dict[str, list[float]]:
+    """{kernel name: [per-dispatch value]} from a rocprofv3 counter_collection csv."""
+    import csv
+
+    files = sorted(directory.rglob("*counter_collection.csv"))
+    if not files:
+        raise FileNotFoundError(f"no counter_collection.csv under {directory}")
+    out: dict[str, list[float]] = {}
+    for f in files:
+        with f.open() as fh:
+            for row in csv.DictReader(fh):
+                if row.get("Counter_Name") != counter:
+                    continue
+                out.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+    return out
+
+
+def measure_traffic(cfg_name: str, kernel_prefix: str, out_dir: Path) -> dict:
+    """HBM bytes per launch of the first kernel whose name starts with
+    kernel_prefix, from two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE, KiB
+    per dispatch) over a child process running pmc_workload, each scaled by the
+    same counter's reading for the calibration copy of COPY_BYTES bytes."""
+    import shutil
+    import subprocess
+
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        raise FileNotFoundError("rocprofv3 not on PATH")
+    res = {"kernel": None, "counters": {}}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = out_dir / f"pmc_{counter.lower()}"
+        shutil.rmtree(d, ignore_errors=True)
+        cmd = ["timeout", "-s", "KILL", "240", exe, "--pmc", counter, "--output-format", "csv",
+               "-d", str(d), "-o", "pmc", "--", sys.executable, "-u", str(Path(__file__).resolve()),
+               "--pmc-workload", "--config", cfg_name]
+        log(f"[bench] counter pass {counter}: {' '.join(cmd)}")
+        proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+        vals = read_counter_csv(d, counter)  # results are whole even if the profiler exits non-zero
+        copy = [v for k, v in vals.items() if k.startswith("netra_moe_copy_gfx950")]
+        kern = [(k, v) for k, v in vals.items() if k.startswith(kernel_prefix)]
+        if not copy or not kern:
+            raise RuntimeError(f"{counter}: kernels missing from the counter csv (rc {proc.returncode})")
+        copy_kib = sorted(copy[0])[len(copy[0]) // 2]
+        name, kv = kern[0]
+        kib = sorted(kv)[len(kv) // 2]
+        factor = COPY_BYTES / copy_kib  # bytes per counter unit, from the copy
+        res["kernel"] = name
+        res["counters"][counter] = {"kernel_kib_median": kib, "dispatches": len(kv),
+                                    "copy_kib_median": copy_kib, "bytes_per_unit": factor,
+                                    "bytes": kib * factor}
+    res["bytes"] = res["counters"]["FETCH_SIZE"]["bytes"] + res["counters"]["WRITE_SIZE"]["bytes"]
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -121,19 +234,24 @@ def main() -> int:
                     help="comma-separated extra configs with the same dims ('' for none)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 --pmc passes that measure the dominant kernel's HBM bytes")
+    ap.add_argument("--pmc-workload", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
 
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is a design "
                           "note (expert parallel over RCCL), not implemented", "n_gpus": args.gpus}))
         return 2
+    if args.pmc_workload:
+        return pmc_workload(args.config)
 
     import numpy as np
     import torch
 
     from netra_moe import weights as W
     from netra_moe.config import BASELINE_CONFIGS
-    from netra_moe.engine import OP_NAMES
+    from netra_moe.engine import OP_NAMES, operations, resolve_path
     from netra_moe.layer import MoELayer
 
     if not torch.cuda.is_available():
@@ -142,6 +260,9 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     cfg = BASELINE_CONFIGS[args.config]
+    path = resolve_path(cfg)
+    copy_gbps = copy_probe(W, torch, dev)
+    log(f"[bench] copy kernel: {copy_gbps:.0f} GB/s (read + write)")
     log(f"[bench] weights: 2 copies of {cfg.Etot} experts ({2 * cfg.Etot * cfg.expert_bytes() / 1e9:.2f} GB)")
     # copy 0 also keeps its row-major bytes: the CPU baseline reads that layout
     wsets = [W.synthetic_expert_weights(cfg, WEIGHT_SEED + i, dev, keep_row_major=(i == 0))
@@ -161,9 +282,10 @@ def main() -> int:
         touched = int(np.unique(ids).size)
         flops = c.flops()
         nbytes = c.algorithmic_bytes(touched)
-        res = {"T": c.T, "ms_per_step": ms, "wall_ms_per_step": wall_ms, "tokens_per_s": c.T / (ms / 1e3),
-               "tflops": flops / (ms / 1e3) / 1e12, "gbps": nbytes / (ms / 1e3) / 1e9,
-               "touched_experts": touched, "algorithmic_bytes": nbytes, "flops": flops}
+        res = {"T": c.T, "gemm_path": resolve_path(c), "ms_per_step": ms, "wall_ms_per_step": wall_ms,
+               "tokens_per_s": c.T / (ms / 1e3), "tflops": flops / (ms / 1e3) / 1e12,
+               "gbps": nbytes / (ms / 1e3) / 1e9, "touched_experts": touched,
+               "algorithmic_bytes": nbytes, "flops": flops}
         res["hbm_frac"] = res["gbps"] / HBM_PEAK_GBPS
         res["mfma_frac"] = res["tflops"] / FP8_PEAK_TFLOPS
         kern = None
@@ -185,12 +307,18 @@ def main() -> int:
 
     log(f"[bench] {cfg.name}: warmup {args.warmup}, steps {args.steps}")
     main_res, kern, act = run_config(cfg, args.steps, args.warmup, True)
-    gu_us = kern["gate_up"]
-    gu_bytes = gate_up_bytes(cfg, main_res["touched_experts"])
-    roof = {"kernel": "netra_moe_gate_up_gfx950", "bound": "hbm",
+    touched = main_res["touched_experts"]
+    gu_us, dn_us = kern["gate_up"], kern["down"]
+    gu_bytes = gate_up_bytes(cfg, touched, path)
+    dn_bytes = down_bytes(cfg, touched, path)
+    gu_symbol = next(op["symbol"] for op in operations(cfg, path) if op["name"] == "moe.gate_up")
+    roof = {"kernel": gu_symbol, "bound": "hbm",
             "achieved": gu_bytes / (gu_us * 1e-6) / 1e9, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "traffic": None, "avg_us": gu_us, "algorithmic_bytes_per_launch": gu_bytes}
+            "traffic": None, "avg_us": gu_us, "algorithmic_bytes_per_launch": gu_bytes,
+            "box_copy_gbps": copy_gbps}
     roof["frac"] = roof["achieved"] / roof["peak"]
+    other = {"down": {"achieved_gbps": dn_bytes / (dn_us * 1e-6) / 1e9, "avg_us": dn_us,
+                      "algorithmic_bytes_per_launch": dn_bytes}}
 
     secondary = {}
     for name in [s for s in args.secondary.split(",") if s]:
@@ -210,6 +338,17 @@ def main() -> int:
                   "w2_scale": wsets[0]["w2_scale"].cpu().numpy()}
         cpu = cpu_baseline(cfg, act, w_host, threads, args.cpu_seconds)
 
+    if not args.no_traffic:
+        del wsets
+        torch.cuda.empty_cache()
+        try:
+            t = measure_traffic(cfg.name, gu_symbol, REPO / "gpurun_out" / "bench_pmc")
+            roof["traffic"] = t["bytes"]
+            roof["traffic_detail"] = t
+        except Exception as exc:  # counters unavailable: traffic stays null, the reason is reported
+            roof["traffic_error"] = f"{type(exc).__name__}: {exc}"
+            log(f"[bench] traffic not measured: {roof['traffic_error']}")
+
     line = {
         "metric": "MoE layer tokens/s, decode T=64 (H=2048, 256 routed + 1 shared expert, top-8, I=512, "
                   "FP8 E4M3 128x128/1x128 block scales)",
@@ -218,8 +357,8 @@ def main() -> int:
         "scaling": "weak", "vs_baseline": None, "dtype": "fp8_e4m3", "data": "synthetic (seeded)",
         "config": {"workload": cfg.name, "T": cfg.T, "H": cfg.H, "E": cfg.E, "K": cfg.K, "S": cfg.S,
                    "I": cfg.I, "block_m": 64, "weight_copies_rotated": 2},
-        "layer": main_res, "kernels_us": kern, "roofline": roof, "cpu_baseline": cpu,
-        "secondary": secondary,
+        "layer": main_res, "kernels_us": kern, "roofline": roof, "other_kernels": other,
+        "cpu_baseline": cpu, "secondary": secondary,
     }
     print(json.dumps(line), flush=True)
     return 0

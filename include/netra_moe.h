@@ -29,7 +29,7 @@
 //       h bf16[CAP*64,I]; T, H, I, Ktot, Etot)   grid 512, block 256 (persistent)
 //   netra_moe_down_stream_i<I>_gfx950(h, w2 e4m3[Etot,H,I], w2s f32[Etot,H/128,I/128],
 //       sorted_ids, sorted_expert, tile_map, num_valid, partial f32[T*Ktot,H];
-//       T, H, I, Ktot, Etot)   grid 768, block 256 (persistent)
+//       T, H, I, Ktot, Etot)   grid 1024, block 256 (persistent)
 //   prefill ("tile") GEMMs:
 //   netra_moe_gate_up_tile_gfx950(xq, xs, w13, w13s, sorted_ids, sorted_expert,
 //       num_valid, hq e4m3[CAP*64,I], hs f32[CAP*64,I/128]; T, H, I, Ktot, Etot)
@@ -66,8 +66,10 @@ int netra_moe_quant_blocks(const float* w, uint8_t* q, float* s, uint32_t groups
 
 // Weight layout change for the GEMM kernels: row-major e4m3 src[groups, n, k]
 // -> dst in the tile16x128 layout (n/16 x k/128 tiles, row tiles outermost;
-// inside a tile lane l's 32 bytes are row l % 16, columns (l / 16) * 32 .. +31,
-// at byte l * 32). n % 16 == 0, k % 128 == 0, src and dst distinct. The
+// each tile is 2 KiB; lane l's 32-byte MFMA operand, row l % 16, columns
+// (l / 16) * 32 .. +31, is split into its low half at byte l * 16 and its high
+// half at byte 1024 + l * 16, so each half-operand wave load reads 1 KiB
+// contiguous). n % 16 == 0, k % 128 == 0, src and dst distinct. The
 // reference consumes AITER's own shuffled layout
 // (kernels/gfx950/templates/common/addressing.inc:22-27); this is the
 // layout of this build's kernels. Same error convention as above.
@@ -79,6 +81,12 @@ int netra_moe_pack_tiles(const uint8_t* src, uint8_t* dst, uint32_t groups, uint
 // No counterpart in the reference; tests use it to prove the two agree.
 int netra_moe_e4m3_check(const float* in, uint8_t* sw, uint8_t* hw, uint32_t n,
                          hipStream_t stream);
+
+// Device-to-device copy of `bytes` (a multiple of 16, both pointers 16-byte
+// aligned) by a plain streaming kernel. No counterpart in the reference: the
+// benchmark uses it to calibrate the HBM byte counters and to measure the
+// achievable copy bandwidth.
+int netra_moe_copy(const void* src, void* dst, uint64_t bytes, hipStream_t stream);
 
 const char* netra_moe_last_error(void);
 

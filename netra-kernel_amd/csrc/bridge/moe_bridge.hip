@@ -57,4 +57,16 @@ extern "C" int netra_moe_e4m3_check(const float* in, uint8_t* sw, uint8_t* hw, u
   return 0;
 }
 
+extern "C" int netra_moe_copy(const void* src, void* dst, uint64_t bytes, hipStream_t stream) {
+  if (!src || !dst || bytes == 0 || bytes % 16u || (reinterpret_cast<uintptr_t>(src) & 15u) ||
+      (reinterpret_cast<uintptr_t>(dst) & 15u))
+    return fail(-1, "netra_moe_copy: null pointer, or size/alignment not a multiple of 16 bytes");
+  hipLaunchKernelGGL(netra_moe_copy_gfx950, dim3(2048), dim3(256), 0, stream,
+                     static_cast<const uint4*>(src), static_cast<uint4*>(dst), bytes / 16u);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(static_cast<int>(err), hipGetErrorString(err));
+  g_last_error.clear();
+  return 0;
+}
+
 extern "C" const char* netra_moe_last_error(void) { return g_last_error.c_str(); }

@@ -109,3 +109,14 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_pack_tiles_gfx950(
   *reinterpret_cast<uint4*>(d) = lo;
   *reinterpret_cast<uint4*>(d + 1024) = hi;
 }
+
+// ---------------------------------------------------------------------------
+// Plain 16-byte-per-lane copy of known size. Counter calibration: its
+// FETCH_SIZE / WRITE_SIZE readings over a copy of B bytes convert the same
+// counters' readings on the MoE kernels into HBM bytes, and its duration gives
+// the achievable copy bandwidth of the box.
+NK_KERNEL __launch_bounds__(256) void netra_moe_copy_gfx950(
+    const uint4* __restrict__ src, uint4* __restrict__ dst, uint64_t n16) {
+  const uint64_t stride = (uint64_t)gridDim.x * 256u;
+  for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+}

@@ -35,6 +35,8 @@ def bridge_library() -> ctypes.CDLL:
         lib.netra_moe_pack_tiles.restype = ctypes.c_int
         lib.netra_moe_e4m3_check.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_uint32, ctypes.c_void_p]
         lib.netra_moe_e4m3_check.restype = ctypes.c_int
+        lib.netra_moe_copy.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_uint64, ctypes.c_void_p]
+        lib.netra_moe_copy.restype = ctypes.c_int
         lib.netra_moe_last_error.argtypes = []
         lib.netra_moe_last_error.restype = ctypes.c_char_p
         _bridge = lib
@@ -72,6 +74,19 @@ def pack_tiles(q: torch.Tensor) -> torch.Tensor:
     if rc != 0:
         raise RuntimeError(f"netra_moe_pack_tiles failed ({rc}): {lib.netra_moe_last_error().decode()}")
     return out
+
+
+def device_copy(src: torch.Tensor, dst: torch.Tensor) -> None:
+    """Byte copy src -> dst (same size, GPU, 16-byte multiple) by the library's
+    plain streaming kernel, on the current stream."""
+    n = src.numel() * src.element_size()
+    if not (src.is_cuda and dst.is_cuda and src.is_contiguous() and dst.is_contiguous()) or \
+            n != dst.numel() * dst.element_size():
+        raise ValueError("device_copy needs two contiguous GPU tensors of the same byte size")
+    lib = bridge_library()
+    rc = lib.netra_moe_copy(src.data_ptr(), dst.data_ptr(), n, torch.cuda.current_stream(src.device).cuda_stream)
+    if rc != 0:
+        raise RuntimeError(f"netra_moe_copy failed ({rc}): {lib.netra_moe_last_error().decode()}")
 
 
 def pack_tiles_host(q: np.ndarray) -> np.ndarray:

@@ -17,12 +17,14 @@
 //   netra_moe_router_h<H>_gfx950, H in {512,1024,2048,4096} (x bf16[T,H],
 //       w bf16[E+S,H], logits bf16[T,E+S], xq e4m3[T,H], xs f32[T,H/128],
 //       mask u64[(E+S)*W]; T, H, rows=E+S, (E+S)*W)
-//       grid (ceil(rows/16), ceil(T/4)), block 256
+//       grid (ceil(rows/16), ceil(T/NT)), block 256, NT = 4 (2 for H = 4096),
+//       static LDS 4 * NT * H bytes
 //   netra_moe_topk_gfx950(logits, bias f32[E], ids i32[T,Ktot], weights f32[T,Ktot],
-//       mask; T, E, K, S, W)   grid ceil(T/4), block 256
+//       mask; T, E, K, S, W)   grid ceil(T/4), block 256 (one wave per token)
 //   netra_moe_sort_gfx950(ids, mask, sorted_ids i32[CAP*64], sorted_expert i32[CAP],
 //       tile_map i32[CAPT], num_valid i32[4], counts i32[E+S]; T, Ktot, Etot, W, CAP)
-//       grid 1, block 1024, dynamic LDS 4*(Etot*W + 3*Etot + 2 + CAP)
+//       grid 1, block 1024, dynamic LDS 4*B + (8*Etot*W if that stays <= 160 KiB),
+//       B = Etot*W + 3*Etot + 34 + CAP rounded up to even
 //   decode ("stream") GEMMs, H in {512,1024,2048,4096}, I in {256,512,1024,2048}:
 //   netra_moe_gate_up_stream_h<H>_gfx950(xq, xs, w13 e4m3[Etot,2I,H],
 //       w13s f32[Etot,2I/128,H/128], sorted_ids, sorted_expert, tile_map, num_valid,

@@ -9,6 +9,10 @@
 // route_reduce_splitk2_f16.inc:6-117 and down_reduce_mfma_2wave.inc:202-213:
 // slot-ordered weighted sum, then bf16). out[t, n] = bf16(sum over slots in
 // order of fmaf(w[t, s], partial[t * Ktot + s, n], acc)).
+// Up to kCombineBatch slots' partial rows are requested before the first fmaf,
+// so a token waits on memory once per batch rather than once per slot.
+constexpr uint32_t kCombineBatch = 16;
+
 NK_KERNEL __launch_bounds__(256) void netra_moe_combine_gfx950(
     const float* __restrict__ partial, const float* __restrict__ weights,
     uint16_t* __restrict__ out, uint32_t T, uint32_t H, uint32_t Ktot) {
@@ -16,13 +20,26 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_combine_gfx950(
   const uint32_t n = (blockIdx.x * 256u + threadIdx.x) * 4u;
   if (t >= T || n >= H) return;
   float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-  for (uint32_t s = 0; s < Ktot; ++s) {
-    const float w = weights[(size_t)t * Ktot + s];
-    const float4 p = *reinterpret_cast<const float4*>(partial + ((size_t)t * Ktot + s) * H + n);
-    a0 = fmaf(w, p.x, a0);
-    a1 = fmaf(w, p.y, a1);
-    a2 = fmaf(w, p.z, a2);
-    a3 = fmaf(w, p.w, a3);
+  const float* prow = partial + (size_t)t * Ktot * H + n;
+  for (uint32_t s0 = 0; s0 < Ktot; s0 += kCombineBatch) {
+    float4 p[kCombineBatch];
+    float w[kCombineBatch];
+#pragma unroll
+    for (uint32_t i = 0; i < kCombineBatch; ++i) {
+      if (s0 + i < Ktot) {
+        p[i] = *reinterpret_cast<const float4*>(prow + (size_t)(s0 + i) * H);
+        w[i] = weights[(size_t)t * Ktot + s0 + i];
+      }
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kCombineBatch; ++i) {
+      if (s0 + i < Ktot) {
+        a0 = fmaf(w[i], p[i].x, a0);
+        a1 = fmaf(w[i], p[i].y, a1);
+        a2 = fmaf(w[i], p[i].z, a2);
+        a3 = fmaf(w[i], p[i].w, a3);
+      }
+    }
   }
   uint2 o;
   o.x = (uint32_t)nk::bf16_rne(a0) | ((uint32_t)nk::bf16_rne(a1) << 16);

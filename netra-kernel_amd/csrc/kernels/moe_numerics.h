@@ -137,4 +137,33 @@ __device__ __forceinline__ v4f mfma_e4m3_16x16x128(v8i a, v8i b) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, zero, 0, 0, 0, 0, 0, 0);
 }
 
+// Wave-wide unsigned max / min (every lane active): DPP inside each 16-lane
+// row (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror), then the four row results combined from scalar readlanes.
+template <bool kMax>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v) {
+  auto pick = [](uint32_t a, uint32_t b) { return kMax ? (a > b ? a : b) : (a < b ? a : b); };
+  v = pick(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  v = pick(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  v = pick(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+  v = pick(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return pick(pick(a, b), pick(c, d));
+}
+
+// Order-preserving map of fp32 onto uint32 (larger float -> larger code);
+// -0 is first folded onto +0 so the two compare equal. Finite and infinite
+// inputs map to codes >= 0x007fffff, so 0 is free as an "absent" marker.
+__device__ __forceinline__ uint32_t order_bits(float z) {
+  uint32_t u = __float_as_uint(z);
+  if (z == 0.0f) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float from_order_bits(uint32_t o) {
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
 }  // namespace nk

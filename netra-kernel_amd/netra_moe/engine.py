@@ -104,7 +104,11 @@ def tensor_table(cfg: MoEConfig, path: str = "auto") -> dict[str, TensorSpec]:
 
 OP_NAMES = ("router", "topk", "sort", "gate_up", "down", "combine")
 ROUTER_H = (512, 1024, 2048, 4096)   # netra_moe_router_h<H>_gfx950
-ROUTER_TOKENS = 4                     # tokens per router workgroup (kRouterTokens)
+
+
+def router_tokens(H: int) -> int:
+    """Tokens per router workgroup (template NT of netra_moe_router_h<H>)."""
+    return 2 if H >= 4096 else 4
 
 
 def operations(cfg: MoEConfig, path: str = "auto") -> list[dict]:
@@ -117,15 +121,15 @@ def operations(cfg: MoEConfig, path: str = "auto") -> list[dict]:
     u = lambda v: ("u32", int(v))  # noqa: E731
     ops = [
         dict(name="moe.router", symbol=f"netra_moe_router_h{H}_gfx950",
-             grid=((cfg.router_rows + 15) // 16, (T + ROUTER_TOKENS - 1) // ROUTER_TOKENS, 1),
-             block=(256, 1, 1), lds=0, dyn=0,
+             grid=((cfg.router_rows + 15) // 16, (T + router_tokens(H) - 1) // router_tokens(H), 1),
+             block=(256, 1, 1), lds=4 * router_tokens(H) * H, dyn=0,
              args=["x", "router_w", "logits", "x_q", "x_scale", "mask",
                    u(T), u(H), u(cfg.router_rows), u(cfg.Etot * W)],
              reads=["x", "router_w"], writes=["logits", "x_q", "x_scale", "mask"],
              refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150",
                    "tools/benchmark/export_qwen36_router_bf16_capture.py:78"]),
         dict(name="moe.topk", symbol="netra_moe_topk_gfx950",
-             grid=((T + 3) // 4, 1, 1), block=(256, 1, 1), lds=19712, dyn=0,
+             grid=((T + 3) // 4, 1, 1), block=(256, 1, 1), lds=0, dyn=0,
              args=["logits", "router_bias", "topk_ids", "topk_weights", "mask",
                    u(T), u(cfg.E), u(cfg.K), u(cfg.S), u(W)],
              reads=["logits", "router_bias", "mask"], writes=["topk_ids", "topk_weights", "mask"],

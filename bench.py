@@ -251,7 +251,7 @@ def main() -> int:
 
     from netra_moe import weights as W
     from netra_moe.config import BASELINE_CONFIGS
-    from netra_moe.engine import OP_NAMES, operations, resolve_path
+    from netra_moe.engine import operations, resolve_path
     from netra_moe.layer import MoELayer
 
     if not torch.cuda.is_available():
@@ -297,7 +297,7 @@ def main() -> int:
                 lay.x.copy_(act["x"].to(dev))
                 dl.append(lay)
             kern = {}
-            for op in OP_NAMES:
+            for op in dl[0].op_names:
                 kern[op] = time_operation(dl, op, max(20, steps // 2), torch) * 1e3  # us
             for lay in dl:
                 lay.close()

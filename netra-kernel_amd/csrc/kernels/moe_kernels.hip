@@ -3,14 +3,16 @@
 //
 // Layer pipeline, one engine operation per kernel, fixed grids with
 // device-side early exit so a whole layer call is one capturable HIP graph:
-//   router (logits + input quant) -> topk_sort (top-k, then the sort in the
-//   last workgroup) -> gate_up_{stream|tile} -> down_{stream|tile} -> combine
+//   front end, exact:  router (logits + input quant) -> topk -> sort
+//   front end, screen: route_screen -> sort_scan -> sort_scatter
+//   then gate_up_{stream|tile} -> down_{stream|tile} -> combine
 // Every kernel takes plain pointers followed by u32 shape constants, in the
 // order documented in include/netra_moe.h. Host code validates shapes before
 // a launch; kernels also bound-check data-dependent indices (expert ids,
 // sorted positions) so malformed routing cannot address memory outside the
 // buffers the shapes describe.
 #include "moe_router.hip"
+#include "moe_route_prefill.hip"
 #include "moe_gemm_stream.hip"
 #include "moe_gemm_tile.hip"
 #include "moe_misc.hip"

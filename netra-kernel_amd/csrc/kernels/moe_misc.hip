@@ -47,6 +47,51 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_combine_gfx950(
   *reinterpret_cast<uint2*>(out + (size_t)t * H + n) = o;
 }
 
+// The same combine over bf16 route partials (the tile-path down GEMM's output,
+// as the reference's prefill route reducer reads 16-bit partials): eight
+// columns per lane, fp32 accumulation in slot order, bf16 out.
+NK_KERNEL __launch_bounds__(256) void netra_moe_combine_bf16_gfx950(
+    const uint16_t* __restrict__ partial, const float* __restrict__ weights,
+    uint16_t* __restrict__ out, uint32_t T, uint32_t H, uint32_t Ktot) {
+  const uint32_t t = blockIdx.y;
+  const uint32_t n = (blockIdx.x * 256u + threadIdx.x) * 8u;
+  if (t >= T || n >= H) return;
+  float a[8];
+#pragma unroll
+  for (uint32_t i = 0; i < 8; ++i) a[i] = 0.0f;
+  const uint16_t* prow = partial + (size_t)t * Ktot * H + n;
+  for (uint32_t s0 = 0; s0 < Ktot; s0 += kCombineBatch) {
+    uint4 p[kCombineBatch];
+    float w[kCombineBatch];
+#pragma unroll
+    for (uint32_t i = 0; i < kCombineBatch; ++i) {
+      if (s0 + i < Ktot) {
+        p[i] = *reinterpret_cast<const uint4*>(prow + (size_t)(s0 + i) * H);
+        w[i] = weights[(size_t)t * Ktot + s0 + i];
+      }
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kCombineBatch; ++i) {
+      if (s0 + i < Ktot) {
+        a[0] = fmaf(w[i], nk::bf16_lo(p[i].x), a[0]);
+        a[1] = fmaf(w[i], nk::bf16_hi(p[i].x), a[1]);
+        a[2] = fmaf(w[i], nk::bf16_lo(p[i].y), a[2]);
+        a[3] = fmaf(w[i], nk::bf16_hi(p[i].y), a[3]);
+        a[4] = fmaf(w[i], nk::bf16_lo(p[i].z), a[4]);
+        a[5] = fmaf(w[i], nk::bf16_hi(p[i].z), a[5]);
+        a[6] = fmaf(w[i], nk::bf16_lo(p[i].w), a[6]);
+        a[7] = fmaf(w[i], nk::bf16_hi(p[i].w), a[7]);
+      }
+    }
+  }
+  uint4 o;
+  o.x = (uint32_t)nk::bf16_rne(a[0]) | ((uint32_t)nk::bf16_rne(a[1]) << 16);
+  o.y = (uint32_t)nk::bf16_rne(a[2]) | ((uint32_t)nk::bf16_rne(a[3]) << 16);
+  o.z = (uint32_t)nk::bf16_rne(a[4]) | ((uint32_t)nk::bf16_rne(a[5]) << 16);
+  o.w = (uint32_t)nk::bf16_rne(a[6]) | ((uint32_t)nk::bf16_rne(a[7]) << 16);
+  *reinterpret_cast<uint4*>(out + (size_t)t * H + n) = o;
+}
+
 // ---------------------------------------------------------------------------
 // Weight preparation: fp32 [groups, n, k] -> e4m3 + fp32 128x128 block scales
 // (scale = max(amax, 1e-10) * 0x3b124925, q = e4m3(w * (1 / scale))); one

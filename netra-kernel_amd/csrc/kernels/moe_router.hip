@@ -320,7 +320,8 @@ NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_gfx950(
   }
   if (tid < Etot) { block_off[tid] = cb + ib - vb; tile_off[tid] = ct + it - vt; }
   if (tid == 0) { block_off[Etot] = total; tile_off[Etot] = total_t; }
-  if (total > cap_blocks) {  // impossible for ids from the top-k kernel; write nothing
+  const uint32_t cap_tiles = (T * Ktot + 15u) / 16u + Etot;
+  if (total > cap_blocks || total_t > cap_tiles) {  // impossible for ids from the top-k kernel; write nothing
     if (tid == 0) { num_valid[0] = 0; num_valid[1] = -1; num_valid[2] = 0; num_valid[3] = 0; }
     return;
   }

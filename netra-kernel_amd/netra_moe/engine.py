@@ -52,6 +52,8 @@ class TensorSpec:
 GEMM_PATHS = ("stream", "tile")
 STREAM_H = (512, 1024, 2048, 4096)   # netra_moe_gate_up_stream_h<H>_gfx950
 STREAM_I = (256, 512, 1024, 2048)    # netra_moe_down_stream_i<I>_gfx950
+TILE_H = (512, 1024, 2048, 4096)     # netra_moe_gate_up_tile_h<H>_gfx950
+TILE_I = (256, 512, 1024)            # netra_moe_down_tile_i<I>_gfx950
 # Persistent stream kernels: 256 CUs x 4 SIMDs x resident waves per SIMD
 # (NK_GATE_UP_WAVES_PER_EU = 2, NK_DOWN_WAVES_PER_EU = 4) / 4 waves per group.
 STREAM_GRID_GATE_UP = 512
@@ -66,11 +68,57 @@ def resolve_path(cfg: MoEConfig, path: str = "auto") -> str:
         raise ValueError(f"unknown GEMM path {path!r}")
     if path == "stream" and (cfg.H not in STREAM_H or cfg.I not in STREAM_I):
         raise ValueError(f"stream path kernels exist for H in {STREAM_H} and I in {STREAM_I}")
+    if path == "tile" and (cfg.H not in TILE_H or cfg.I not in TILE_I):
+        raise ValueError(f"tile path kernels exist for H in {TILE_H} and I in {TILE_I}")
     return path
 
 
-def tensor_table(cfg: MoEConfig, path: str = "auto") -> dict[str, TensorSpec]:
+def xcd_grid(items: int) -> int:
+    """Workgroups for an XCD-major item assignment (nktile::xcd_item): a
+    multiple of 8 covering every item."""
+    return (items + 7) // 8 * 8
+
+
+FRONTS = ("exact", "screen")
+SCREEN_H = (512, 1024, 2048)          # netra_moe_route_screen_h<H>_r<RP>_gfx950
+SCREEN_ROWS = (384, 528)              # router-row capacities RP of the screen kernels
+SCREEN_TOKENS = 16                    # tokens per route_screen workgroup (nkroute::kTok)
+
+
+def resolve_front(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> str:
+    """exact: VALU router (every logit in the contract order) + top-k + one-
+    workgroup sort; screen: bf16-MFMA screen with exact recomputation of the
+    certified candidates + two-kernel sort (the tile path's default)."""
     path = resolve_path(cfg, path)
+    ok = cfg.H in SCREEN_H and cfg.router_rows <= SCREEN_ROWS[-1]
+    if front == "auto":
+        front = "screen" if path == "tile" and ok else "exact"
+    if front not in FRONTS:
+        raise ValueError(f"unknown front end {front!r}")
+    if front == "screen" and not ok:
+        raise ValueError(f"screen front end needs H in {SCREEN_H} and E + S <= {SCREEN_ROWS[-1]}")
+    return front
+
+
+def screen_rows(cfg: MoEConfig) -> int:
+    return next(r for r in SCREEN_ROWS if cfg.router_rows <= r)
+
+
+def screen_lds_bytes(cfg: MoEConfig) -> int:
+    """Static LDS of netra_moe_route_screen (s_x, s_a, s_b, s_cand, s_n, s_ids, s_hist)."""
+    rp = screen_rows(cfg)
+    emax = 384 if rp == 384 else 512
+    return (SCREEN_TOKENS * cfg.H * 2 + 2 * SCREEN_TOKENS * rp * 4 + SCREEN_TOKENS * emax * 2
+            + SCREEN_TOKENS * 4 + SCREEN_TOKENS * 64 * 4 + rp * 4)
+
+
+def screen_groups(cfg: MoEConfig) -> int:
+    return (cfg.T + SCREEN_TOKENS - 1) // SCREEN_TOKENS
+
+
+def tensor_table(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> dict[str, TensorSpec]:
+    path = resolve_path(cfg, path)
+    front = resolve_front(cfg, path, front)
     T, H, I = cfg.T, cfg.H, cfg.I
     specs = [
         TensorSpec("x", "bf16", (T, H), "input"),
@@ -82,7 +130,6 @@ def tensor_table(cfg: MoEConfig, path: str = "auto") -> dict[str, TensorSpec]:
         TensorSpec("w2_scale", "f32", (cfg.Etot, H // 128, I // 128), "weight"),
         TensorSpec("out", "bf16", (T, H), "output"),
         TensorSpec("logits", "bf16", (T, cfg.router_rows), "temporary"),
-        TensorSpec("mask", "u64", (cfg.Etot, cfg.mask_words_per_expert), "temporary"),
         TensorSpec("topk_ids", "i32", (T, cfg.Ktot), "temporary"),
         TensorSpec("topk_weights", "f32", (T, cfg.Ktot), "temporary"),
         TensorSpec("x_q", "e4m3", (T, H), "temporary"),
@@ -93,16 +140,26 @@ def tensor_table(cfg: MoEConfig, path: str = "auto") -> dict[str, TensorSpec]:
         TensorSpec("num_valid", "i32", (4,), "temporary"),
         TensorSpec("expert_counts", "i32", (cfg.Etot,), "temporary"),
     ]
+    if front == "exact":
+        specs.append(TensorSpec("mask", "u64", (cfg.Etot, cfg.mask_words_per_expert), "temporary"))
+    else:
+        specs += [TensorSpec("route_base", "i32", (screen_groups(cfg), cfg.Etot), "temporary"),
+                  TensorSpec("route_rank", "i32", (T * cfg.Ktot,), "temporary")]
     if path == "stream":
         specs.append(TensorSpec("h", "bf16", (cfg.cap_rows, I), "temporary"))
     else:
         specs += [TensorSpec("h_q", "e4m3", (cfg.cap_rows, I), "temporary"),
                   TensorSpec("h_scale", "f32", (cfg.cap_rows, I // 128), "temporary")]
-    specs.append(TensorSpec("partial", "f32", (cfg.routes, H), "temporary"))
+    specs.append(TensorSpec("partial", "f32" if path == "stream" else "bf16", (cfg.routes, H), "temporary"))
     return {s.name: s for s in specs}
 
 
 OP_NAMES = ("router", "topk", "sort", "gate_up", "down", "combine")
+SCREEN_OP_NAMES = ("route", "sort_scan", "sort_scatter", "gate_up", "down", "combine")
+
+
+def op_names(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> tuple[str, ...]:
+    return OP_NAMES if resolve_front(cfg, path, front) == "exact" else SCREEN_OP_NAMES
 ROUTER_H = (512, 1024, 2048, 4096)   # netra_moe_router_h<H>_gfx950
 
 
@@ -111,9 +168,40 @@ def router_tokens(H: int) -> int:
     return 2 if H >= 4096 else 4
 
 
-def operations(cfg: MoEConfig, path: str = "auto") -> list[dict]:
+def _screen_front(cfg: MoEConfig) -> list[dict]:
+    T, H = cfg.T, cfg.H
+    u = lambda v: ("u32", int(v))  # noqa: E731
+    G = screen_groups(cfg)
+    return [
+        dict(name="moe.route", symbol=f"netra_moe_route_screen_h{H}_r{screen_rows(cfg)}_gfx950",
+             grid=(G, 1, 1), block=(512, 1, 1), lds=screen_lds_bytes(cfg), dyn=0,
+             args=["x", "router_w", "router_bias", "logits", "topk_ids", "topk_weights", "x_q",
+                   "x_scale", "route_base", "route_rank", u(T), u(H), u(cfg.E), u(cfg.K), u(cfg.S)],
+             reads=["x", "router_w", "router_bias"],
+             writes=["logits", "topk_ids", "topk_weights", "x_q", "x_scale", "route_base", "route_rank"],
+             refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150",
+                   "runtime/gfx950/routing/decode/qwen36_shared_gate_append_bridge.hip:76-112"]),
+        dict(name="moe.sort_scan", symbol="netra_moe_sort_scan_gfx950",
+             grid=(1, 1, 1), block=(1024, 1, 1), lds=0,
+             dyn=4 * (1024 + 3 * cfg.Etot + 34 + cfg.cap_blocks),
+             args=["route_base", "sorted_ids", "sorted_expert", "tile_map", "num_valid", "expert_counts",
+                   u(T), u(cfg.Ktot), u(cfg.Etot), u(G), u(cfg.cap_blocks)],
+             reads=["route_base"],
+             writes=["route_base", "sorted_ids", "sorted_expert", "tile_map", "num_valid", "expert_counts"],
+             refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]),
+        dict(name="moe.sort_scatter", symbol="netra_moe_sort_scatter_gfx950",
+             grid=((T * cfg.Ktot + 255) // 256, 1, 1), block=(256, 1, 1), lds=0, dyn=0,
+             args=["topk_ids", "route_base", "route_rank", "sorted_ids",
+                   u(T), u(cfg.Ktot), u(cfg.Etot), u(cfg.cap_blocks)],
+             reads=["topk_ids", "route_base", "route_rank"], writes=["sorted_ids"],
+             refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]),
+    ]
+
+
+def operations(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> list[dict]:
     """The six launches of one layer call, in stream order."""
     path = resolve_path(cfg, path)
+    front = resolve_front(cfg, path, front)
     T, H, I = cfg.T, cfg.H, cfg.I
     W = cfg.mask_words_per_expert
     if H not in ROUTER_H:
@@ -144,6 +232,8 @@ def operations(cfg: MoEConfig, path: str = "auto") -> list[dict]:
              writes=["sorted_ids", "sorted_expert", "tile_map", "num_valid", "expert_counts"],
              refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]),
     ]
+    if front == "screen":
+        ops = _screen_front(cfg)
     common = ["sorted_ids", "sorted_expert", "num_valid"]
     if path == "stream":
         ops += [
@@ -165,23 +255,28 @@ def operations(cfg: MoEConfig, path: str = "auto") -> list[dict]:
         ]
     else:
         ops += [
-            dict(name="moe.gate_up", symbol="netra_moe_gate_up_tile_gfx950",
-                 grid=(cfg.cap_blocks, I // 128, 1), block=(256, 1, 1), lds=1536, dyn=0,
+            dict(name="moe.gate_up", symbol=f"netra_moe_gate_up_tile_h{H}_gfx950",
+                 grid=(xcd_grid(cfg.cap_blocks * (I // 128)), 1, 1), block=(256, 1, 1),
+                 lds=2 * 64 * 144 + 64 * (H // 128) * 4 + 64 * 4 + 4 * 64 * 4 + 64 * 4, dyn=0,
                  args=["x_q", "x_scale", "w13", "w13_scale", *common, "h_q", "h_scale",
                        u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
                  reads=["x_q", "x_scale", "w13", "w13_scale", *common], writes=["h_q", "h_scale"],
                  refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/gate_up.inc",
                        "kernels/gfx950/templates/moe/prefill/fused_splitk2/silu_quant.inc"]),
-            dict(name="moe.down", symbol="netra_moe_down_tile_gfx950",
-                 grid=(cfg.cap_blocks, H // 256, 1), block=(256, 1, 1), lds=256, dyn=0,
+            dict(name="moe.down", symbol=f"netra_moe_down_tile_i{I}_gfx950",
+                 grid=(xcd_grid(cfg.cap_blocks * (H // 256)), 1, 1), block=(256, 1, 1),
+                 lds=max(64 * (I + 16), 64 * 528) + 64 * (I // 128) * 4 + 64 * 4, dyn=0,
                  args=["h_q", "h_scale", "w2", "w2_scale", *common, "partial",
                        u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
                  reads=["h_q", "h_scale", "w2", "w2_scale", *common], writes=["partial"],
-                 refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/down_partial.inc"]),
+                 refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/down_partial.inc",
+                       "kernels/gfx950/templates/moe/prefill/route_reduce_splitk2_f16.inc:6-117"]),
         ]
+    combine_sym, combine_cols = ("netra_moe_combine_gfx950", 1024) if path == "stream" else \
+        ("netra_moe_combine_bf16_gfx950", 2048)
     ops.append(
-        dict(name="moe.combine", symbol="netra_moe_combine_gfx950",
-             grid=((H + 1023) // 1024, T, 1), block=(256, 1, 1), lds=0, dyn=0,
+        dict(name="moe.combine", symbol=combine_sym,
+             grid=((H + combine_cols - 1) // combine_cols, T, 1), block=(256, 1, 1), lds=0, dyn=0,
              args=["partial", "topk_weights", "out", u(T), u(H), u(cfg.Ktot)],
              reads=["partial", "topk_weights"], writes=["out"],
              refs=["kernels/gfx950/templates/moe/prefill/route_reduce_splitk2_f16.inc:6-117"]))
@@ -204,18 +299,19 @@ def _dependencies(ops: list[dict]) -> list[list[int]]:
 
 
 def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ...] = (),
-                       hsaco: Path | None = None, path: str = "auto") -> dict:
+                       hsaco: Path | None = None, path: str = "auto", front: str = "auto") -> dict:
     """Write the engine directory; returns the graph recipe (also on disk)."""
     path = resolve_path(cfg, path)
+    front = resolve_front(cfg, path, front)
     directory = Path(directory)
     hsaco = Path(hsaco) if hsaco else paths.hsaco_path()
     if not hsaco.is_file():
         raise FileNotFoundError(f"code object {hsaco} is missing; run the build first")
-    tensors = tensor_table(cfg, path)
+    tensors = tensor_table(cfg, path, front)
     unknown = set(expose) - set(tensors)
     if unknown:
         raise ValueError(f"cannot expose unknown tensors {sorted(unknown)}")
-    ops = operations(cfg, path)
+    ops = operations(cfg, path, front)
     code = hsaco.read_bytes()
     sha = hashlib.sha256(code).hexdigest()
 
@@ -270,6 +366,7 @@ def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ..
         "name": f"netra-moe-{cfg.name}",
         "configuration": cfg.to_dict(),
         "gemm_path": path,
+        "front_end": front,
         "workspace_bytes": workspace_bytes,
         "profiles": [{"name": profile.name, "guards": profile.to_dict()["guards"],
                       "tensor_parallel": profile.tensor_parallel}],
@@ -278,6 +375,7 @@ def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ..
     recipe = {
         "format": "netra-graph-recipe-1",
         "gemm_path": path,
+        "front_end": front,
         "operations": [op["name"] for op in ops],
         "tensors": {n: {"dtype": s.dtype, "shape": list(s.shape), "role": s.role,
                         "bytes": s.nbytes, "storage": "workspace" if n in offsets else "binding"}

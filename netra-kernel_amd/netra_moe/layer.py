@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 from .config import MoEConfig
-from .engine import OP_NAMES, compile_moe_engine, resolve_path, tensor_table
+from .engine import compile_moe_engine, op_names, resolve_front, resolve_path, tensor_table
 from .runtime import Engine, LaunchShape
 
 TORCH_DTYPES = {"bf16": torch.bfloat16, "f32": torch.float32, "e4m3": torch.uint8,
@@ -23,9 +23,10 @@ TORCH_DTYPES = {"bf16": torch.bfloat16, "f32": torch.float32, "e4m3": torch.uint
 WEIGHT_NAMES = ("router_w", "router_bias", "w13", "w13_scale", "w2", "w2_scale")
 
 
-def _engine_cache_dir(cfg: MoEConfig, expose: tuple[str, ...], path: str) -> Path:
+def _engine_cache_dir(cfg: MoEConfig, expose: tuple[str, ...], path: str, front: str) -> Path:
     root = Path(os.environ.get("NETRA_MOE_ENGINE_CACHE", Path(tempfile.gettempdir()) / "netra_moe_engines"))
-    key = hashlib.sha256(json.dumps([cfg.to_dict(), sorted(expose), path], sort_keys=True).encode()).hexdigest()[:16]
+    key = hashlib.sha256(json.dumps([cfg.to_dict(), sorted(expose), path, front],
+                                    sort_keys=True).encode()).hexdigest()[:16]
     return root / f"{cfg.name}-{key}"
 
 
@@ -39,16 +40,20 @@ def check_tensor(name: str, t: torch.Tensor, dtype: str, shape: tuple[int, ...],
 class MoELayer:
     def __init__(self, cfg: MoEConfig, weights: dict[str, torch.Tensor], *, device: int = 0,
                  expose: tuple[str, ...] = (), graph: bool = True, engine_dir: Path | None = None,
-                 path: str = "auto"):
+                 path: str = "auto", front: str = "auto"):
         if not torch.cuda.is_available():
             raise RuntimeError("MoELayer needs a ROCm GPU; there is no CPU fallback")
         self.cfg = cfg
         self.device = torch.device("cuda", device)
         self.expose = tuple(expose)
         self.path = resolve_path(cfg, path)
-        self.engine_dir = Path(engine_dir) if engine_dir else _engine_cache_dir(cfg, self.expose, self.path)
-        self.recipe = compile_moe_engine(cfg, self.engine_dir, expose=self.expose, path=self.path)
-        self.specs = tensor_table(cfg, self.path)
+        self.front = resolve_front(cfg, self.path, front)
+        self.op_names = op_names(cfg, self.path, self.front)
+        self.engine_dir = Path(engine_dir) if engine_dir else _engine_cache_dir(cfg, self.expose, self.path,
+                                                                                self.front)
+        self.recipe = compile_moe_engine(cfg, self.engine_dir, expose=self.expose, path=self.path,
+                                         front=self.front)
+        self.specs = tensor_table(cfg, self.path, self.front)
         with torch.cuda.device(self.device):
             self.engine = Engine(self.engine_dir, device_id=device, graph_capture=graph)
         self.graph = graph
@@ -103,7 +108,7 @@ class MoELayer:
 
     def run_operation(self, index_or_name: int | str) -> None:
         """Launch one operation (direct-launch engines only)."""
-        idx = OP_NAMES.index(index_or_name) if isinstance(index_or_name, str) else int(index_or_name)
+        idx = self.op_names.index(index_or_name) if isinstance(index_or_name, str) else int(index_or_name)
         self.engine.launch_operation(0, idx, self.shape, self._stream())
 
     def close(self) -> None:

@@ -8,17 +8,18 @@ import torch
 
 import oracle
 from netra_moe.config import MoEConfig
-from netra_moe.engine import tensor_table
+from netra_moe.engine import resolve_front, resolve_path
 from netra_moe.layer import MoELayer
 from netra_moe import weights as W
 
-ROUTING = ("logits", "mask", "topk_ids", "topk_weights", "x_q", "x_scale", "sorted_ids",
+ROUTING = ("logits", "topk_ids", "topk_weights", "x_q", "x_scale", "sorted_ids",
            "sorted_expert", "tile_map", "num_valid", "expert_counts", "partial")
 PATH_INTERMEDIATES = {"stream": ("h",), "tile": ("h_q", "h_scale")}
+FRONT_INTERMEDIATES = {"exact": ("mask",), "screen": ()}
 
 
-def intermediates(path: str) -> tuple[str, ...]:
-    return ROUTING + PATH_INTERMEDIATES[path]
+def intermediates(path: str, front: str) -> tuple[str, ...]:
+    return ROUTING + PATH_INTERMEDIATES[path] + FRONT_INTERMEDIATES[front]
 WEIGHT_SEED = 77
 
 
@@ -57,17 +58,18 @@ def make_inputs(cfg: MoEConfig, device: torch.device, weights_on_gpu: bool | Non
 
 
 def run_gpu(cfg: MoEConfig, x: torch.Tensor, gpu_weights: dict, device: torch.device,
-            expose=None, graph: bool = False, repeats: int = 1, path: str = "auto"):
-    layer = MoELayer(cfg, gpu_weights, device=device.index or 0, expose=expose or intermediates(
-        __import__("netra_moe.engine", fromlist=["resolve_path"]).resolve_path(cfg, path)),
-        graph=graph, path=path)
+            expose=None, graph: bool = False, repeats: int = 1, path: str = "auto", front: str = "auto"):
+    path = resolve_path(cfg, path)
+    front = resolve_front(cfg, path, front)
+    layer = MoELayer(cfg, gpu_weights, device=device.index or 0,
+                     expose=expose or intermediates(path, front), graph=graph, path=path, front=front)
     expose = layer.expose
     outs = []
     for _ in range(repeats):
         layer.forward(x)
         torch.cuda.synchronize(device)
         outs.append(bf16_bits(layer.out))
-    res = {"out": outs[-1], "runs": outs}
+    res = {"out": outs[-1], "runs": outs, "path": path, "front": front}
     for name in expose:
         t = layer.buffer(name).detach().cpu()
         if t.dtype == torch.bfloat16:

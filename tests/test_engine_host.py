@@ -14,7 +14,7 @@ import pytest
 
 import netra_moe as nm
 from netra_moe import paths, runtime
-from netra_moe.engine import OP_NAMES, operations
+from netra_moe.engine import OP_NAMES, SCREEN_OP_NAMES, operations
 
 REPO = Path(__file__).resolve().parent.parent
 
@@ -144,9 +144,20 @@ def test_engine_emission_is_deterministic_and_contract_ids_track_shape(tmp_path)
 def test_every_emitted_kernel_symbol_is_in_the_code_object():
     blob = paths.hsaco_path().read_bytes()
     for cfg in nm.BASELINE_CONFIGS.values():
-        for path in ("stream", "tile"):
-            for op in operations(cfg, path):
+        for path, front in (("stream", "exact"), ("tile", "exact"), ("tile", "auto")):
+            for op in operations(cfg, path, front):
                 assert op["symbol"].encode() in blob, op["symbol"]
+
+
+def test_prefill_engines_use_the_screen_front_end(tmp_path):
+    cfg = nm.BASELINE_CONFIGS["prefill_t4096"]
+    nm.compile_moe_engine(cfg, tmp_path / "p")
+    doc = json.loads((tmp_path / "p" / "engine.json").read_text())
+    assert doc["front_end"] == "screen" and doc["gemm_path"] == "tile"
+    assert [op["name"] for op in doc["operations"]] == [f"moe.{n}" for n in SCREEN_OP_NAMES]
+    assert nm.manifest_check(tmp_path / "p")[0] == nm.Status.OK
+    route = doc["operations"][0]
+    assert route["launch"]["grid"] == [256, 1, 1] and route["launch"]["lds_bytes"] <= 160 * 1024
 
 
 def test_profiles_select_exact_shapes_and_refuse_neighbours():

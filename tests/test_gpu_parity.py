@@ -1,7 +1,9 @@
 """HIP path vs the CPU oracle on identical seeded inputs, all five configs.
 
-Bars: router logits, top-k ids and weights, the 1x128 input quant, expert
-counts, the sorted permutation and the expert-block table are bit-exact; the
+Bars: router logits (every logit on the exact front end; the selected and
+shared-gate logits on the screen front end, the others within the screen's
+bound), top-k ids and weights, the 1x128 input quant, expert counts, the
+sorted permutation and the expert-block table are bit-exact; the
 layer output is within max|y - y_ref| / max|y_ref| <= 2e-2 of the fp64-
 accumulated oracle (checked on every token for T <= 64 and on a seeded sample
 of tokens above that). The FP8 intermediate h must agree code-for-code up to
@@ -34,14 +36,32 @@ def case(request):
           flush=True)
     x, gpu_w, host = make_inputs(cfg, DEV)
     got = run_gpu(cfg, x, gpu_w, DEV, repeats=2, path=path)
-    got["path"] = path
+    print(f"[parity] front end: {got['front']}", flush=True)
     ref = oracle_routing(cfg, host)
     return cfg, host, got, ref
 
 
-def test_router_logits_bit_exact(case):
+def test_router_logits(case):
     cfg, host, got, ref = case
-    np.testing.assert_array_equal(got["logits"], ref["logits"])
+    if got["front"] == "exact":
+        np.testing.assert_array_equal(got["logits"], ref["logits"])
+        return
+    # screen front end: the logits that decide top-k weights and the shared gate
+    # are the exact contract values ...
+    tok = np.arange(cfg.T)[:, None]
+    sel = ref["topk_ids"]
+    np.testing.assert_array_equal(got["logits"][tok, sel], ref["logits"][tok, sel])
+    # ... the others are the bf16-rounded MFMA screen: within one bf16 step of
+    # each plus the screen's margin 2^-10 * sum |x w|
+    x = oracle.f32_from_bf16(host["x"]).astype(np.float32)
+    w = oracle.f32_from_bf16(host["router_w"]).astype(np.float32)
+    s_abs = np.abs(x) @ np.abs(w).T
+    g = oracle.f32_from_bf16(got["logits"]).astype(np.float64)
+    r = oracle.f32_from_bf16(ref["logits"]).astype(np.float64)
+    bound = 2.0 ** -8 * np.maximum(np.abs(g), np.abs(r)) + 2.0 ** -10 * s_abs
+    worst = float(np.max(np.abs(g - r) - bound))
+    print(f"[parity] {cfg.name} screen logits: exact share {np.mean(g == r):.3f}, worst excess {worst:.2e}")
+    assert worst <= 0.0
 
 
 def test_topk_ids_and_weights_bit_exact(case):

@@ -210,6 +210,23 @@ extern "C" netra_status_t netra_engine_create(const char* directory,
     }
     err = hipModuleGetFunction(&functions[i], it->second, spec.kernel_symbol.c_str());
     if (err != hipSuccess) { release(e); delete e; return NETRA_STATUS_MANIFEST; }
+    // The launch must fit what the code object was compiled for: a block
+    // beyond the kernel's flat work-group bound, or static + dynamic LDS beyond
+    // the CU's 160 KiB, is a manifest error here rather than a failed launch.
+    int max_threads = 0, static_lds = 0;
+    if (hipFuncGetAttribute(&max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, functions[i]) != hipSuccess ||
+        hipFuncGetAttribute(&static_lds, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, functions[i]) != hipSuccess) {
+      release(e);
+      delete e;
+      return NETRA_STATUS_HIP;
+    }
+    const uint64_t threads = static_cast<uint64_t>(spec.block[0]) * spec.block[1] * spec.block[2];
+    if (threads > static_cast<uint64_t>(max_threads) ||
+        static_cast<uint64_t>(static_lds) + spec.dynamic_lds_bytes > 160u * 1024u) {
+      release(e);
+      delete e;
+      return NETRA_STATUS_MANIFEST;
+    }
   }
 
   e->profiles.resize(manifest.profiles.size());

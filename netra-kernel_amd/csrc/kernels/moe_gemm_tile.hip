@@ -3,8 +3,8 @@
 // gate/up epilogue, bf16 route partials out of the down GEMM.
 //
 // Both kernels stage the block's activation rows in LDS once per workgroup
-// (the four waves share them), prefetch the next 128-K block of weight
-// operands while the current one is multiplied, and synchronise through LDS-only barriers so the weight
+// (the waves share them), keep several 128-K blocks of weight operands in
+// flight per wave, and synchronise through LDS-only barriers so the weight
 // prefetch is never drained. Work items are assigned XCD-major: the hardware
 // hands consecutive workgroup ids to the eight XCDs in turn, so workgroup i
 // takes item (i % 8) * per + i / 8 and each XCD walks a contiguous range of
@@ -49,13 +49,16 @@ __device__ __forceinline__ v8i lds_fp8x32(const uint8_t* p) {
 // (reference: kernels/gfx950/templates/moe/decode/gate_up_mfma.inc:12-161 and
 // silu_quant.inc:16-236; oracle tools/benchmark/export_qwen36_moe_stage1_capture.py:80-97).
 //
-// Item (b, ng): expert block b, h columns [128 ng, 128 ng + 128). Wave w owns
-// h columns 32 w .. 32 w + 31: W13 rows n and n + 16 (gate) and I + n,
-// I + n + 16 (up), against the block's non-empty 16-row tiles. Per 128-K
-// block: acc += (w_s * a_s) * mfma. Epilogue: h = bf16(silu(g) * u), amax over
-// the 128-column group (lanes, then waves through LDS), scale = max(amax,
+// Item (b, ng): expert block b, h columns [128 ng, 128 ng + 128), WAVES waves.
+// Wave w owns the CPW = 128 / WAVES h columns n = 128 ng + CPW w .. +CPW-1:
+// CPW / 16 W13 tiles of gate rows and as many of up rows (I + n), against the
+// block's non-empty 16-row tiles. Weight operands are prefetched AHEAD 128-K
+// blocks ahead (a ring in registers, raw buffer loads with scalar offsets),
+// activation rows two blocks ahead of their LDS store. Per 128-K block:
+// acc += (w_s * a_s) * mfma. Epilogue: h = bf16(silu(g) * u), amax over the
+// 128-column group (lanes, then the waves through LDS), scale = max(amax,
 // 1e-10) * 0x3b124925, q = e4m3(h * (1 / scale)).
-template <uint32_t KB>  // H / 128
+template <uint32_t KB, uint32_t WAVES, uint32_t AHEAD>  // KB = H / 128
 __device__ __forceinline__ void gate_up_tile(
     const uint8_t* __restrict__ xq, const float* __restrict__ xs, const uint8_t* __restrict__ w13,
     const float* __restrict__ w13s, const int32_t* __restrict__ sorted_ids,
@@ -63,13 +66,21 @@ __device__ __forceinline__ void gate_up_tile(
     uint8_t* __restrict__ hq, float* __restrict__ hs, uint32_t T, uint32_t I, uint32_t Ktot,
     uint32_t Etot) {
   constexpr uint32_t H = 128u * KB;
-  constexpr uint32_t kStride = 144;  // LDS bytes per A row (128 + 16: rotates banks across rows)
+  constexpr uint32_t kThreads = 64u * WAVES;
+  constexpr uint32_t CPW = 128u / WAVES;  // h columns per wave
+  constexpr uint32_t CT = CPW / 16u;      // 16-column tiles per wave (gate; up likewise)
+  constexpr uint32_t APT = 8u / WAVES;    // A uint4 per thread per 128-K block
+  constexpr uint32_t kStride = 144;       // LDS bytes per A row (128 + 16: rotates banks across rows)
+  constexpr uint32_t kRing = AHEAD + 1u;
+  static_assert(WAVES == 4 || WAVES == 8, "128 columns over 4 or 8 waves");
   __shared__ __align__(16) uint8_t s_a[2][kRows * kStride];
-  __shared__ float s_as[kRows * KB];
+  __shared__ float s_sg[kRows * KB];  // w_s(gate block, kb) * a_s(row, kb)
+  __shared__ float s_su[kRows * KB];  // w_s(up block, kb) * a_s(row, kb)
   __shared__ int32_t s_tok[kRows];
-  __shared__ float s_amax[4][kRows];
+  __shared__ float s_amax[WAVES][kRows];
   __shared__ float s_scale[kRows];
-  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));  // uniform: scalar addressing
   const uint32_t NG = I / 128u;
   uint32_t item;
   if (!xcd_item(blockIdx.x, ((uint32_t)num_valid[0] / kRows) * NG, item)) return;
@@ -84,56 +95,70 @@ __device__ __forceinline__ void gate_up_tile(
   __syncthreads();
   const uint32_t nvalid = (uint32_t)__popcll(__ballot(s_tok[lane] >= 0));
   const uint32_t ntiles = (nvalid + 15u) >> 4;
-  for (uint32_t i = tid; i < kRows * KB; i += 256u) {
-    const int32_t tk = s_tok[i / KB];
-    s_as[i] = tk >= 0 ? xs[(size_t)tk * KB + (i % KB)] : 0.0f;
-  }
-  // A loader: thread moves 16 bytes of rows (tid >> 3) and 32 + (tid >> 3)
-  const uint32_t ar0 = tid >> 3, ac = (tid & 7u) * 16u;
-  const int32_t tk0 = s_tok[ar0], tk1 = s_tok[ar0 + 32u];
-  const uint8_t* asrc0 = xq + (size_t)(tk0 < 0 ? 0 : tk0) * H + ac;
-  const uint8_t* asrc1 = xq + (size_t)(tk1 < 0 ? 0 : tk1) * H + ac;
+  // A loader: thread moves APT x 16 bytes of the 64 x 128 block per step
+  // (pieces tid and, with 4 waves, tid + 256; explicit variables, not arrays,
+  // so they stay in registers)
+  const uint32_t ar0 = tid >> 3, ar1 = (tid + kThreads) >> 3, ac = (tid & 7u) * 16u;
+  const int32_t tka0 = s_tok[ar0], tka1 = APT > 1 ? s_tok[ar1 & 63u] : 0;
+  const uint8_t* asrc0 = xq + (size_t)(tka0 < 0 ? 0 : tka0) * H + ac;
+  const uint8_t* asrc1 = xq + (size_t)(tka1 < 0 ? 0 : tka1) * H + ac;
   uint8_t* adst0 = &s_a[0][ar0 * kStride + ac];
-  uint8_t* adst1 = &s_a[0][(ar0 + 32u) * kStride + ac];
+  uint8_t* adst1 = &s_a[0][(ar1 & 63u) * kStride + ac];
 
-  const uint8_t* we = w13 + (size_t)e * 2u * I * H;
+  const uint32_t n0 = ng * 128u + wave * CPW;
+  // gate / up tile strips: CT row tiles x KB tiles of 2 KiB, contiguous in the tile16x128 layout
+  const uint8_t* w13e = w13 + (size_t)e * 2u * I * H;
+  const __amdgpu_buffer_rsrc_t wg = nk::buffer_rsrc(nk::tile_base(w13e, n0 >> 4, 0, KB), CT * KB * 2048u);
+  const __amdgpu_buffer_rsrc_t wu = nk::buffer_rsrc(nk::tile_base(w13e, (I + n0) >> 4, 0, KB), CT * KB * 2048u);
   const float* wse = w13s + (size_t)e * (2u * I / 128u) * KB;
-  const uint32_t n0 = ng * 128u + wave * 32u;
-  const uint32_t ntile[4] = {n0 >> 4, (n0 >> 4) + 1u, (I + n0) >> 4, ((I + n0) >> 4) + 1u};
-  const float* wsg = wse + (size_t)ng * KB;           // gate rows' 128-row block
+  const float* wsg = wse + (size_t)ng * KB;               // gate rows' 128-row block
   const float* wsu = wse + (size_t)(I / 128u + ng) * KB;  // up rows' block
-  v8i bq[2][4];
-  auto load_b = [&](uint32_t kb, v8i (&dst)[4]) __attribute__((always_inline)) {
-#pragma unroll
-    for (uint32_t c = 0; c < 4; ++c) dst[c] = nk::load_tile_operand(nk::tile_base(we, ntile[c], kb, KB), lane);
-  };
+  for (uint32_t i = tid; i < kRows * KB; i += kThreads) {
+    const int32_t tk = s_tok[i / KB];
+    const float as = tk >= 0 ? xs[(size_t)tk * KB + (i % KB)] : 0.0f;
+    s_sg[i] = wsg[i % KB] * as;
+    s_su[i] = wsu[i % KB] * as;
+  }
+  const uint32_t g = lane >> 4;
 
-  v4f acc[4][4];
+  v4f acc[4][2 * CT];
 #pragma unroll
   for (uint32_t rt = 0; rt < 4; ++rt)
 #pragma unroll
-    for (uint32_t c = 0; c < 4; ++c) acc[rt][c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  const uint32_t g = lane >> 4;
+    for (uint32_t c = 0; c < 2 * CT; ++c) acc[rt][c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // The K loop is instantiated per number of non-empty row tiles so it has no
-  // branches: the compiler then keeps every load where it is issued (it sinks
-  // loads into the branch that uses them otherwise).
+  // K loop, instantiated per number of non-empty row tiles so it has no
+  // branches (the compiler sinks loads into the branch that uses them
+  // otherwise, which would serialise them with their use).
   auto kloop = [&](auto ntc) __attribute__((always_inline)) {
     constexpr uint32_t NT = decltype(ntc)::value;
-    uint4 a0 = *reinterpret_cast<const uint4*>(asrc0);
-    uint4 a1 = *reinterpret_cast<const uint4*>(asrc1);
-    load_b(0, bq[0]);
-    *reinterpret_cast<uint4*>(adst0) = a0;
-    *reinterpret_cast<uint4*>(adst1) = a1;
+    v8i bq[kRing][2 * CT];
+    uint4 e0, e1, o0, o1;  // A pieces (0 / 1) of the even / odd 128-K block in flight
+    auto load_b = [&](uint32_t kb, v8i (&dst)[2 * CT]) __attribute__((always_inline)) {
+#pragma unroll
+      for (uint32_t c = 0; c < CT; ++c) {
+        dst[c] = nk::load_tile_operand(wg, (c * KB + kb) * 2048u, lane);
+        dst[CT + c] = nk::load_tile_operand(wu, (c * KB + kb) * 2048u, lane);
+      }
+    };
+#pragma unroll
+    for (uint32_t k = 0; k < AHEAD && k < KB; ++k) load_b(k, bq[k]);
+    e0 = *reinterpret_cast<const uint4*>(asrc0);
+    if (APT > 1) e1 = *reinterpret_cast<const uint4*>(asrc1);
     if (KB > 1) {
-      a0 = *reinterpret_cast<const uint4*>(asrc0 + 128u);
-      a1 = *reinterpret_cast<const uint4*>(asrc1 + 128u);
+      o0 = *reinterpret_cast<const uint4*>(asrc0 + 128u);
+      if (APT > 1) o1 = *reinterpret_cast<const uint4*>(asrc1 + 128u);
+    }
+    *reinterpret_cast<uint4*>(adst0) = e0;
+    if (APT > 1) *reinterpret_cast<uint4*>(adst1) = e1;
+    if (KB > 2) {
+      e0 = *reinterpret_cast<const uint4*>(asrc0 + 256u);
+      if (APT > 1) e1 = *reinterpret_cast<const uint4*>(asrc1 + 256u);
     }
     lds_barrier();
 #pragma unroll
     for (uint32_t kb = 0; kb < KB; ++kb) {
-      if (kb + 1u < KB) load_b(kb + 1u, bq[(kb + 1u) & 1u]);
-      const float sg = wsg[kb], su = wsu[kb];
+      if (kb + AHEAD < KB) load_b(kb + AHEAD, bq[(kb + AHEAD) % kRing]);
       const uint8_t* abuf = s_a[kb & 1u];
 #pragma unroll
       for (uint32_t rt = 0; rt < NT; ++rt) {
@@ -141,24 +166,25 @@ __device__ __forceinline__ void gate_up_tile(
         float scg[4], scu[4];
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
-          const float as = s_as[(rt * 16u + g * 4u + j) * KB + kb];
-          scg[j] = sg * as;
-          scu[j] = su * as;
+          scg[j] = s_sg[(rt * 16u + g * 4u + j) * KB + kb];
+          scu[j] = s_su[(rt * 16u + g * 4u + j) * KB + kb];
         }
 #pragma unroll
-        for (uint32_t c = 0; c < 4; ++c) {
-          const v4f d = nk::mfma_e4m3_16x16x128(af, bq[kb & 1u][c]);
+        for (uint32_t c = 0; c < 2 * CT; ++c) {
+          const v4f d = nk::mfma_e4m3_16x16x128(af, bq[kb % kRing][c]);
 #pragma unroll
-          for (uint32_t j = 0; j < 4; ++j) acc[rt][c][j] = fmaf(c < 2 ? scg[j] : scu[j], d[j], acc[rt][c][j]);
+          for (uint32_t j = 0; j < 4; ++j) acc[rt][c][j] = fmaf(c < CT ? scg[j] : scu[j], d[j], acc[rt][c][j]);
         }
       }
-      if (kb + 1u < KB) {
+      if (kb + 1u < KB) {  // A(kb + 1) -> LDS, A(kb + 3) requested
         constexpr uint32_t kBuf = sizeof(s_a[0]);
-        *reinterpret_cast<uint4*>(adst0 + ((kb + 1u) & 1u) * kBuf) = a0;
-        *reinterpret_cast<uint4*>(adst1 + ((kb + 1u) & 1u) * kBuf) = a1;
-        if (kb + 2u < KB) {
-          a0 = *reinterpret_cast<const uint4*>(asrc0 + (kb + 2u) * 128u);
-          a1 = *reinterpret_cast<const uint4*>(asrc1 + (kb + 2u) * 128u);
+        uint4& q0 = ((kb + 1u) & 1u) ? o0 : e0;
+        uint4& q1 = ((kb + 1u) & 1u) ? o1 : e1;
+        *reinterpret_cast<uint4*>(adst0 + ((kb + 1u) & 1u) * kBuf) = q0;
+        if (APT > 1) *reinterpret_cast<uint4*>(adst1 + ((kb + 1u) & 1u) * kBuf) = q1;
+        if (kb + 3u < KB) {
+          q0 = *reinterpret_cast<const uint4*>(asrc0 + (kb + 3u) * 128u);
+          if (APT > 1) q1 = *reinterpret_cast<const uint4*>(asrc1 + (kb + 3u) * 128u);
         }
       }
       lds_barrier();
@@ -171,16 +197,16 @@ __device__ __forceinline__ void gate_up_tile(
     default: kloop(std::integral_constant<uint32_t, 4>{}); break;
   }
 
-  // Epilogue: h = bf16(silu(g) * u); per-row amax over this wave's 32 columns.
-  float h[4][2][4];
+  // Epilogue: h = bf16(silu(g) * u); per-row amax over this wave's columns.
+  float h[4][CT][4];
 #pragma unroll
   for (uint32_t rt = 0; rt < 4; ++rt) {
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j) {
       float m = 0.0f;
 #pragma unroll
-      for (uint32_t c = 0; c < 2; ++c) {
-        const float v = nk::bf16_f32(nk::bf16_rne(nk::silu(acc[rt][c][j]) * acc[rt][c + 2][j]));
+      for (uint32_t c = 0; c < CT; ++c) {
+        const float v = nk::bf16_f32(nk::bf16_rne(nk::silu(acc[rt][c][j]) * acc[rt][CT + c][j]));
         h[rt][c][j] = v;
         m = fmaxf(m, fabsf(v));
       }
@@ -195,7 +221,7 @@ __device__ __forceinline__ void gate_up_tile(
   if (tid < kRows) {
     float m = nk::kAmaxFloor;
 #pragma unroll
-    for (uint32_t w = 0; w < 4; ++w) m = fmaxf(m, s_amax[w][tid]);
+    for (uint32_t w = 0; w < WAVES; ++w) m = fmaxf(m, s_amax[w][tid]);
     const float scale = m * nk::inv_e4m3_max();
     s_scale[tid] = scale;
     if (tid < nvalid) hs[(size_t)(b * kRows + tid) * (I / 128u) + ng] = scale;
@@ -208,10 +234,9 @@ __device__ __forceinline__ void gate_up_tile(
       const uint32_t row = rt * 16u + g * 4u + j;
       if (row < nvalid) {
         const float inv = 1.0f / s_scale[row];
-        const uint32_t q = nk::e4m3x4(h[rt][0][j] * inv, h[rt][1][j] * inv, 0.0f, 0.0f);
         uint8_t* dst = hq + (size_t)(b * kRows + row) * I + n0 + (lane & 15u);
-        dst[0] = (uint8_t)q;
-        dst[16] = (uint8_t)(q >> 8);
+#pragma unroll
+        for (uint32_t c = 0; c < CT; ++c) dst[16u * c] = (uint8_t)nk::e4m3x4(h[rt][c][j] * inv, 0.0f, 0.0f, 0.0f);
       }
     }
   }
@@ -223,11 +248,12 @@ __device__ __forceinline__ void gate_up_tile(
 // moe/prefill/route_reduce_splitk2_f16.inc:6-117; oracle
 // tools/benchmark/export_qwen36_moe_stage2_capture.py:90-110).
 //
-// Item (b, nb): expert block b, output columns [256 nb, 256 nb + 256). The
-// block's 64 h rows (contiguous in sorted order, all of K) are staged in LDS
-// once; wave w owns 64 columns (four 16-column tiles). Each valid row's
-// result, rounded to bf16, goes to partial[route], route = token * Ktot +
-// slot, through an LDS transpose so each row is written as 512 contiguous
+// Item (b, nb), 256 threads: expert block b, output columns [128 nb, 128 nb
+// + 128). The block's 64 h rows (contiguous in sorted order, all of K) are
+// staged in LDS once; wave w owns 32 columns (two 16-column tiles), all of
+// whose weight operands are requested before the first multiply. Each valid
+// row's result, rounded to bf16, goes to partial[route], route = token * Ktot
+// + slot, through an LDS transpose so each row is written as 256 contiguous
 // bytes; combine applies the top-k weights in slot order.
 template <uint32_t KB>  // I / 128
 __device__ __forceinline__ void down_tile(
@@ -237,13 +263,14 @@ __device__ __forceinline__ void down_tile(
     uint16_t* __restrict__ partial, uint32_t T, uint32_t H, uint32_t Ktot, uint32_t Etot) {
   constexpr uint32_t I = 128u * KB;
   constexpr uint32_t kStride = I + 16u;   // LDS bytes per A row
-  constexpr uint32_t kOut = 512u + 16u;   // LDS bytes per output row (256 bf16 + pad)
+  constexpr uint32_t kOut = 256u + 16u;   // LDS bytes per output row (128 bf16 + pad)
   constexpr uint32_t kLds = (kRows * kStride > kRows * kOut) ? kRows * kStride : kRows * kOut;
   __shared__ __align__(16) uint8_t s_buf[kLds];
-  __shared__ float s_as[kRows * KB];
+  __shared__ float s_as[kRows * KB];  // w_s(kb) * h_s(row, kb)
   __shared__ int32_t s_route[kRows];
-  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
-  const uint32_t NB = H / 256u;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));  // uniform: scalar addressing
+  const uint32_t NB = H / 128u;
   uint32_t item;
   if (!xcd_item(blockIdx.x, ((uint32_t)num_valid[0] / kRows) * NB, item)) return;
   const uint32_t b = item / NB, nb = item - b * NB;
@@ -254,28 +281,27 @@ __device__ __forceinline__ void down_tile(
     const uint32_t t = (uint32_t)id & 0xffffffu, slot = (uint32_t)id >> 24;
     s_route[tid] = (t < T && slot < Ktot) ? (int32_t)(t * Ktot + slot) : -1;
   }
+  const uint32_t n0 = nb * 128u + wave * 32u;
+  // row tiles n0 / 16 and n0 / 16 + 1: 2 KB tiles of 2 KiB, contiguous
+  const __amdgpu_buffer_rsrc_t wt =
+      nk::buffer_rsrc(nk::tile_base(w2 + (size_t)e * H * I, n0 >> 4, 0, KB), 2u * KB * 2048u);
+  v8i bq[KB][2];
+#pragma unroll
+  for (uint32_t kb = 0; kb < KB; ++kb) {
+    bq[kb][0] = nk::load_tile_operand(wt, kb * 2048u, lane);
+    bq[kb][1] = nk::load_tile_operand(wt, (KB + kb) * 2048u, lane);
+  }
   // all of A (64 rows x I bytes, contiguous) and its scales
   constexpr uint32_t kA16 = kRows * I / 16u / 256u;  // uint4 per thread
   uint4 areg[kA16];
   const uint8_t* ablk = hq + (size_t)b * kRows * I;
 #pragma unroll
   for (uint32_t p = 0; p < kA16; ++p) areg[p] = reinterpret_cast<const uint4*>(ablk)[p * 256u + tid];
-  for (uint32_t i = tid; i < kRows * KB; i += 256u) s_as[i] = hs[(size_t)b * kRows * KB + i];
-
-  const uint8_t* we = w2 + (size_t)e * H * I;
-  const float* wse = w2s + (size_t)e * (H / 128u) * KB;
-  const uint32_t n0 = nb * 256u + wave * 64u;
-  const float* wsn = wse + (size_t)(n0 >> 7) * KB;  // the wave's 64 columns lie in one 128-row block
-  v8i bq[2][4];
-  auto load_b = [&](uint32_t kb, v8i (&dst)[4]) __attribute__((always_inline)) {
-#pragma unroll
-    for (uint32_t c = 0; c < 4; ++c) dst[c] = nk::load_tile_operand(nk::tile_base(we, (n0 >> 4) + c, kb, KB), lane);
-  };
-  load_b(0, bq[0]);
-  if (KB > 1) load_b(1, bq[1]);
+  const float* wsn = w2s + ((size_t)e * (H / 128u) + (nb * 128u >> 7)) * KB;  // the item's 128-row block
+  for (uint32_t i = tid; i < kRows * KB; i += 256u) s_as[i] = wsn[i % KB] * hs[(size_t)b * kRows * KB + i];
 #pragma unroll
   for (uint32_t p = 0; p < kA16; ++p) {
-    const uint32_t idx = p * 256u + tid;            // uint4 index in the block
+    const uint32_t idx = p * 256u + tid;  // uint4 index in the block
     const uint32_t row = idx / (I / 16u), c16 = idx - row * (I / 16u);
     *reinterpret_cast<uint4*>(&s_buf[row * kStride + c16 * 16u]) = areg[p];
   }
@@ -284,30 +310,25 @@ __device__ __forceinline__ void down_tile(
   const uint32_t ntiles = (nvalid + 15u) >> 4;
   const uint32_t g = lane >> 4;
 
-  v4f acc[4][4];
+  v4f acc[4][2];
 #pragma unroll
-  for (uint32_t rt = 0; rt < 4; ++rt)
-#pragma unroll
-    for (uint32_t c = 0; c < 4; ++c) acc[rt][c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  auto kloop = [&](auto ntc) __attribute__((always_inline)) {  // per tile count, branch-free (see gate_up_tile)
+  for (uint32_t rt = 0; rt < 4; ++rt) acc[rt][0] = acc[rt][1] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  auto kloop = [&](auto ntc) __attribute__((always_inline)) {  // branch-free per tile count
     constexpr uint32_t NT = decltype(ntc)::value;
 #pragma unroll
     for (uint32_t kb = 0; kb < KB; ++kb) {
-      const float sw = wsn[kb];
 #pragma unroll
       for (uint32_t rt = 0; rt < NT; ++rt) {
         const v8i af = lds_fp8x32(&s_buf[(rt * 16u + (lane & 15u)) * kStride + kb * 128u + g * 32u]);
-        float sc[4];
+        const v4f d0 = nk::mfma_e4m3_16x16x128(af, bq[kb][0]);
+        const v4f d1 = nk::mfma_e4m3_16x16x128(af, bq[kb][1]);
 #pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) sc[j] = sw * s_as[(rt * 16u + g * 4u + j) * KB + kb];
-#pragma unroll
-        for (uint32_t c = 0; c < 4; ++c) {
-          const v4f d = nk::mfma_e4m3_16x16x128(af, bq[kb & 1u][c]);
-#pragma unroll
-          for (uint32_t j = 0; j < 4; ++j) acc[rt][c][j] = fmaf(sc[j], d[j], acc[rt][c][j]);
+        for (uint32_t j = 0; j < 4; ++j) {
+          const float sc = s_as[(rt * 16u + g * 4u + j) * KB + kb];
+          acc[rt][0][j] = fmaf(sc, d0[j], acc[rt][0][j]);
+          acc[rt][1][j] = fmaf(sc, d1[j], acc[rt][1][j]);
         }
       }
-      if (kb + 2u < KB) load_b(kb + 2u, bq[kb & 1u]);
     }
   };
   switch (ntiles) {
@@ -323,40 +344,52 @@ __device__ __forceinline__ void down_tile(
     for (uint32_t j = 0; j < 4; ++j) {
       const uint32_t row = rt * 16u + g * 4u + j;
 #pragma unroll
-      for (uint32_t c = 0; c < 4; ++c)
-        *reinterpret_cast<uint16_t*>(&s_buf[row * kOut + (wave * 64u + c * 16u + (lane & 15u)) * 2u]) =
+      for (uint32_t c = 0; c < 2; ++c)
+        *reinterpret_cast<uint16_t*>(&s_buf[row * kOut + (wave * 32u + c * 16u + (lane & 15u)) * 2u]) =
             nk::bf16_rne(acc[rt][c][j]);
     }
   __syncthreads();
-  // 64 rows x 512 bytes: 32 uint4 per row, 8 per thread
+  // 64 rows x 256 bytes: 16 uint4 per row, 4 per thread
 #pragma unroll
-  for (uint32_t p = 0; p < 8u; ++p) {
+  for (uint32_t p = 0; p < 4u; ++p) {
     const uint32_t idx = p * 256u + tid;
-    const uint32_t row = idx >> 5, c16 = idx & 31u;
+    const uint32_t row = idx >> 4, c16 = idx & 15u;
     const int32_t route = s_route[row];
     if (row < nvalid && route >= 0)
-      *reinterpret_cast<uint4*>(partial + (size_t)route * H + nb * 256u + c16 * 8u) =
+      *reinterpret_cast<uint4*>(partial + (size_t)route * H + nb * 128u + c16 * 8u) =
           *reinterpret_cast<const uint4*>(&s_buf[row * kOut + c16 * 16u]);
   }
 }
 
 }  // namespace nktile
 
-#define NK_GATE_UP_TILE(HV)                                                                        \
-  NK_KERNEL __launch_bounds__(256) void netra_moe_gate_up_tile_h##HV##_gfx950(                     \
+// Gate/up tile kernels: 4 waves x 32 columns, one weight block in flight
+// ahead (the variant measured fastest at prefill shapes;
+// the _w / _a instantiations for H = 2048 are the alternatives kept for
+// tuning runs).
+#define NK_GATE_UP_TILE_V(NAME, HV, WAVES, AHEAD, ATTR)                                            \
+  NK_KERNEL __launch_bounds__(64 * WAVES) ATTR void NAME(                                          \
       const uint8_t* __restrict__ xq, const float* __restrict__ xs, const uint8_t* __restrict__ w13, \
       const float* __restrict__ w13s, const int32_t* __restrict__ sorted_ids,                      \
       const int32_t* __restrict__ sorted_expert, const int32_t* __restrict__ num_valid,            \
       uint8_t* __restrict__ hq, float* __restrict__ hs, uint32_t T, uint32_t H, uint32_t I,        \
       uint32_t Ktot, uint32_t Etot) {                                                              \
     (void)H;                                                                                       \
-    nktile::gate_up_tile<HV / 128>(xq, xs, w13, w13s, sorted_ids, sorted_expert, num_valid, hq,    \
-                                   hs, T, I, Ktot, Etot);                                          \
+    nktile::gate_up_tile<HV / 128, WAVES, AHEAD>(xq, xs, w13, w13s, sorted_ids, sorted_expert,     \
+                                                 num_valid, hq, hs, T, I, Ktot, Etot);             \
   }
-NK_GATE_UP_TILE(512)
-NK_GATE_UP_TILE(1024)
-NK_GATE_UP_TILE(2048)
-NK_GATE_UP_TILE(4096)
+#define NK_NOATTR
+#define NK_OCC4 __attribute__((amdgpu_waves_per_eu(4)))
+NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h512_gfx950, 512, 4, 1, NK_NOATTR)
+NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h1024_gfx950, 1024, 4, 1, NK_NOATTR)
+NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h2048_gfx950, 2048, 4, 1, NK_NOATTR)
+NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h4096_gfx950, 4096, 4, 1, NK_NOATTR)
+NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h2048_w4_a2_gfx950, 2048, 4, 2, NK_NOATTR)
+NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h2048_w8_a1_gfx950, 2048, 8, 1, NK_NOATTR)
+NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h2048_w4_a3_gfx950, 2048, 4, 3, NK_NOATTR)
+NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h2048_w8_a4_gfx950, 2048, 8, 4, NK_NOATTR)
+NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h2048_w8_a2_gfx950, 2048, 8, 2, __attribute__((amdgpu_waves_per_eu(4))))
+NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h2048_w8_a1_o4_gfx950, 2048, 8, 1, NK_OCC4)
 
 #define NK_DOWN_TILE(IV)                                                                           \
   NK_KERNEL __launch_bounds__(256)                                                                \

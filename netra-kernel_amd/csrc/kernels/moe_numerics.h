@@ -118,6 +118,24 @@ __device__ __forceinline__ v8i load_tile_operand(const uint8_t* tile, uint32_t l
   return r;
 }
 
+// The same operand through a raw buffer resource (SGPR base, per-lane offset
+// lane * 16 and a uniform scalar offset per tile): a run of tiles costs one
+// address VGPR instead of a 64-bit address per load. Loads past `bytes`
+// return zeros.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ v8i load_tile_operand(__amdgpu_buffer_rsrc_t r, uint32_t tile_offset,
+                                                 uint32_t lane) {
+  const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(lane * 16u), (int)tile_offset, 0);
+  const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(lane * 16u + 1024u), (int)tile_offset, 0);
+  v8i v;
+  v[0] = (int)lo.x; v[1] = (int)lo.y; v[2] = (int)lo.z; v[3] = (int)lo.w;
+  v[4] = (int)hi.x; v[5] = (int)hi.y; v[6] = (int)hi.z; v[7] = (int)hi.w;
+  return v;
+}
+
 // Tiled activation layout for h (bf16, [rows, I]) between the decode GEMMs:
 // per 16-row tile and 128-column block, lane l's 32 values (row l & 15,
 // columns (l >> 4) * 32 .. +31) form four 16-byte pieces; piece q of every

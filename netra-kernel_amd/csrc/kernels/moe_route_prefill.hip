@@ -1,8 +1,12 @@
-// Routing front end for large token counts (prefill, T > 256), three kernels:
-//   route_screen  bf16-MFMA screen of the router logits, certified candidate
-//                 sets, exact contract logits for the candidates, top-k +
-//                 weights + shared-expert append, input quant, and per-
-//                 workgroup expert histograms and in-workgroup ranks
+// Routing front end for large token counts (prefill, T > 256), four kernels:
+//   route_screen  bf16-MFMA router GEMM over all tokens and router rows: the
+//                 approximate logit a and a bound m on its distance from the
+//                 contract logit (2^-10 * ||x|| * ||w||, Cauchy-Schwarz)
+//   route_select  one wave per token: certified candidate set from (a, m),
+//                 exact contract logits of the candidates and the shared-gate
+//                 row, top-k + weights + shared-expert append, input quant,
+//                 logits out; per 16-token workgroup expert histogram and the
+//                 in-workgroup rank of every route
 //   sort_scan     per-expert totals, 64-row block layout, padding, and the
 //                 absolute row base of every (workgroup, expert) pair
 //   sort_scatter  sorted ids = base + in-workgroup rank
@@ -17,29 +21,34 @@
 namespace nkroute {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-constexpr uint32_t kTok = 16;       // tokens per route_screen workgroup (one MFMA row tile)
-constexpr uint32_t kThreads = 512;  // 8 waves
-constexpr uint32_t kWaves = kThreads / 64u;
+constexpr uint32_t kTok = 16;       // tokens per route_select workgroup (route_base granularity)
 constexpr uint32_t kMaxSlots = 64;  // K + S <= 64
-// Screen margin: |L - a| <= 2^-10 * sum |x_i w_i| covers the contract's fp32
-// chains (< 140 roundings of relative size 2^-24) plus the MFMA's fp32
+// Screen margin: |L - a| <= 2^-10 * ||x|| ||w||. Both the contract's fp32
+// chains (< 140 roundings of relative size 2^-24) and the MFMA's fp32
 // accumulation of exact bf16 products (< 2^11 roundings of at most 2^-23 even
-// if truncating), with a factor > 3 to spare.
+// if truncating) stay within 2.5e-4 * sum |x_i w_i| <= 2.5e-4 * ||x|| ||w||;
+// 2^-10 leaves a factor > 3, and the norms are rounded up by (1 + 2^-9).
 constexpr float kScreenMargin = 0.0009765625f;
-// Exact logits in the per-token scratch are tagged with this prefix; the
-// screen's sum |x w| values stored in the same words are non-negative floats,
-// whose top half is never 0xFFFF.
-constexpr uint32_t kExactTag = 0xFFFF0000u;
+constexpr float kNormSlack = 1.001953125f;
 
 __device__ __forceinline__ nk::v4f mfma_bf16(uint4 a, uint4 b, nk::v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
-__device__ __forceinline__ uint4 abs8(uint4 v) {
-  return make_uint4(v.x & 0x7fff7fffu, v.y & 0x7fff7fffu, v.z & 0x7fff7fffu, v.w & 0x7fff7fffu);
-}
 __device__ __forceinline__ uint32_t lane_rank(unsigned long long bal) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+}
+__device__ __forceinline__ float sumsq8(uint4 v) {
+  float s = 0.0f;
+  s = fmaf(nk::bf16_lo(v.x), nk::bf16_lo(v.x), s);
+  s = fmaf(nk::bf16_hi(v.x), nk::bf16_hi(v.x), s);
+  s = fmaf(nk::bf16_lo(v.y), nk::bf16_lo(v.y), s);
+  s = fmaf(nk::bf16_hi(v.y), nk::bf16_hi(v.y), s);
+  s = fmaf(nk::bf16_lo(v.z), nk::bf16_lo(v.z), s);
+  s = fmaf(nk::bf16_hi(v.z), nk::bf16_hi(v.z), s);
+  s = fmaf(nk::bf16_lo(v.w), nk::bf16_lo(v.w), s);
+  s = fmaf(nk::bf16_hi(v.w), nk::bf16_hi(v.w), s);
+  return s;
 }
 
 __device__ __forceinline__ void quant8(uint4 v, uint8_t* __restrict__ q_dst, float* __restrict__ s_dst,
@@ -64,7 +73,8 @@ __device__ __forceinline__ void quant8(uint4 v, uint8_t* __restrict__ q_dst, flo
 
 // Exact contract logit of one (token, router row) pair by a 16-lane group:
 // lane s runs the sequential fmaf chain over elements 128 j + 8 s + i from +0,
-// then the +8/+4/+2/+1 tree (the same order as netra_moe_router_h<H>).
+// then the +8/+4/+2/+1 tree (the same order as netra_moe_router_h<H>). The
+// token row comes from LDS (bf16, natural order), the router row from wv.
 template <uint32_t NJ>
 __device__ __forceinline__ float exact_dot(const uint4* __restrict__ xrow, const uint4 (&wv)[NJ], uint32_t s) {
   float a = 0.0f;
@@ -88,231 +98,225 @@ __device__ __forceinline__ float exact_dot(const uint4* __restrict__ xrow, const
   return a;
 }
 
-// route_screen: one workgroup per 16 tokens, 512 threads.
-//  1. stage the 16 token rows in LDS (bf16, natural order) and quantise them
-//     (1x128 groups, the same rule as the exact router);
-//  2. bf16 MFMA over all router rows: a = x . w and b = |x| . |w| (wave w owns
-//     column tiles w, w + 8, ...; the K order inside a 128-wide block is a
-//     permutation shared by both operands);
-//  3. per token (one wave): bounds zlo/zhi of z = f32(bf16(L)) + bias from
-//     L in [a - m, a + m], m = 2^-10 b (bf16 rounding and the bias add are
-//     monotone); theta = K-th largest zlo; candidates = {e : zhi_e >= theta}
-//     contain the true top-K, since every other expert lies strictly below K
-//     experts;
-//  4. exact logits of every candidate and of the shared-gate row (16-lane
-//     groups, two dot products at a time);
-//  5. per token: top-K over the candidates' exact z (descending, ties to the
-//     lower expert index), weights, shared expert append (as the exact top-k
-//     kernel);
-//  6. logits out, in-workgroup rank of every route among the workgroup's
-//     routes to the same expert (token order), per-expert histogram.
-template <uint32_t NJ, uint32_t RP, uint32_t EMAX>
-__device__ __forceinline__ void route_screen(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
-    uint16_t* __restrict__ logits, int32_t* __restrict__ ids, float* __restrict__ weights,
-    uint8_t* __restrict__ xq, float* __restrict__ xs, int32_t* __restrict__ hist,
-    int32_t* __restrict__ lrank, uint32_t T, uint32_t E, uint32_t K, uint32_t S) {
+// ---------------------------------------------------------------------------
+// route_screen: workgroup (tm, tn), 256 threads: tokens 64 tm .. +63 x router
+// rows 64 tn .. +63. Per 128-K block the x and w tiles are staged in LDS
+// (loads for the next block in flight during this one's multiplies); wave w
+// multiplies its 16 tokens by the four 16-row tiles with
+// v_mfma_f32_16x16x32_bf16. The staging threads also accumulate the squared
+// norms of their rows. Output screen[t][e] = (a, m) for t < T, e < rows,
+// row stride RP (rows rounded up to 64).
+template <uint32_t NJ>  // H / 128
+__device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                             float2* __restrict__ screen, uint32_t T, uint32_t rows,
+                                             uint32_t RP) {
   constexpr uint32_t H = 128u * NJ;
-  constexpr uint32_t kRow16 = 16u * NJ;                    // uint4 per token row
-  constexpr uint32_t kMaxTiles = (RP / 16u + kWaves - 1u) / kWaves;
-  constexpr uint32_t P = EMAX / 64u;                       // experts per lane
-  static_assert(RP % 16u == 0 && EMAX % 64u == 0 && P <= 8u, "shape");
-  __shared__ uint4 s_x[kTok * kRow16];
-  __shared__ float s_a[kTok * RP];
-  __shared__ uint32_t s_b[kTok * RP];
-  __shared__ uint16_t s_cand[kTok * EMAX];
-  __shared__ uint32_t s_n[kTok];
-  __shared__ int32_t s_ids[kTok * kMaxSlots];
-  __shared__ uint32_t s_hist[RP];
-
-  const uint32_t rows = E + S, Ktot = K + S;
-  if (rows > RP || E > EMAX || K == 0 || K > E || Ktot > kMaxSlots || S > 1u) return;  // uniform
+  constexpr uint32_t kStride = 136;  // bf16 per LDS row (128 + 8: rotates banks across rows)
+  __shared__ __align__(16) uint16_t s_x[2][64 * kStride];
+  __shared__ __align__(16) uint16_t s_w[2][64 * kStride];
+  __shared__ float s_nx[64], s_nw[64];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const uint32_t t0 = blockIdx.x * kTok;
-  for (uint32_t e = tid; e < RP; e += kThreads) s_hist[e] = 0u;
-
-  // 1. staging + input quant
-  constexpr uint32_t kPass = kTok * kRow16 / kThreads;
-  static_assert(kTok * kRow16 % kThreads == 0, "staging passes");
-  {
-    uint4 v[kPass];
+  const uint32_t t0 = blockIdx.x * 64u, r0 = blockIdx.y * 64u;
+  // staging: thread moves row (16 p + tid / 16) bytes (tid % 16) * 16 of both tiles, p = 0..3
+  const uint32_t srow = tid >> 4, sc = (tid & 15u) * 8u;  // sc in bf16
+  const uint16_t* xsrc[4];
+  const uint16_t* wsrc[4];
 #pragma unroll
-    for (uint32_t p = 0; p < kPass; ++p) {
-      const uint32_t idx = p * kThreads + tid;
-      const uint32_t tt = idx / kRow16, c16 = idx - tt * kRow16;
-      const uint32_t t = t0 + tt < T ? t0 + tt : T - 1u;
-      v[p] = *reinterpret_cast<const uint4*>(x + (size_t)t * H + 8u * c16);
-    }
-#pragma unroll
-    for (uint32_t p = 0; p < kPass; ++p) {
-      const uint32_t idx = p * kThreads + tid;
-      const uint32_t tt = idx / kRow16, c16 = idx - tt * kRow16;
-      s_x[idx] = v[p];
-      if (t0 + tt < T)  // uniform per wave: a row is >= 64 uint4
-        quant8(v[p], xq + (size_t)(t0 + tt) * H + 8u * c16, xs + (size_t)(t0 + tt) * NJ + (c16 >> 4),
-               (tid & 15u) == 0);
-    }
+  for (uint32_t p = 0; p < 4; ++p) {
+    const uint32_t t = t0 + 16u * p + srow, r = r0 + 16u * p + srow;
+    xsrc[p] = x + (size_t)(t < T ? t : T - 1u) * H + sc;
+    wsrc[p] = w + (size_t)(r < rows ? r : rows - 1u) * H + sc;
   }
-  __syncthreads();
-
-  // 2. screen: a = x . w, b = |x| . |w|
-  {
-    const uint32_t g = lane >> 4, rl = lane & 15u;
-    const uint32_t ntiles = (rows + 15u) / 16u;
-    nk::v4f acc[kMaxTiles], aab[kMaxTiles];
-    const uint16_t* wrow[kMaxTiles];
+  uint4 xv[4], wv[4];
+  float nx[4] = {0.0f, 0.0f, 0.0f, 0.0f}, nw[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (uint32_t m = 0; m < kMaxTiles; ++m) {
-      acc[m] = nk::v4f{0.0f, 0.0f, 0.0f, 0.0f};
-      aab[m] = acc[m];
-      const uint32_t r = (wave + kWaves * m) * 16u + rl;
-      wrow[m] = w + (size_t)(r < rows ? r : rows - 1u) * H + 32u * g;
+  for (uint32_t p = 0; p < 4; ++p) {
+    xv[p] = *reinterpret_cast<const uint4*>(xsrc[p]);
+    wv[p] = *reinterpret_cast<const uint4*>(wsrc[p]);
+  }
+  nk::v4f acc[4];
+#pragma unroll
+  for (uint32_t n = 0; n < 4; ++n) acc[n] = nk::v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t g = lane >> 4, rl = lane & 15u;
+  for (uint32_t kb = 0; kb < NJ; ++kb) {
+    const uint32_t buf = kb & 1u;
+#pragma unroll
+    for (uint32_t p = 0; p < 4; ++p) {
+      *reinterpret_cast<uint4*>(&s_x[buf][(16u * p + srow) * kStride + sc]) = xv[p];
+      *reinterpret_cast<uint4*>(&s_w[buf][(16u * p + srow) * kStride + sc]) = wv[p];
+      nx[p] += sumsq8(xv[p]);
+      nw[p] += sumsq8(wv[p]);
     }
-    const uint4* arow = s_x + rl * kRow16 + 4u * g;
-    uint4 bb[2][kMaxTiles][4];
-    auto load_b = [&](uint32_t kb, uint32_t buf) {
+    __syncthreads();
+    if (kb + 1u < NJ) {
 #pragma unroll
-      for (uint32_t m = 0; m < kMaxTiles; ++m)
-        if (wave + kWaves * m < ntiles)
-#pragma unroll
-          for (uint32_t q = 0; q < 4; ++q)
-            bb[buf][m][q] = *reinterpret_cast<const uint4*>(wrow[m] + 128u * kb + 8u * q);
-    };
-    auto compute = [&](uint32_t kb, uint32_t buf) {
-      uint4 a[4];
-#pragma unroll
-      for (uint32_t q = 0; q < 4; ++q) a[q] = arow[16u * kb + q];
-#pragma unroll
-      for (uint32_t m = 0; m < kMaxTiles; ++m)
-        if (wave + kWaves * m < ntiles)
-#pragma unroll
-          for (uint32_t q = 0; q < 4; ++q) {
-            acc[m] = mfma_bf16(a[q], bb[buf][m][q], acc[m]);
-            aab[m] = mfma_bf16(abs8(a[q]), abs8(bb[buf][m][q]), aab[m]);
-          }
-    };
-    load_b(0, 0);
-    for (uint32_t kb = 0; kb < NJ; kb += 2u) {
-      load_b(kb + 1u, 1);  // NJ is even
-      compute(kb, 0);
-      if (kb + 2u < NJ) load_b(kb + 2u, 0);
-      compute(kb + 1u, 1);
+      for (uint32_t p = 0; p < 4; ++p) {
+        xv[p] = *reinterpret_cast<const uint4*>(xsrc[p] + 128u * (kb + 1u));
+        wv[p] = *reinterpret_cast<const uint4*>(wsrc[p] + 128u * (kb + 1u));
+      }
     }
 #pragma unroll
-    for (uint32_t m = 0; m < kMaxTiles; ++m) {
-      const uint32_t c = wave + kWaves * m;
-      if (c < ntiles) {
+    for (uint32_t q = 0; q < 4; ++q) {
+      const uint4 a = *reinterpret_cast<const uint4*>(&s_x[buf][(16u * wave + rl) * kStride + 32u * q + 8u * g]);
 #pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) {
-          const uint32_t at = (g * 4u + i) * RP + c * 16u + rl;
-          s_a[at] = acc[m][i];
-          s_b[at] = __float_as_uint(aab[m][i]);
-        }
+      for (uint32_t n = 0; n < 4; ++n) {
+        const uint4 b = *reinterpret_cast<const uint4*>(&s_w[buf][(16u * n + rl) * kStride + 32u * q + 8u * g]);
+        acc[n] = mfma_bf16(a, b, acc[n]);
       }
     }
   }
-  __syncthreads();
-
-  // 3. certified candidate sets, one wave per token
-  for (uint32_t tt = wave; tt < kTok; tt += kWaves) {
-    if (t0 + tt >= T) {
-      if (lane == 0) s_n[tt] = 0u;
-      continue;
+  // row norms: the 16 threads of a row hold its 16 column slices
+#pragma unroll
+  for (uint32_t p = 0; p < 4; ++p) {
+    float a = nx[p], b = nw[p];
+    a += __shfl_xor(a, 1u); b += __shfl_xor(b, 1u);
+    a += __shfl_xor(a, 2u); b += __shfl_xor(b, 2u);
+    a += __shfl_xor(a, 4u); b += __shfl_xor(b, 4u);
+    a += __shfl_xor(a, 8u); b += __shfl_xor(b, 8u);
+    if ((tid & 15u) == 0) {
+      s_nx[16u * p + srow] = sqrtf(a) * kNormSlack;
+      s_nw[16u * p + srow] = sqrtf(b) * kNormSlack;
     }
+  }
+  __syncthreads();
+#pragma unroll
+  for (uint32_t n = 0; n < 4; ++n) {
+    const uint32_t r = r0 + 16u * n + rl;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+      const uint32_t tl = 16u * wave + 4u * g + i, t = t0 + tl;
+      if (t < T && r < rows)
+        screen[(size_t)t * RP + r] = make_float2(acc[n][i], kScreenMargin * s_nx[tl] * s_nw[16u * n + rl]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// route_select: workgroup of 8 waves for 16 tokens (a wave handles tokens
+// w and w + 8 in turn; 256 VGPRs per wave keep the exact phase in registers).
+//  1. bounds zlo/zhi of z = f32(bf16(L)) + bias from L in [a - m, a + m] (bf16
+//     rounding and the bias add are monotone); theta = K-th largest zlo;
+//     candidates = {e : zhi_e >= theta} contain the true top-K, since every
+//     other expert lies strictly below K experts;
+//  2. exact logits of the candidates and of the shared-gate row, one per
+//     16-lane group at a time (the token row staged in LDS);
+//  3. top-K over the candidates' exact z (descending, ties to the lower expert
+//     index), weights, shared expert append (as the exact top-k kernel);
+//  4. logits row (the input quant of the token is done while staging its row);
+//  5. per workgroup: in-workgroup rank of every route among the workgroup's
+//     routes to the same expert (token order) and the per-expert histogram.
+template <uint32_t NJ, uint32_t EMAX>
+__device__ __forceinline__ void route_select(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
+    const float2* __restrict__ screen, uint16_t* __restrict__ logits, int32_t* __restrict__ ids,
+    float* __restrict__ weights, uint8_t* __restrict__ xq, float* __restrict__ xs,
+    int32_t* __restrict__ hist, int32_t* __restrict__ lrank, uint32_t T, uint32_t E, uint32_t K,
+    uint32_t S, uint32_t RP) {
+  constexpr uint32_t H = 128u * NJ;
+  constexpr uint32_t P = EMAX / 64u;  // experts per lane
+  static_assert(EMAX % 64u == 0 && P <= 8u, "shape");
+  __shared__ uint4 s_x[kTok][16u * NJ];         // the tokens' rows (bf16)
+  __shared__ uint16_t s_cand[kTok][EMAX];
+  __shared__ uint16_t s_exact[kTok][EMAX + 1];  // exact logit bits, candidate order; shared row last
+  __shared__ int32_t s_ids[kTok][kMaxSlots];
+  __shared__ uint32_t s_hist[EMAX + 1];
+  const uint32_t rows = E + S, Ktot = K + S;
+  if (E > EMAX || K == 0 || K > E || Ktot > kMaxSlots || S > 1u) return;  // uniform
+  constexpr uint32_t kThreads = 512u;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
+  for (uint32_t e = tid; e <= EMAX; e += kThreads) s_hist[e] = 0u;
+  __syncthreads();
+  const uint32_t s = lane & 15u, g = lane >> 4;
+
+#pragma unroll 1
+  for (uint32_t tt = wave; tt < kTok; tt += kThreads / 64u) {
+    const uint32_t t = blockIdx.x * kTok + tt;
+    if (t >= T) break;  // uniform per wave; later tokens are past T too
+    // 1. certified candidates
+    const float2* srow = screen + (size_t)t * RP;
     uint32_t clo[P], chi[P];
+    float aval[P];
 #pragma unroll
     for (uint32_t j = 0; j < P; ++j) {
       const uint32_t e = lane + 64u * j;
-      clo[j] = 0u;
-      chi[j] = 0u;
+      clo[j] = chi[j] = 0u;
+      aval[j] = 0.0f;
       if (e < E) {
-        const float a = s_a[tt * RP + e];
-        const float m = __uint_as_float(s_b[tt * RP + e]) * kScreenMargin;
+        const float2 am = srow[e];
         const float b = bias[e];
-        clo[j] = nk::order_bits(nk::bf16_f32(nk::bf16_rne(a - m)) + b);
-        chi[j] = nk::order_bits(nk::bf16_f32(nk::bf16_rne(a + m)) + b);
+        aval[j] = am.x;
+        clo[j] = nk::order_bits(nk::bf16_f32(nk::bf16_rne(am.x - am.y)) + b);
+        chi[j] = nk::order_bits(nk::bf16_f32(nk::bf16_rne(am.x + am.y)) + b);
       }
     }
     uint32_t theta = 0u;
-    for (uint32_t r = 0; r < K; ++r) {
-      uint32_t best = 0u, bj = 0u;
+    {
+      uint32_t c[P];
 #pragma unroll
-      for (uint32_t j = 0; j < P; ++j)
-        if (clo[j] > best) { best = clo[j]; bj = j; }
-      theta = nk::wave_reduce_u32<true>(best);
-      const int wl = __ffsll(__ballot(best == theta)) - 1;
-      if ((int)lane == wl) {
+      for (uint32_t j = 0; j < P; ++j) c[j] = clo[j];
+      for (uint32_t r = 0; r < K; ++r) {
+        uint32_t best = 0u, bj = 0u;
 #pragma unroll
         for (uint32_t j = 0; j < P; ++j)
-          if (j == bj) clo[j] = 0u;
+          if (c[j] > best) { best = c[j]; bj = j; }
+        theta = nk::wave_reduce_u32<true>(best);
+        const int wl = __ffsll(__ballot(best == theta)) - 1;
+        if ((int)lane == wl) {
+#pragma unroll
+          for (uint32_t j = 0; j < P; ++j)
+            if (j == bj) c[j] = 0u;
+        }
       }
     }
-    uint32_t n = 0u;
+    uint32_t n = 0u, pos[P];
 #pragma unroll
     for (uint32_t j = 0; j < P; ++j) {
       const uint32_t e = lane + 64u * j;
       const bool pred = e < E && chi[j] >= theta;
       const unsigned long long bal = __ballot(pred);
-      if (pred) s_cand[tt * EMAX + n + lane_rank(bal)] = (uint16_t)e;
+      pos[j] = pred ? n + lane_rank(bal) : 0xffffffffu;
+      if (pred) s_cand[tt][pos[j]] = (uint16_t)e;
       n += (uint32_t)__popcll(bal);
     }
-    if (lane == 0) s_n[tt] = n;
-  }
-  __syncthreads();
 
-  // 4. exact logits of the candidates (+ the shared-gate row), two per group
-  {
-    const uint32_t grp = tid >> 4, s = tid & 15u;
-    uint32_t pref[kTok + 1];
-    pref[0] = 0u;
+    // 2. token row -> LDS (and its 1x128 quant); exact logits: jobs 0..n-1 are
+    // the candidates, job n the shared-gate row
 #pragma unroll
-    for (uint32_t i = 0; i < kTok; ++i)
-      pref[i + 1] = pref[i] + s_n[i] + ((S != 0u && t0 + i < T) ? 1u : 0u);
-    const uint32_t jobs = pref[kTok];
-    auto decode = [&](uint32_t q, uint32_t& tt, uint32_t& e) {
-      tt = 0u;
-#pragma unroll
-      for (uint32_t i = 1; i < kTok; ++i) tt += q >= pref[i] ? 1u : 0u;
-      const uint32_t idx = q - pref[tt];
-      e = idx < s_n[tt] ? (uint32_t)s_cand[tt * EMAX + idx] : E;
-    };
-    for (uint32_t q0 = grp; q0 < jobs; q0 += 2u * (kThreads / 16u)) {
-      const uint32_t q1 = q0 + kThreads / 16u;
-      const bool has1 = q1 < jobs;
-      uint32_t tt0, e0, tt1, e1;
-      decode(q0, tt0, e0);
-      decode(has1 ? q1 : q0, tt1, e1);
-      uint4 w0[NJ], w1[NJ];
-#pragma unroll
-      for (uint32_t j = 0; j < NJ; ++j) {
-        w0[j] = *reinterpret_cast<const uint4*>(w + (size_t)e0 * H + 128u * j + 8u * s);
-        w1[j] = *reinterpret_cast<const uint4*>(w + (size_t)e1 * H + 128u * j + 8u * s);
-      }
-      const float l0 = exact_dot<NJ>(s_x + tt0 * kRow16, w0, s);
-      const float l1 = exact_dot<NJ>(s_x + tt1 * kRow16, w1, s);
-      if (s == 0) {
-        s_b[tt0 * RP + e0] = kExactTag | nk::bf16_rne(l0);
-        if (has1) s_b[tt1 * RP + e1] = kExactTag | nk::bf16_rne(l1);
-      }
+    for (uint32_t p = 0; p < H / 512u; ++p) {
+      const uint32_t i0 = 512u * p + 8u * lane;
+      const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)t * H + i0);
+      s_x[tt][64u * p + lane] = v;
+      quant8(v, xq + (size_t)t * H + i0, xs + (size_t)t * NJ + (i0 >> 7), s == 0);
     }
-  }
-  __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's row is in LDS
+    __builtin_amdgcn_wave_barrier();
+    const uint32_t jobs = n + S;
+#pragma unroll 1
+    for (uint32_t q = g; q < jobs; q += 4u) {
+      const uint32_t e = q < n ? (uint32_t)s_cand[tt][q] : E;
+      uint4 wv[NJ];
+#pragma unroll
+      for (uint32_t j = 0; j < NJ; ++j) wv[j] = *reinterpret_cast<const uint4*>(w + (size_t)e * H + 128u * j + 8u * s);
+      const float l = exact_dot<NJ>(s_x[tt], wv, s);
+      if (s == 0) s_exact[tt][q] = nk::bf16_rne(l);
+    }
+    // (the exact values are read back by this wave only)
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
 
-  // 5. top-K over the candidates' exact z, weights, shared append
-  for (uint32_t tt = wave; tt < kTok; tt += kWaves) {
-    const uint32_t t = t0 + tt;
-    if (t >= T) continue;
-    const uint32_t n = s_n[tt];
+    // 3. top-K over the candidates' exact z
+    const uint32_t Pc = (n + 63u) / 64u;  // candidate slots per lane in use (uniform)
     uint32_t code[P], eid[P];
 #pragma unroll
     for (uint32_t j = 0; j < P; ++j) {
       const uint32_t i = lane + 64u * j;
       code[j] = 0u;
       eid[j] = 0u;
-      if (i < n) {
-        const uint32_t e = s_cand[tt * EMAX + i];
+      if (j < Pc && i < n) {
+        const uint32_t e = s_cand[tt][i];
         eid[j] = e;
-        code[j] = nk::order_bits(nk::bf16_f32(s_b[tt * RP + e] & 0xffffu) + bias[e]);
+        code[j] = nk::order_bits(nk::bf16_f32(s_exact[tt][i]) + bias[e]);
       }
     }
     uint32_t my_id = 0u, my_code = 0u;
@@ -356,56 +360,70 @@ __device__ __forceinline__ void route_screen(
     }
     if (S != 0u && lane == K) {
       my_id = E;
-      const uint32_t lb = s_b[tt * RP + E] & 0xffffu;
       ids[(size_t)t * Ktot + K] = (int32_t)E;
-      weights[(size_t)t * Ktot + K] = nk::bf16_f32(nk::bf16_rne(nk::sigmoid(nk::bf16_f32(lb))));
+      weights[(size_t)t * Ktot + K] = nk::bf16_f32(nk::bf16_rne(nk::sigmoid(nk::bf16_f32(s_exact[tt][n]))));
     }
     if (lane < Ktot) {
-      s_ids[tt * kMaxSlots + lane] = (int32_t)my_id;
+      s_ids[tt][lane] = (int32_t)my_id;
       atomicAdd(&s_hist[my_id], 1u);
     }
+
+    // 4. logits row
+    uint16_t* lrow = logits + (size_t)t * rows;
+#pragma unroll
+    for (uint32_t j = 0; j < P; ++j) {
+      const uint32_t e = lane + 64u * j;
+      if (e < E) lrow[e] = pos[j] != 0xffffffffu ? s_exact[tt][pos[j]] : nk::bf16_rne(aval[j]);
+    }
+    if (S != 0u && lane == 0) lrow[E] = s_exact[tt][n];
   }
   __syncthreads();
 
-  // 6. logits, in-workgroup ranks, histogram
-  for (uint32_t idx = tid; idx < kTok * rows; idx += kThreads) {
-    const uint32_t tt = idx / rows, e = idx - tt * rows;
-    if (t0 + tt >= T) break;  // later idx belong to later tokens
-    const uint32_t b = s_b[tt * RP + e];
-    const uint16_t bits = (b & kExactTag) == kExactTag ? (uint16_t)(b & 0xffffu) : nk::bf16_rne(s_a[tt * RP + e]);
-    logits[(size_t)(t0 + tt) * rows + e] = bits;
-  }
+  // 5. in-workgroup ranks and histogram
+  const uint32_t t0 = blockIdx.x * kTok;
   for (uint32_t r = tid; r < kTok * Ktot; r += kThreads) {
-    const uint32_t tt = r / Ktot, s = r - tt * Ktot;
-    if (t0 + tt >= T) break;
-    const int32_t e = s_ids[tt * kMaxSlots + s];
+    const uint32_t tk = r / Ktot, sl = r - tk * Ktot;
+    if (t0 + tk >= T) break;
+    const int32_t e = s_ids[tk][sl];
     uint32_t rank = 0u;
-    for (uint32_t u = 0; u < tt; ++u)
-      for (uint32_t v = 0; v < Ktot; ++v) rank += s_ids[u * kMaxSlots + v] == e ? 1u : 0u;
-    lrank[(size_t)(t0 + tt) * Ktot + s] = (int32_t)rank;
+    for (uint32_t u = 0; u < tk; ++u)
+      for (uint32_t v = 0; v < Ktot; ++v) rank += s_ids[u][v] == e ? 1u : 0u;
+    lrank[(size_t)(t0 + tk) * Ktot + sl] = (int32_t)rank;
   }
   for (uint32_t e = tid; e < rows; e += kThreads) hist[(size_t)blockIdx.x * rows + e] = (int32_t)s_hist[e];
 }
 
 }  // namespace nkroute
 
-#define NK_ROUTE_SCREEN(HV, RPV, EMAXV)                                                           \
-  NK_KERNEL __launch_bounds__(512) void netra_moe_route_screen_h##HV##_r##RPV##_gfx950(           \
-      const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,                             \
-      const float* __restrict__ bias, uint16_t* __restrict__ logits, int32_t* __restrict__ ids,   \
-      float* __restrict__ weights, uint8_t* __restrict__ xq, float* __restrict__ xs,              \
-      int32_t* __restrict__ hist, int32_t* __restrict__ lrank, uint32_t T, uint32_t H,            \
-      uint32_t E, uint32_t K, uint32_t S) {                                                       \
+#define NK_ROUTE_SCREEN(HV)                                                                       \
+  NK_KERNEL __launch_bounds__(256) void netra_moe_route_screen_h##HV##_gfx950(                    \
+      const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, float2* __restrict__ screen, \
+      uint32_t T, uint32_t H, uint32_t rows, uint32_t RP) {                                       \
     (void)H;                                                                                      \
-    nkroute::route_screen<HV / 128, RPV, EMAXV>(x, w, bias, logits, ids, weights, xq, xs, hist,   \
-                                                lrank, T, E, K, S);                               \
+    nkroute::route_screen<HV / 128>(x, w, screen, T, rows, RP);                                   \
   }
-NK_ROUTE_SCREEN(512, 384, 384)
-NK_ROUTE_SCREEN(1024, 384, 384)
-NK_ROUTE_SCREEN(2048, 384, 384)
-NK_ROUTE_SCREEN(512, 528, 512)
-NK_ROUTE_SCREEN(1024, 528, 512)
-NK_ROUTE_SCREEN(2048, 528, 512)
+NK_ROUTE_SCREEN(512)
+NK_ROUTE_SCREEN(1024)
+NK_ROUTE_SCREEN(2048)
+
+#define NK_ROUTE_SELECT(HV, EMAXV)                                                                \
+  NK_KERNEL __launch_bounds__(512) void netra_moe_route_select_h##HV##_e##EMAXV##_gfx950(         \
+      const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,                             \
+      const float* __restrict__ bias, const float2* __restrict__ screen,                          \
+      uint16_t* __restrict__ logits, int32_t* __restrict__ ids, float* __restrict__ weights,      \
+      uint8_t* __restrict__ xq, float* __restrict__ xs, int32_t* __restrict__ hist,               \
+      int32_t* __restrict__ lrank, uint32_t T, uint32_t H, uint32_t E, uint32_t K, uint32_t S,    \
+      uint32_t RP) {                                                                              \
+    (void)H;                                                                                      \
+    nkroute::route_select<HV / 128, EMAXV>(x, w, bias, screen, logits, ids, weights, xq, xs,      \
+                                           hist, lrank, T, E, K, S, RP);                          \
+  }
+NK_ROUTE_SELECT(512, 256)
+NK_ROUTE_SELECT(1024, 256)
+NK_ROUTE_SELECT(2048, 256)
+NK_ROUTE_SELECT(512, 512)
+NK_ROUTE_SELECT(1024, 512)
+NK_ROUTE_SELECT(2048, 512)
 
 // ---------------------------------------------------------------------------
 // sort_scan (one 1024-thread workgroup): hist[g][e] holds the routes of

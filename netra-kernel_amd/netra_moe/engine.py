@@ -54,6 +54,7 @@ STREAM_H = (512, 1024, 2048, 4096)   # netra_moe_gate_up_stream_h<H>_gfx950
 STREAM_I = (256, 512, 1024, 2048)    # netra_moe_down_stream_i<I>_gfx950
 TILE_H = (512, 1024, 2048, 4096)     # netra_moe_gate_up_tile_h<H>_gfx950
 TILE_I = (256, 512, 1024)            # netra_moe_down_tile_i<I>_gfx950
+TILE_GU_WAVES = 4                    # waves of netra_moe_gate_up_tile_h<H>_gfx950 (its launch bound)
 # Persistent stream kernels: 256 CUs x 4 SIMDs x resident waves per SIMD
 # (NK_GATE_UP_WAVES_PER_EU = 2, NK_DOWN_WAVES_PER_EU = 4) / 4 waves per group.
 STREAM_GRID_GATE_UP = 512
@@ -80,9 +81,9 @@ def xcd_grid(items: int) -> int:
 
 
 FRONTS = ("exact", "screen")
-SCREEN_H = (512, 1024, 2048)          # netra_moe_route_screen_h<H>_r<RP>_gfx950
-SCREEN_ROWS = (384, 528)              # router-row capacities RP of the screen kernels
-SCREEN_TOKENS = 16                    # tokens per route_screen workgroup (nkroute::kTok)
+SCREEN_H = (512, 1024, 2048)          # netra_moe_route_screen_h<H>_gfx950 / route_select_h<H>_e<EMAX>
+SCREEN_EMAX = (256, 512)              # expert capacities of the route_select kernels
+SCREEN_TOKENS = 16                    # tokens per route_select workgroup (nkroute::kTok)
 
 
 def resolve_front(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> str:
@@ -90,26 +91,23 @@ def resolve_front(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> st
     workgroup sort; screen: bf16-MFMA screen with exact recomputation of the
     certified candidates + two-kernel sort (the tile path's default)."""
     path = resolve_path(cfg, path)
-    ok = cfg.H in SCREEN_H and cfg.router_rows <= SCREEN_ROWS[-1]
+    ok = cfg.H in SCREEN_H and cfg.E <= SCREEN_EMAX[-1]
     if front == "auto":
         front = "screen" if path == "tile" and ok else "exact"
     if front not in FRONTS:
         raise ValueError(f"unknown front end {front!r}")
     if front == "screen" and not ok:
-        raise ValueError(f"screen front end needs H in {SCREEN_H} and E + S <= {SCREEN_ROWS[-1]}")
+        raise ValueError(f"screen front end needs H in {SCREEN_H} and E <= {SCREEN_EMAX[-1]}")
     return front
 
 
-def screen_rows(cfg: MoEConfig) -> int:
-    return next(r for r in SCREEN_ROWS if cfg.router_rows <= r)
+def screen_row_pad(cfg: MoEConfig) -> int:
+    """Router rows rounded up to the screen GEMM's 64-row tiles (row stride of the screen buffer)."""
+    return (cfg.router_rows + 63) // 64 * 64
 
 
-def screen_lds_bytes(cfg: MoEConfig) -> int:
-    """Static LDS of netra_moe_route_screen (s_x, s_a, s_b, s_cand, s_n, s_ids, s_hist)."""
-    rp = screen_rows(cfg)
-    emax = 384 if rp == 384 else 512
-    return (SCREEN_TOKENS * cfg.H * 2 + 2 * SCREEN_TOKENS * rp * 4 + SCREEN_TOKENS * emax * 2
-            + SCREEN_TOKENS * 4 + SCREEN_TOKENS * 64 * 4 + rp * 4)
+def screen_emax(cfg: MoEConfig) -> int:
+    return next(e for e in SCREEN_EMAX if cfg.E <= e)
 
 
 def screen_groups(cfg: MoEConfig) -> int:
@@ -143,7 +141,8 @@ def tensor_table(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> dic
     if front == "exact":
         specs.append(TensorSpec("mask", "u64", (cfg.Etot, cfg.mask_words_per_expert), "temporary"))
     else:
-        specs += [TensorSpec("route_base", "i32", (screen_groups(cfg), cfg.Etot), "temporary"),
+        specs += [TensorSpec("screen", "f32", (T, 2 * screen_row_pad(cfg)), "temporary"),
+                  TensorSpec("route_base", "i32", (screen_groups(cfg), cfg.Etot), "temporary"),
                   TensorSpec("route_rank", "i32", (T * cfg.Ktot,), "temporary")]
     if path == "stream":
         specs.append(TensorSpec("h", "bf16", (cfg.cap_rows, I), "temporary"))
@@ -155,7 +154,7 @@ def tensor_table(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> dic
 
 
 OP_NAMES = ("router", "topk", "sort", "gate_up", "down", "combine")
-SCREEN_OP_NAMES = ("route", "sort_scan", "sort_scatter", "gate_up", "down", "combine")
+SCREEN_OP_NAMES = ("route_screen", "route_select", "sort_scan", "sort_scatter", "gate_up", "down", "combine")
 
 
 def op_names(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> tuple[str, ...]:
@@ -172,12 +171,20 @@ def _screen_front(cfg: MoEConfig) -> list[dict]:
     T, H = cfg.T, cfg.H
     u = lambda v: ("u32", int(v))  # noqa: E731
     G = screen_groups(cfg)
+    RP = screen_row_pad(cfg)
     return [
-        dict(name="moe.route", symbol=f"netra_moe_route_screen_h{H}_r{screen_rows(cfg)}_gfx950",
-             grid=(G, 1, 1), block=(512, 1, 1), lds=screen_lds_bytes(cfg), dyn=0,
-             args=["x", "router_w", "router_bias", "logits", "topk_ids", "topk_weights", "x_q",
-                   "x_scale", "route_base", "route_rank", u(T), u(H), u(cfg.E), u(cfg.K), u(cfg.S)],
-             reads=["x", "router_w", "router_bias"],
+        dict(name="moe.route_screen", symbol=f"netra_moe_route_screen_h{H}_gfx950",
+             grid=((T + 63) // 64, RP // 64, 1), block=(256, 1, 1), lds=2 * 2 * 64 * 136 * 2 + 2 * 64 * 4, dyn=0,
+             args=["x", "router_w", "screen", u(T), u(H), u(cfg.router_rows), u(RP)],
+             reads=["x", "router_w"], writes=["screen"],
+             refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150"]),
+        dict(name="moe.route_select", symbol=f"netra_moe_route_select_h{H}_e{screen_emax(cfg)}_gfx950",
+             grid=(G, 1, 1), block=(512, 1, 1),
+             lds=SCREEN_TOKENS * H * 2 + 2 * SCREEN_TOKENS * (2 * screen_emax(cfg) + 1) + SCREEN_TOKENS * 64 * 4
+             + 4 * (screen_emax(cfg) + 1), dyn=0,
+             args=["x", "router_w", "router_bias", "screen", "logits", "topk_ids", "topk_weights", "x_q",
+                   "x_scale", "route_base", "route_rank", u(T), u(H), u(cfg.E), u(cfg.K), u(cfg.S), u(RP)],
+             reads=["x", "router_w", "router_bias", "screen"],
              writes=["logits", "topk_ids", "topk_weights", "x_q", "x_scale", "route_base", "route_rank"],
              refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150",
                    "runtime/gfx950/routing/decode/qwen36_shared_gate_append_bridge.hip:76-112"]),
@@ -256,16 +263,16 @@ def operations(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> list[
     else:
         ops += [
             dict(name="moe.gate_up", symbol=f"netra_moe_gate_up_tile_h{H}_gfx950",
-                 grid=(xcd_grid(cfg.cap_blocks * (I // 128)), 1, 1), block=(256, 1, 1),
-                 lds=2 * 64 * 144 + 64 * (H // 128) * 4 + 64 * 4 + 4 * 64 * 4 + 64 * 4, dyn=0,
+                 grid=(xcd_grid(cfg.cap_blocks * (I // 128)), 1, 1), block=(64 * TILE_GU_WAVES, 1, 1),
+                 lds=2 * 64 * 144 + 2 * 64 * (H // 128) * 4 + 64 * 4 + TILE_GU_WAVES * 64 * 4 + 64 * 4, dyn=0,
                  args=["x_q", "x_scale", "w13", "w13_scale", *common, "h_q", "h_scale",
                        u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
                  reads=["x_q", "x_scale", "w13", "w13_scale", *common], writes=["h_q", "h_scale"],
                  refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/gate_up.inc",
                        "kernels/gfx950/templates/moe/prefill/fused_splitk2/silu_quant.inc"]),
             dict(name="moe.down", symbol=f"netra_moe_down_tile_i{I}_gfx950",
-                 grid=(xcd_grid(cfg.cap_blocks * (H // 256)), 1, 1), block=(256, 1, 1),
-                 lds=max(64 * (I + 16), 64 * 528) + 64 * (I // 128) * 4 + 64 * 4, dyn=0,
+                 grid=(xcd_grid(cfg.cap_blocks * (H // 128)), 1, 1), block=(256, 1, 1),
+                 lds=max(64 * (I + 16), 64 * 272) + 64 * (I // 128) * 4 + 64 * 4, dyn=0,
                  args=["h_q", "h_scale", "w2", "w2_scale", *common, "partial",
                        u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
                  reads=["h_q", "h_scale", "w2", "w2_scale", *common], writes=["partial"],

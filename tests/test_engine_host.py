@@ -156,8 +156,9 @@ def test_prefill_engines_use_the_screen_front_end(tmp_path):
     assert doc["front_end"] == "screen" and doc["gemm_path"] == "tile"
     assert [op["name"] for op in doc["operations"]] == [f"moe.{n}" for n in SCREEN_OP_NAMES]
     assert nm.manifest_check(tmp_path / "p")[0] == nm.Status.OK
-    route = doc["operations"][0]
-    assert route["launch"]["grid"] == [256, 1, 1] and route["launch"]["lds_bytes"] <= 160 * 1024
+    screen, select = doc["operations"][0], doc["operations"][1]
+    assert screen["launch"]["grid"] == [64, 5, 1]  # 4096 / 64 tokens x 320 / 64 router rows
+    assert select["launch"]["grid"] == [256, 1, 1] and select["launch"]["lds_bytes"] <= 160 * 1024
 
 
 def test_profiles_select_exact_shapes_and_refuse_neighbours():

@@ -10,10 +10,12 @@
 // Waves never synchronise with each other; per-item values that every lane
 // needs (activation scales) go through the wave's own LDS slot.
 //
-// gate/up writes h = bf16(silu(g) * u) in sorted-row order; down requantises h
-// per 1x128 group as it consumes it (the SiLU-quant step of the reference's
-// decode trio folded into the consumer) and writes fp32 route partials.
-// Symbols: netra_moe_gate_up_stream_h<H>_gfx950, netra_moe_down_stream_i<I>_gfx950.
+// gate/up writes h = bf16(silu(g) * u) in sorted-row order; a requant kernel
+// turns each (16-row tile, 128-column block) into the FP8 operand plus row
+// scales once (the SiLU-quant step of the reference's decode trio); down
+// streams W2 against it and writes fp32 route partials.
+// Symbols: netra_moe_gate_up_stream_h<H>_gfx950, netra_moe_requant_h_gfx950,
+// netra_moe_down_stream_i<I>_gfx950.
 #pragma once
 #include "moe_numerics.h"
 
@@ -224,25 +226,83 @@ NK_GATE_UP_STREAM(2048)
 NK_GATE_UP_STREAM(4096)
 
 // ---------------------------------------------------------------------------
-// (reference: kernels/gfx950/templates/moe/decode/silu_quant.inc:16-236 for the
-// requant and down_reduce_mfma_2wave.inc:14-291 for the GEMM; oracle
-// tools/benchmark/export_qwen36_moe_stage2_capture.py:90-110)
+// 1x128 FP8 requant of h between the decode GEMMs (reference: kernels/gfx950/
+// templates/moe/decode/silu_quant.inc:16-236; rule of harness/gfx950/fp8/moe/
+// decode/qwen36_moe_silu_mul_quant_fp8_gfx950.hip:57-94).
+//
+// One wave per (16-row tile, 128-column block), persistent over the sort's
+// tile list: lane l holds 32 bf16 of row l & 15 (columns (l >> 4) * 32 .. +31
+// of the block); the four lanes of a row combine their maxima, scale =
+// max(amax, 1e-10) * 0x3b124925, q = e4m3(h * (1 / scale)). The FP8 tile is
+// written in the tile16x128 operand layout (lo half at l * 16, hi half at
+// 1024 + l * 16) and the 16 row scales of the (tile, block) contiguously, so
+// the down GEMM loads its A operand and scales without further arithmetic.
+NK_KERNEL __launch_bounds__(256) void netra_moe_requant_h_gfx950(
+    const uint16_t* __restrict__ h, uint8_t* __restrict__ hq, float* __restrict__ hs,
+    const int32_t* __restrict__ tile_map, const int32_t* __restrict__ num_valid, uint32_t I) {
+  using namespace nkstream;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t KB = I / 128u;
+  const Range r = wave_range((uint32_t)num_valid[2] * KB);
+  for (uint32_t item = r.beg; item < r.end; ++item) {
+    const uint32_t ti = item / KB, kb = item - ti * KB;
+    const uint32_t m = (uint32_t)tile_map[ti];
+    const uint32_t tile = (m >> 2) * 4u + (m & 3u);  // 16-row tile index in sorted order
+    const size_t blk = (size_t)tile * KB + kb;
+    const uint4* src = reinterpret_cast<const uint4*>(h + blk * 2048u) + lane;
+    uint4 raw[4];
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) raw[q] = src[q * 64u];
+    float f[32];
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+      f[8 * q + 0] = nk::bf16_lo(raw[q].x); f[8 * q + 1] = nk::bf16_hi(raw[q].x);
+      f[8 * q + 2] = nk::bf16_lo(raw[q].y); f[8 * q + 3] = nk::bf16_hi(raw[q].y);
+      f[8 * q + 4] = nk::bf16_lo(raw[q].z); f[8 * q + 5] = nk::bf16_hi(raw[q].z);
+      f[8 * q + 6] = nk::bf16_lo(raw[q].w); f[8 * q + 7] = nk::bf16_hi(raw[q].w);
+    }
+    float amax = nk::kAmaxFloor;
+#pragma unroll
+    for (uint32_t q = 0; q < 32; ++q) amax = fmaxf(amax, fabsf(f[q]));
+    amax = fmaxf(amax, __shfl_xor(amax, 16u));
+    amax = fmaxf(amax, __shfl_xor(amax, 32u));
+    const float scale = amax * nk::inv_e4m3_max();
+    const float inv = 1.0f / scale;
+    uint4 lo, hi;
+    lo.x = nk::e4m3x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv);
+    lo.y = nk::e4m3x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv);
+    lo.z = nk::e4m3x4(f[8] * inv, f[9] * inv, f[10] * inv, f[11] * inv);
+    lo.w = nk::e4m3x4(f[12] * inv, f[13] * inv, f[14] * inv, f[15] * inv);
+    hi.x = nk::e4m3x4(f[16] * inv, f[17] * inv, f[18] * inv, f[19] * inv);
+    hi.y = nk::e4m3x4(f[20] * inv, f[21] * inv, f[22] * inv, f[23] * inv);
+    hi.z = nk::e4m3x4(f[24] * inv, f[25] * inv, f[26] * inv, f[27] * inv);
+    hi.w = nk::e4m3x4(f[28] * inv, f[29] * inv, f[30] * inv, f[31] * inv);
+    uint8_t* dst = hq + blk * 2048u;
+    *reinterpret_cast<uint4*>(dst + lane * 16u) = lo;
+    *reinterpret_cast<uint4*>(dst + 1024u + lane * 16u) = hi;
+    if (lane < 16u) hs[blk * 16u + lane] = scale;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// (reference: kernels/gfx950/templates/moe/decode/down_reduce_mfma_2wave.inc:
+// 14-291; oracle tools/benchmark/export_qwen36_moe_stage2_capture.py:90-110)
 //
 // Item (tile, c): output columns [32 c, 32 c + 32) (two 16-column tiles) of one
-// 16-row tile; one 128-wide K block per step. Each lane loads 32 bf16 of h
-// (row l & 15), the four lanes holding one row combine their maxima,
-// scale = max(amax, 1e-10) * 0x3b124925 and q = e4m3(h * (1 / scale)) form the
-// MFMA operand in registers. After the last step each valid row's fp32 result
+// 16-row tile; one 128-wide K block per step. The A operand is the requantised
+// FP8 tile and its row scales (netra_moe_requant_h_gfx950); per block
+// acc += w_s * (a_s * mfma). After the last step each valid row's fp32 result
 // goes to partial[route].
 struct DownStep {
-  uint4 hraw[4];
+  nk::v8i a;
+  float4 as;
   nk::v8i w[2];
   float s[2];
 };
 
 template <uint32_t KB>
 __device__ __forceinline__ void down_stream(
-    const uint16_t* __restrict__ h, const uint8_t* __restrict__ w2,
+    const uint8_t* __restrict__ hq, const float* __restrict__ hs, const uint8_t* __restrict__ w2,
     const float* __restrict__ w2s, const int32_t* __restrict__ sorted_ids,
     const int32_t* __restrict__ sorted_expert, const int32_t* __restrict__ tile_map,
     const int32_t* __restrict__ num_valid, float* __restrict__ partial, uint32_t T, uint32_t H,
@@ -252,7 +312,6 @@ __device__ __forceinline__ void down_stream(
   constexpr uint32_t NCH = KB;
   static_assert(NCH % 2 == 0, "I must be a multiple of 256");
   const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t kofs = (lane >> 4) * 32u;
   const uint32_t cols = H / 32u;
   const Range r = wave_range((uint32_t)num_valid[2] * cols);
   const uint32_t steps = (r.end - r.beg) * NCH;
@@ -264,10 +323,9 @@ __device__ __forceinline__ void down_stream(
   auto issue = [&](DownStep& st, const TileRows& m, uint32_t s) {
     const uint32_t item = r.beg + s / NCH, kb = s % NCH;
     const uint32_t c = item % cols;
-    // h tile layout: four 1 KiB pieces per (tile, K block), lane l at l * 16.
-    const uint4* src = reinterpret_cast<const uint4*>(h + ((size_t)(m.row0 >> 4) * KB + kb) * 2048u) + lane;
-#pragma unroll
-    for (uint32_t q = 0; q < 4; ++q) st.hraw[q] = src[q * 64u];
+    const size_t blk = (size_t)(m.row0 >> 4) * KB + kb;
+    st.a = nk::load_tile_operand(hq + blk * 2048u, lane);
+    st.as = *reinterpret_cast<const float4*>(hs + blk * 16u + (lane >> 4) * 4u);
     const uint8_t* we = w2 + (size_t)m.expert * H * I;
     const float* wse = w2s + (size_t)m.expert * (H / 128u) * KB;
 #pragma unroll
@@ -278,30 +336,9 @@ __device__ __forceinline__ void down_stream(
   };
   nk::v4f acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
   auto compute = [&](const DownStep& st, const TileRows& m, uint32_t s) {
-    float f[32];
-#pragma unroll
-    for (uint32_t q = 0; q < 4; ++q) {
-      f[8 * q + 0] = nk::bf16_lo(st.hraw[q].x); f[8 * q + 1] = nk::bf16_hi(st.hraw[q].x);
-      f[8 * q + 2] = nk::bf16_lo(st.hraw[q].y); f[8 * q + 3] = nk::bf16_hi(st.hraw[q].y);
-      f[8 * q + 4] = nk::bf16_lo(st.hraw[q].z); f[8 * q + 5] = nk::bf16_hi(st.hraw[q].z);
-      f[8 * q + 6] = nk::bf16_lo(st.hraw[q].w); f[8 * q + 7] = nk::bf16_hi(st.hraw[q].w);
-    }
-    float amax = nk::kAmaxFloor;
-#pragma unroll
-    for (uint32_t q = 0; q < 32; ++q) amax = fmaxf(amax, fabsf(f[q]));
-    amax = fmaxf(amax, __shfl_xor(amax, 16u));
-    amax = fmaxf(amax, __shfl_xor(amax, 32u));
-    const float scale = amax * nk::inv_e4m3_max();
-    const float inv = 1.0f / scale;
-    nk::v8i a;
-#pragma unroll
-    for (uint32_t q = 0; q < 8; ++q)
-      a[q] = (int)nk::e4m3x4(f[4 * q] * inv, f[4 * q + 1] * inv, f[4 * q + 2] * inv, f[4 * q + 3] * inv);
-    float as[4];
-#pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) as[j] = __shfl(scale, (lane >> 4) * 4u + j);
-    const nk::v4f d0 = nk::mfma_e4m3_16x16x128(a, st.w[0]);
-    const nk::v4f d1 = nk::mfma_e4m3_16x16x128(a, st.w[1]);
+    const float as[4] = {st.as.x, st.as.y, st.as.z, st.as.w};
+    const nk::v4f d0 = nk::mfma_e4m3_16x16x128(st.a, st.w[0]);
+    const nk::v4f d1 = nk::mfma_e4m3_16x16x128(st.a, st.w[1]);
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j) {
       acc0[j] = acc0[j] + st.s[0] * (as[j] * d0[j]);
@@ -348,14 +385,14 @@ __device__ __forceinline__ void down_stream(
 #define NK_DOWN_STREAM(IV)                                                                      \
   NK_KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NK_DOWN_WAVES_PER_EU)))    \
   void netra_moe_down_stream_i##IV##_gfx950(                                                    \
-      const uint16_t* __restrict__ h, const uint8_t* __restrict__ w2,                           \
+      const uint8_t* __restrict__ hq, const float* __restrict__ hs, const uint8_t* __restrict__ w2, \
       const float* __restrict__ w2s, const int32_t* __restrict__ sorted_ids,                    \
       const int32_t* __restrict__ sorted_expert, const int32_t* __restrict__ tile_map,          \
       const int32_t* __restrict__ num_valid, float* __restrict__ partial, uint32_t T,           \
       uint32_t H, uint32_t I, uint32_t Ktot, uint32_t Etot) {                                   \
     (void)I;                                                                                    \
-    down_stream<IV / 128>(h, w2, w2s, sorted_ids, sorted_expert, tile_map, num_valid, partial, T, \
-                          H, Ktot, Etot);                                                       \
+    down_stream<IV / 128>(hq, hs, w2, w2s, sorted_ids, sorted_expert, tile_map, num_valid,      \
+                          partial, T, H, Ktot, Etot);                                           \
   }
 NK_DOWN_STREAM(256)
 NK_DOWN_STREAM(512)

@@ -119,42 +119,48 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
   const uint32_t t0 = blockIdx.x * 64u, r0 = blockIdx.y * 64u;
   // staging: thread moves row (16 p + tid / 16) bytes (tid % 16) * 16 of both tiles, p = 0..3
   const uint32_t srow = tid >> 4, sc = (tid & 15u) * 8u;  // sc in bf16
-  const uint16_t* xsrc[4];
-  const uint16_t* wsrc[4];
+  // buffer loads: one 32-bit byte offset per row and a scalar offset per block
+  const __amdgpu_buffer_rsrc_t xr = nk::buffer_rsrc(x, T * H * 2u);
+  const __amdgpu_buffer_rsrc_t wr = nk::buffer_rsrc(w, rows * H * 2u);
+  uint32_t xoff[4], woff[4];
 #pragma unroll
   for (uint32_t p = 0; p < 4; ++p) {
     const uint32_t t = t0 + 16u * p + srow, r = r0 + 16u * p + srow;
-    xsrc[p] = x + (size_t)(t < T ? t : T - 1u) * H + sc;
-    wsrc[p] = w + (size_t)(r < rows ? r : rows - 1u) * H + sc;
+    xoff[p] = ((t < T ? t : T - 1u) * H + sc) * 2u;
+    woff[p] = ((r < rows ? r : rows - 1u) * H + sc) * 2u;
   }
-  uint4 xv[4], wv[4];
+  // register ring: loads for block kb + 2 are issued while block kb is
+  // multiplied; LDS-only barriers keep them in flight
+  constexpr uint32_t kRing = 3;
+  uint4 xv[kRing][4], wv[kRing][4];
   float nx[4] = {0.0f, 0.0f, 0.0f, 0.0f}, nw[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto load = [&](uint32_t kb, uint32_t slot) __attribute__((always_inline)) {
 #pragma unroll
-  for (uint32_t p = 0; p < 4; ++p) {
-    xv[p] = *reinterpret_cast<const uint4*>(xsrc[p]);
-    wv[p] = *reinterpret_cast<const uint4*>(wsrc[p]);
-  }
+    for (uint32_t p = 0; p < 4; ++p) {
+      const nk::u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(xr, (int)xoff[p], (int)(256u * kb), 0);
+      const nk::u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(wr, (int)woff[p], (int)(256u * kb), 0);
+      xv[slot][p] = make_uint4(a.x, a.y, a.z, a.w);
+      wv[slot][p] = make_uint4(b.x, b.y, b.z, b.w);
+    }
+  };
+  load(0, 0);
+  if (NJ > 1) load(1, 1);
   nk::v4f acc[4];
 #pragma unroll
   for (uint32_t n = 0; n < 4; ++n) acc[n] = nk::v4f{0.0f, 0.0f, 0.0f, 0.0f};
   const uint32_t g = lane >> 4, rl = lane & 15u;
+#pragma unroll
   for (uint32_t kb = 0; kb < NJ; ++kb) {
-    const uint32_t buf = kb & 1u;
+    const uint32_t buf = kb & 1u, slot = kb % kRing;
 #pragma unroll
     for (uint32_t p = 0; p < 4; ++p) {
-      *reinterpret_cast<uint4*>(&s_x[buf][(16u * p + srow) * kStride + sc]) = xv[p];
-      *reinterpret_cast<uint4*>(&s_w[buf][(16u * p + srow) * kStride + sc]) = wv[p];
-      nx[p] += sumsq8(xv[p]);
-      nw[p] += sumsq8(wv[p]);
+      *reinterpret_cast<uint4*>(&s_x[buf][(16u * p + srow) * kStride + sc]) = xv[slot][p];
+      *reinterpret_cast<uint4*>(&s_w[buf][(16u * p + srow) * kStride + sc]) = wv[slot][p];
+      nx[p] += sumsq8(xv[slot][p]);
+      nw[p] += sumsq8(wv[slot][p]);
     }
-    __syncthreads();
-    if (kb + 1u < NJ) {
-#pragma unroll
-      for (uint32_t p = 0; p < 4; ++p) {
-        xv[p] = *reinterpret_cast<const uint4*>(xsrc[p] + 128u * (kb + 1u));
-        wv[p] = *reinterpret_cast<const uint4*>(wsrc[p] + 128u * (kb + 1u));
-      }
-    }
+    if (kb + 2u < NJ) load(kb + 2u, (kb + 2u) % kRing);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
     for (uint32_t q = 0; q < 4; ++q) {
       const uint4 a = *reinterpret_cast<const uint4*>(&s_x[buf][(16u * wave + rl) * kStride + 32u * q + 8u * g]);
@@ -164,6 +170,7 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
         acc[n] = mfma_bf16(a, b, acc[n]);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);  // one 128-K block per schedule region
   }
   // row norms: the 16 threads of a row hold its 16 column slices
 #pragma unroll
@@ -219,6 +226,7 @@ __device__ __forceinline__ void route_select(
   __shared__ uint16_t s_cand[kTok][EMAX];
   __shared__ uint16_t s_exact[kTok][EMAX + 1];  // exact logit bits, candidate order; shared row last
   __shared__ int32_t s_ids[kTok][kMaxSlots];
+  __shared__ uint2 s_sel[kTok][kMaxSlots];       // (expert, code) by slot
   __shared__ uint32_t s_hist[EMAX + 1];
   const uint32_t rows = E + S, Ktot = K + S;
   if (E > EMAX || K == 0 || K > E || Ktot > kMaxSlots || S > 1u) return;  // uniform
@@ -250,24 +258,16 @@ __device__ __forceinline__ void route_select(
         chi[j] = nk::order_bits(nk::bf16_f32(nk::bf16_rne(am.x + am.y)) + b);
       }
     }
+    // theta = K-th largest zlo: the largest code with at least K codes >= it,
+    // found bit by bit from the top (absent experts have code 0)
     uint32_t theta = 0u;
-    {
-      uint32_t c[P];
+#pragma unroll 1
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t cand = theta | (1u << bit);
+      uint32_t cnt = 0u;
 #pragma unroll
-      for (uint32_t j = 0; j < P; ++j) c[j] = clo[j];
-      for (uint32_t r = 0; r < K; ++r) {
-        uint32_t best = 0u, bj = 0u;
-#pragma unroll
-        for (uint32_t j = 0; j < P; ++j)
-          if (c[j] > best) { best = c[j]; bj = j; }
-        theta = nk::wave_reduce_u32<true>(best);
-        const int wl = __ffsll(__ballot(best == theta)) - 1;
-        if ((int)lane == wl) {
-#pragma unroll
-          for (uint32_t j = 0; j < P; ++j)
-            if (j == bj) c[j] = 0u;
-        }
-      }
+      for (uint32_t j = 0; j < P; ++j) cnt += (uint32_t)__popcll(__ballot(clo[j] >= cand));
+      if (cnt >= K) theta = cand;
     }
     uint32_t n = 0u, pos[P];
 #pragma unroll
@@ -305,48 +305,70 @@ __device__ __forceinline__ void route_select(
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
 
-    // 3. top-K over the candidates' exact z
-    const uint32_t Pc = (n + 63u) / 64u;  // candidate slots per lane in use (uniform)
-    uint32_t code[P], eid[P];
-#pragma unroll
-    for (uint32_t j = 0; j < P; ++j) {
-      const uint32_t i = lane + 64u * j;
-      code[j] = 0u;
-      eid[j] = 0u;
-      if (j < Pc && i < n) {
-        const uint32_t e = s_cand[tt][i];
-        eid[j] = e;
-        code[j] = nk::order_bits(nk::bf16_f32(s_exact[tt][i]) + bias[e]);
-      }
-    }
+    // 3. top-K over the candidates' exact z (descending, ties to the lower id)
     uint32_t my_id = 0u, my_code = 0u;
-    for (uint32_t r = 0; r < K; ++r) {
-      uint32_t best = 0u, bj = 0u;
-#pragma unroll
-      for (uint32_t j = 0; j < P; ++j)
-        if (code[j] > best) { best = code[j]; bj = j; }
-      const uint32_t m = nk::wave_reduce_u32<true>(best);
-      const unsigned long long tied = __ballot(best == m);
-      uint32_t wl, wj;
-      if (__popcll(tied) == 1) {
-        wl = (uint32_t)(__ffsll(tied) - 1);
-        wj = (uint32_t)__builtin_amdgcn_readlane((int)bj, (int)wl);
-      } else {  // candidates are in ascending expert order along (j, lane)
-        const uint32_t k = nk::wave_reduce_u32<false>(best == m ? (bj << 6) | lane : 0xffffffffu);
-        wl = k & 63u;
-        wj = k >> 6;
+    if (n <= 64u) {  // one candidate per lane: slot = rank among the candidates
+      uint32_t ei = 0xffffu, ci = 0u;
+      if (lane < n) {
+        ei = s_cand[tt][lane];
+        ci = nk::order_bits(nk::bf16_f32(s_exact[tt][lane]) + bias[ei]);
       }
-      uint32_t ej = eid[0];
+      uint32_t rank = 0u;
+      for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t c2 = (uint32_t)__builtin_amdgcn_readlane((int)ci, (int)i);
+        const uint32_t e2 = (uint32_t)__builtin_amdgcn_readlane((int)ei, (int)i);
+        rank += (c2 > ci || (c2 == ci && e2 < ei)) ? 1u : 0u;
+      }
+      if (lane < n && rank < K) s_sel[tt][rank] = make_uint2(ei, ci);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      __builtin_amdgcn_wave_barrier();
+      if (lane < K) {
+        const uint2 sel = s_sel[tt][lane];
+        my_id = sel.x;
+        my_code = sel.y;
+      }
+    } else {  // more candidates than lanes: K selection rounds over (j, lane)
+      const uint32_t Pc = (n + 63u) / 64u;
+      uint32_t code[P], eid[P];
 #pragma unroll
-      for (uint32_t j = 1; j < P; ++j)
-        if (j == wj) ej = eid[j];
-      const uint32_t win = (uint32_t)__builtin_amdgcn_readlane((int)ej, (int)wl);
-      if (lane == wl) {
+      for (uint32_t j = 0; j < P; ++j) {
+        const uint32_t i = lane + 64u * j;
+        code[j] = 0u;
+        eid[j] = 0u;
+        if (j < Pc && i < n) {
+          const uint32_t e = s_cand[tt][i];
+          eid[j] = e;
+          code[j] = nk::order_bits(nk::bf16_f32(s_exact[tt][i]) + bias[e]);
+        }
+      }
+      for (uint32_t r = 0; r < K; ++r) {
+        uint32_t best = 0u, bj = 0u;
 #pragma unroll
         for (uint32_t j = 0; j < P; ++j)
-          if (j == wj) code[j] = 0u;
+          if (code[j] > best) { best = code[j]; bj = j; }
+        const uint32_t m = nk::wave_reduce_u32<true>(best);
+        const unsigned long long tied = __ballot(best == m);
+        uint32_t wl, wj;
+        if (__popcll(tied) == 1) {
+          wl = (uint32_t)(__ffsll(tied) - 1);
+          wj = (uint32_t)__builtin_amdgcn_readlane((int)bj, (int)wl);
+        } else {  // candidates are in ascending expert order along (j, lane)
+          const uint32_t k = nk::wave_reduce_u32<false>(best == m ? (bj << 6) | lane : 0xffffffffu);
+          wl = k & 63u;
+          wj = k >> 6;
+        }
+        uint32_t ej = eid[0];
+#pragma unroll
+        for (uint32_t j = 1; j < P; ++j)
+          if (j == wj) ej = eid[j];
+        const uint32_t win = (uint32_t)__builtin_amdgcn_readlane((int)ej, (int)wl);
+        if (lane == wl) {
+#pragma unroll
+          for (uint32_t j = 0; j < P; ++j)
+            if (j == wj) code[j] = 0u;
+        }
+        if (lane == r) { my_id = win; my_code = m; }
       }
-      if (lane == r) { my_id = win; my_code = m; }
     }
     const float z = nk::from_order_bits(my_code);
     const float z0 = __shfl(z, 0);
@@ -454,8 +476,10 @@ NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_scan_gfx950(
   const bool member = e < Etot;
   const uint32_t g0 = (G * q) / Q, g1 = (G * (q + 1u)) / Q;
   uint32_t sum = 0u;
-  if (member)
+  if (member) {
+#pragma unroll 16
     for (uint32_t g = g0; g < g1; ++g) sum += (uint32_t)hist[(size_t)g * Etot + e];
+  }
   part[tid] = sum;
   for (uint32_t b = tid; b < cap_blocks; b += 1024u) owner[b] = -1;
   __syncthreads();
@@ -498,6 +522,7 @@ NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_scan_gfx950(
   __syncthreads();
   if (member) {  // absolute base rows, in place
     uint32_t pos = block_off[e] * 64u + before;
+#pragma unroll 16
     for (uint32_t g = g0; g < g1; ++g) {
       const uint32_t v = (uint32_t)hist[(size_t)g * Etot + e];
       hist[(size_t)g * Etot + e] = (int32_t)pos;

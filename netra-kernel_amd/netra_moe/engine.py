@@ -59,6 +59,7 @@ TILE_GU_WAVES = 4                    # waves of netra_moe_gate_up_tile_h<H>_gfx9
 # (NK_GATE_UP_WAVES_PER_EU = 2, NK_DOWN_WAVES_PER_EU = 4) / 4 waves per group.
 STREAM_GRID_GATE_UP = 512
 STREAM_GRID_DOWN = 1024
+STREAM_GRID_REQUANT = 256
 
 
 def resolve_path(cfg: MoEConfig, path: str = "auto") -> str:
@@ -145,7 +146,9 @@ def tensor_table(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> dic
                   TensorSpec("route_base", "i32", (screen_groups(cfg), cfg.Etot), "temporary"),
                   TensorSpec("route_rank", "i32", (T * cfg.Ktot,), "temporary")]
     if path == "stream":
-        specs.append(TensorSpec("h", "bf16", (cfg.cap_rows, I), "temporary"))
+        specs += [TensorSpec("h", "bf16", (cfg.cap_rows, I), "temporary"),
+                  TensorSpec("h_q", "e4m3", (cfg.cap_rows, I), "temporary"),
+                  TensorSpec("h_scale", "f32", (cfg.cap_rows // 16, I // 128, 16), "temporary")]
     else:
         specs += [TensorSpec("h_q", "e4m3", (cfg.cap_rows, I), "temporary"),
                   TensorSpec("h_scale", "f32", (cfg.cap_rows, I // 128), "temporary")]
@@ -153,12 +156,16 @@ def tensor_table(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> dic
     return {s.name: s for s in specs}
 
 
-OP_NAMES = ("router", "topk", "sort", "gate_up", "down", "combine")
-SCREEN_OP_NAMES = ("route_screen", "route_select", "sort_scan", "sort_scatter", "gate_up", "down", "combine")
+EXACT_FRONT_OPS = ("router", "topk", "sort")
+SCREEN_FRONT_OPS = ("route_screen", "route_select", "sort_scan", "sort_scatter")
+PATH_OPS = {"stream": ("gate_up", "requant", "down", "combine"), "tile": ("gate_up", "down", "combine")}
 
 
 def op_names(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> tuple[str, ...]:
-    return OP_NAMES if resolve_front(cfg, path, front) == "exact" else SCREEN_OP_NAMES
+    """Engine operation names of one layer call, in launch order."""
+    path = resolve_path(cfg, path)
+    front_ops = EXACT_FRONT_OPS if resolve_front(cfg, path, front) == "exact" else SCREEN_FRONT_OPS
+    return front_ops + PATH_OPS[path]
 ROUTER_H = (512, 1024, 2048, 4096)   # netra_moe_router_h<H>_gfx950
 
 
@@ -251,14 +258,18 @@ def operations(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> list[
                        u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
                  reads=["x_q", "x_scale", "w13", "w13_scale", *common, "tile_map"], writes=["h"],
                  refs=["kernels/gfx950/templates/moe/decode/gate_up_mfma.inc:12-161"]),
+            dict(name="moe.requant", symbol="netra_moe_requant_h_gfx950",
+                 grid=(STREAM_GRID_REQUANT, 1, 1), block=(256, 1, 1), lds=0, dyn=0,
+                 args=["h", "h_q", "h_scale", "tile_map", "num_valid", u(I)],
+                 reads=["h", "tile_map", "num_valid"], writes=["h_q", "h_scale"],
+                 refs=["kernels/gfx950/templates/moe/decode/silu_quant.inc:16-236"]),
             dict(name="moe.down", symbol=f"netra_moe_down_stream_i{I}_gfx950",
                  grid=(STREAM_GRID_DOWN, 1, 1), block=(256, 1, 1), lds=0, dyn=0,
-                 args=["h", "w2", "w2_scale", "sorted_ids", "sorted_expert", "tile_map",
+                 args=["h_q", "h_scale", "w2", "w2_scale", "sorted_ids", "sorted_expert", "tile_map",
                        "num_valid", "partial",
                        u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
-                 reads=["h", "w2", "w2_scale", *common, "tile_map"], writes=["partial"],
-                 refs=["kernels/gfx950/templates/moe/decode/silu_quant.inc:16-236",
-                       "kernels/gfx950/templates/moe/decode/down_reduce_mfma_2wave.inc:14-291"]),
+                 reads=["h_q", "h_scale", "w2", "w2_scale", *common, "tile_map"], writes=["partial"],
+                 refs=["kernels/gfx950/templates/moe/decode/down_reduce_mfma_2wave.inc:14-291"]),
         ]
     else:
         ops += [

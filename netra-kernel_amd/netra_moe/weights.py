@@ -98,6 +98,13 @@ def pack_tiles_host(q: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(t).reshape(g, n, k)
 
 
+def unpack_tiles_host(q: np.ndarray) -> np.ndarray:
+    """Inverse of pack_tiles_host: tile16x128 bytes [G, N, K] -> row-major."""
+    g, n, k = q.shape
+    t = q.reshape(g, n // 16, k // 128, 2, 4, 16, 16).transpose(0, 1, 5, 2, 4, 3, 6)
+    return np.ascontiguousarray(t).reshape(g, n, k)
+
+
 def unpack_h_tiles_host(h: np.ndarray, cols: int) -> np.ndarray:
     """Inverse of the decode GEMMs' tiled h layout: flat bf16 bits -> [rows, cols].
     Stored order is [row tile, K block, piece q, lane group g, row r, 8 values]

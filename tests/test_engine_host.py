@@ -14,7 +14,7 @@ import pytest
 
 import netra_moe as nm
 from netra_moe import paths, runtime
-from netra_moe.engine import OP_NAMES, SCREEN_OP_NAMES, operations
+from netra_moe.engine import op_names, operations
 
 REPO = Path(__file__).resolve().parent.parent
 
@@ -83,7 +83,9 @@ def test_emitted_engine_passes_the_native_manifest_check(engine_dir):
     st, msg = nm.manifest_check(engine_dir)
     assert st == nm.Status.OK, msg
     doc = json.loads((engine_dir / "engine.json").read_text())
-    assert [op["name"] for op in doc["operations"]] == [f"moe.{n}" for n in OP_NAMES]
+    assert [op["name"] for op in doc["operations"]] == [f"moe.{n}" for n in op_names(nm.BASELINE_CONFIGS["decode_t64"])]
+    assert op_names(nm.BASELINE_CONFIGS["decode_t64"]) == ("router", "topk", "sort", "gate_up", "requant", "down",
+                                                           "combine")
 
 
 def _corrupt(engine_dir: Path, mutate) -> tuple:
@@ -154,7 +156,8 @@ def test_prefill_engines_use_the_screen_front_end(tmp_path):
     nm.compile_moe_engine(cfg, tmp_path / "p")
     doc = json.loads((tmp_path / "p" / "engine.json").read_text())
     assert doc["front_end"] == "screen" and doc["gemm_path"] == "tile"
-    assert [op["name"] for op in doc["operations"]] == [f"moe.{n}" for n in SCREEN_OP_NAMES]
+    assert [op["name"] for op in doc["operations"]] == [f"moe.{n}" for n in op_names(cfg)]
+    assert op_names(cfg) == ("route_screen", "route_select", "sort_scan", "sort_scatter", "gate_up", "down", "combine")
     assert nm.manifest_check(tmp_path / "p")[0] == nm.Status.OK
     screen, select = doc["operations"][0], doc["operations"][1]
     assert screen["launch"]["grid"] == [64, 5, 1]  # 4096 / 64 tokens x 320 / 64 router rows

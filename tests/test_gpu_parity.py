@@ -87,24 +87,28 @@ def test_counts_sort_permutation_bit_exact(case):
 
 
 def test_gate_up_silu_quant_rows(case):
-    """FP8 h on the rows the oracle recomputes. h is bf16 before requant and the
+    """FP8 h (both paths; the stream path requantises in its own kernel) on the
+    rows the oracle recomputes. h is bf16 before requant and the
     fp32 accumulation order differs, so a group max may move by one bf16 step
     (scale ratio within 2^-7) and an element by one E4M3 step (dequantised
     difference within 1/8 relative + 1.5% for the scale); elements near zero,
     where g or u cancel, may move by up to two subnormal steps (2^-9 * scale
     each); fewer than 1% of codes may differ."""
     cfg, host, got, ref = case
-    if got["path"] != "tile":
-        pytest.skip("the stream path keeps h in bf16; see test_gate_up_h_bf16_rows")
     nv = int(ref["num_valid"][0])
     rows = min(nv, 1024)
     h_q, h_s, _ = oracle.gate_up(ref["x_q"], ref["x_scale"], host["w13"], host["w13_scale"],
                                  ref["sorted_ids"], ref["sorted_expert"], rows, cfg.T, cfg.H, cfg.I)
+    if got["path"] == "stream":  # tile16x128 FP8 tiles, scales [tile][block][row]
+        gq = W.unpack_tiles_host(got["h_q"].reshape(1, -1, cfg.I))[0]
+        gs = got["h_scale"].transpose(0, 2, 1).reshape(-1, cfg.I // 128)
+    else:
+        gq, gs = got["h_q"], got["h_scale"]
     t = ref["sorted_ids"][:rows] & 0xFFFFFF
     valid = t < cfg.T
     s_ref = h_s[:rows][valid].astype(np.float64)
-    s_got = got["h_scale"][:rows][valid].astype(np.float64)
-    q_ref, q_got = h_q[:rows][valid], got["h_q"][:rows][valid]
+    s_got = gs[:rows][valid].astype(np.float64)
+    q_ref, q_got = h_q[:rows][valid], gq[:rows][valid]
     table = oracle.e4m3_table().astype(np.float64)
     d_ref = table[q_ref] * np.repeat(s_ref, 128, axis=1)
     d_got = table[q_got] * np.repeat(s_got, 128, axis=1)

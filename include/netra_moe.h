@@ -25,21 +25,36 @@
 //       tile_map i32[CAPT], num_valid i32[4], counts i32[E+S]; T, Ktot, Etot, W, CAP)
 //       grid 1, block 1024, dynamic LDS 4*B + (8*Etot*W if that stays <= 160 KiB),
 //       B = Etot*W + 3*Etot + 34 + CAP rounded up to even
+//   prefill ("screen") front end, H in {512,1024,2048}, EMAX in {256,512}:
+//   netra_moe_route_screen_h<H>_gfx950(x, w, screen f32x2[T,RP]; T, H, rows, RP)
+//       grid (ceil(T/64), RP/64), block 256, RP = rows rounded up to 64
+//   netra_moe_route_select_h<H>_e<EMAX>_gfx950(x, w, bias, screen, logits, ids,
+//       weights, xq, xs, route_base i32[G,Etot], route_rank i32[T*Ktot];
+//       T, H, E, K, S, RP)   grid G = ceil(T/16), block 512
+//   netra_moe_sort_scan_gfx950(route_base, sorted_ids, sorted_expert, tile_map,
+//       num_valid, counts; T, Ktot, Etot, G, CAP)   grid 1, block 1024,
+//       dynamic LDS 4*(1024 + 3*Etot + 34 + CAP)
+//   netra_moe_sort_scatter_gfx950(ids, route_base, route_rank, sorted_ids;
+//       T, Ktot, Etot, CAP)   grid ceil(T*Ktot/256), block 256
 //   decode ("stream") GEMMs, H in {512,1024,2048,4096}, I in {256,512,1024,2048}:
 //   netra_moe_gate_up_stream_h<H>_gfx950(xq, xs, w13 e4m3[Etot,2I,H],
 //       w13s f32[Etot,2I/128,H/128], sorted_ids, sorted_expert, tile_map, num_valid,
-//       h bf16[CAP*64,I]; T, H, I, Ktot, Etot)   grid 512, block 256 (persistent)
-//   netra_moe_down_stream_i<I>_gfx950(h, w2 e4m3[Etot,H,I], w2s f32[Etot,H/128,I/128],
+//       h bf16[CAP*64,I] (tiled); T, H, I, Ktot, Etot)   grid 512, block 256 (persistent)
+//   netra_moe_requant_h_gfx950(h, hq e4m3[CAP*64,I] (tile16x128),
+//       hs f32[CAP*4,I/128,16], tile_map, num_valid; I)   grid 256, block 256
+//   netra_moe_down_stream_i<I>_gfx950(hq, hs, w2 e4m3[Etot,H,I], w2s f32[Etot,H/128,I/128],
 //       sorted_ids, sorted_expert, tile_map, num_valid, partial f32[T*Ktot,H];
 //       T, H, I, Ktot, Etot)   grid 1024, block 256 (persistent)
-//   prefill ("tile") GEMMs:
-//   netra_moe_gate_up_tile_gfx950(xq, xs, w13, w13s, sorted_ids, sorted_expert,
+//   prefill ("tile") GEMMs, H in {512,1024,2048,4096}, I in {256,512,1024}:
+//   netra_moe_gate_up_tile_h<H>_gfx950(xq, xs, w13, w13s, sorted_ids, sorted_expert,
 //       num_valid, hq e4m3[CAP*64,I], hs f32[CAP*64,I/128]; T, H, I, Ktot, Etot)
-//       grid (CAP, I/128), block 256
-//   netra_moe_down_tile_gfx950(hq, hs, w2, w2s, sorted_ids, sorted_expert, num_valid,
-//       partial; T, H, I, Ktot, Etot)   grid (CAP, H/256), block 256
-//   netra_moe_combine_gfx950(partial, weights, out bf16[T,H]; T, H, Ktot)
+//       grid 8*ceil(CAP*I/128/8), block 256 (items assigned XCD-major)
+//   netra_moe_down_tile_i<I>_gfx950(hq, hs, w2, w2s, sorted_ids, sorted_expert, num_valid,
+//       partial bf16[T*Ktot,H]; T, H, I, Ktot, Etot)   grid 8*ceil(CAP*H/128/8), block 256
+//   netra_moe_combine_gfx950(partial f32, weights, out bf16[T,H]; T, H, Ktot)
 //       grid (ceil(H/1024), T), block 256
+//   netra_moe_combine_bf16_gfx950(partial bf16, weights, out; T, H, Ktot)
+//       grid (ceil(H/2048), T), block 256
 //
 // with Ktot = K + S, Etot = E + S (the shared expert is expert E), W =
 // ceil(T/64) mask words per expert, CAP = ceil(T*Ktot/64) + Etot blocks,

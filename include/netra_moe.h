@@ -26,9 +26,10 @@
 //       grid 1, block 1024, dynamic LDS 4*B + (8*Etot*W if that stays <= 160 KiB),
 //       B = Etot*W + 3*Etot + 34 + CAP rounded up to even
 //   prefill ("screen") front end, H in {512,1024,2048}, EMAX in {256,512}:
-//   netra_moe_route_screen_h<H>_gfx950(x, w, screen f32x2[T,RP]; T, H, rows, RP)
-//       grid (ceil(T/64), RP/64), block 256, RP = rows rounded up to 64
-//   netra_moe_route_select_h<H>_e<EMAX>_gfx950(x, w, bias, screen, logits, ids,
+//   netra_moe_route_screen_h<H>_gfx950(x, w, screen f32[T,RP], wnorm f32[RP];
+//       T, H, rows, RP)   grid (ceil(T/64), RP/64), block 256, RP = rows
+//       rounded up to 64; workgroups with blockIdx.x == 0 write wnorm
+//   netra_moe_route_select_h<H>_e<EMAX>_gfx950(x, w, bias, screen, wnorm, logits, ids,
 //       weights, xq, xs, route_base i32[G,Etot], route_rank i32[T*Ktot];
 //       T, H, E, K, S, RP)   grid G = ceil(T/16), block 512
 //   netra_moe_sort_scan_gfx950(route_base, sorted_ids, sorted_expert, tile_map,

@@ -207,9 +207,9 @@ __device__ __forceinline__ void gate_up_stream(
   }
 }
 
-#define NK_GATE_UP_STREAM(HV)                                                                    \
-  NK_KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NK_GATE_UP_WAVES_PER_EU)))  \
-  void netra_moe_gate_up_stream_h##HV##_gfx950(                                                  \
+#define NK_GATE_UP_STREAM_V(NAME, HV, WPE)                                                       \
+  NK_KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE)))                     \
+  void NAME(                                                                                     \
       const uint8_t* __restrict__ xq, const float* __restrict__ xs,                              \
       const uint8_t* __restrict__ w13, const float* __restrict__ w13s,                           \
       const int32_t* __restrict__ sorted_ids, const int32_t* __restrict__ sorted_expert,         \
@@ -220,10 +220,15 @@ __device__ __forceinline__ void gate_up_stream(
     gate_up_stream<HV / 128>(xq, xs, w13, w13s, sorted_ids, sorted_expert, tile_map, num_valid, \
                              h, T, I, Ktot, Etot);                                               \
   }
+#define NK_GATE_UP_STREAM(HV) \
+  NK_GATE_UP_STREAM_V(netra_moe_gate_up_stream_h##HV##_gfx950, HV, NK_GATE_UP_WAVES_PER_EU)
 NK_GATE_UP_STREAM(512)
 NK_GATE_UP_STREAM(1024)
 NK_GATE_UP_STREAM(2048)
 NK_GATE_UP_STREAM(4096)
+// occupancy alternatives kept for tuning runs
+NK_GATE_UP_STREAM_V(netra_moe_gate_up_stream_h2048_o3_gfx950, 2048, 3)
+NK_GATE_UP_STREAM_V(netra_moe_gate_up_stream_h2048_o4_gfx950, 2048, 4)
 
 // ---------------------------------------------------------------------------
 // 1x128 FP8 requant of h between the decode GEMMs (reference: kernels/gfx950/
@@ -382,9 +387,9 @@ __device__ __forceinline__ void down_stream(
   }
 }
 
-#define NK_DOWN_STREAM(IV)                                                                      \
-  NK_KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NK_DOWN_WAVES_PER_EU)))    \
-  void netra_moe_down_stream_i##IV##_gfx950(                                                    \
+#define NK_DOWN_STREAM_V(NAME, IV, WPE)                                                         \
+  NK_KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE)))                     \
+  void NAME(                                                                                    \
       const uint8_t* __restrict__ hq, const float* __restrict__ hs, const uint8_t* __restrict__ w2, \
       const float* __restrict__ w2s, const int32_t* __restrict__ sorted_ids,                    \
       const int32_t* __restrict__ sorted_expert, const int32_t* __restrict__ tile_map,          \
@@ -394,7 +399,11 @@ __device__ __forceinline__ void down_stream(
     down_stream<IV / 128>(hq, hs, w2, w2s, sorted_ids, sorted_expert, tile_map, num_valid,      \
                           partial, T, H, Ktot, Etot);                                           \
   }
+#define NK_DOWN_STREAM(IV) NK_DOWN_STREAM_V(netra_moe_down_stream_i##IV##_gfx950, IV, NK_DOWN_WAVES_PER_EU)
 NK_DOWN_STREAM(256)
 NK_DOWN_STREAM(512)
 NK_DOWN_STREAM(1024)
 NK_DOWN_STREAM(2048)
+// occupancy alternatives kept for tuning runs
+NK_DOWN_STREAM_V(netra_moe_down_stream_i512_o6_gfx950, 512, 6)
+NK_DOWN_STREAM_V(netra_moe_down_stream_i512_o8_gfx950, 512, 8)

@@ -317,16 +317,20 @@ __device__ __forceinline__ void down_tile(
     constexpr uint32_t NT = decltype(ntc)::value;
 #pragma unroll
     for (uint32_t kb = 0; kb < KB; ++kb) {
+      v4f d[NT][2];  // the block's MFMAs first, into separate results
 #pragma unroll
       for (uint32_t rt = 0; rt < NT; ++rt) {
         const v8i af = lds_fp8x32(&s_buf[(rt * 16u + (lane & 15u)) * kStride + kb * 128u + g * 32u]);
-        const v4f d0 = nk::mfma_e4m3_16x16x128(af, bq[kb][0]);
-        const v4f d1 = nk::mfma_e4m3_16x16x128(af, bq[kb][1]);
+        d[rt][0] = nk::mfma_e4m3_16x16x128(af, bq[kb][0]);
+        d[rt][1] = nk::mfma_e4m3_16x16x128(af, bq[kb][1]);
+      }
+#pragma unroll
+      for (uint32_t rt = 0; rt < NT; ++rt) {
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
           const float sc = s_as[(rt * 16u + g * 4u + j) * KB + kb];
-          acc[rt][0][j] = fmaf(sc, d0[j], acc[rt][0][j]);
-          acc[rt][1][j] = fmaf(sc, d1[j], acc[rt][1][j]);
+          acc[rt][0][j] = fmaf(sc, d[rt][0][j], acc[rt][0][j]);
+          acc[rt][1][j] = fmaf(sc, d[rt][1][j], acc[rt][1][j]);
         }
       }
     }

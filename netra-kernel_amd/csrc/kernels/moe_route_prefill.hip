@@ -1,8 +1,8 @@
 // Routing front end for large token counts (prefill, T > 256), four kernels:
 //   route_screen  bf16-MFMA router GEMM over all tokens and router rows: the
-//                 approximate logit a and a bound m on its distance from the
-//                 contract logit (2^-10 * ||x|| * ||w||, Cauchy-Schwarz)
-//   route_select  one wave per token: certified candidate set from (a, m),
+//                 approximate logit a, and the router rows' norms
+//   route_select  one wave per token: certified candidate set from a and
+//                 the bound m = 2^-10 ||x|| ||w|| on |L - a| (Cauchy-Schwarz),
 //                 exact contract logits of the candidates and the shared-gate
 //                 row, top-k + weights + shared-expert append, input quant,
 //                 logits out; per 16-token workgroup expert histogram and the
@@ -103,19 +103,19 @@ __device__ __forceinline__ float exact_dot(const uint4* __restrict__ xrow, const
 // rows 64 tn .. +63. Per 128-K block the x and w tiles are staged in LDS
 // (loads for the next block in flight during this one's multiplies); wave w
 // multiplies its 16 tokens by the four 16-row tiles with
-// v_mfma_f32_16x16x32_bf16. The staging threads also accumulate the squared
-// norms of their rows. Output screen[t][e] = (a, m) for t < T, e < rows,
-// row stride RP (rows rounded up to 64).
+// v_mfma_f32_16x16x32_bf16. Output screen[t][e] = a for t < T, e < rows, row
+// stride RP (rows rounded up to 64). The workgroups of the first token tile
+// also write the router rows' norms wnorm[e] = ||w_e|| (1 + 2^-9).
 template <uint32_t NJ>  // H / 128
 __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                             float2* __restrict__ screen, uint32_t T, uint32_t rows,
-                                             uint32_t RP) {
+                                             float* __restrict__ screen, float* __restrict__ wnorm,
+                                             uint32_t T, uint32_t rows, uint32_t RP) {
   constexpr uint32_t H = 128u * NJ;
   constexpr uint32_t kStride = 136;  // bf16 per LDS row (128 + 8: rotates banks across rows)
   __shared__ __align__(16) uint16_t s_x[2][64 * kStride];
   __shared__ __align__(16) uint16_t s_w[2][64 * kStride];
-  __shared__ float s_nx[64], s_nw[64];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const bool norms = blockIdx.x == 0;  // uniform
   const uint32_t t0 = blockIdx.x * 64u, r0 = blockIdx.y * 64u;
   // staging: thread moves row (16 p + tid / 16) bytes (tid % 16) * 16 of both tiles, p = 0..3
   const uint32_t srow = tid >> 4, sc = (tid & 15u) * 8u;  // sc in bf16
@@ -133,7 +133,7 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
   // multiplied; LDS-only barriers keep them in flight
   constexpr uint32_t kRing = 3;
   uint4 xv[kRing][4], wv[kRing][4];
-  float nx[4] = {0.0f, 0.0f, 0.0f, 0.0f}, nw[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float nw[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   auto load = [&](uint32_t kb, uint32_t slot) __attribute__((always_inline)) {
 #pragma unroll
     for (uint32_t p = 0; p < 4; ++p) {
@@ -156,8 +156,7 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
     for (uint32_t p = 0; p < 4; ++p) {
       *reinterpret_cast<uint4*>(&s_x[buf][(16u * p + srow) * kStride + sc]) = xv[slot][p];
       *reinterpret_cast<uint4*>(&s_w[buf][(16u * p + srow) * kStride + sc]) = wv[slot][p];
-      nx[p] += sumsq8(xv[slot][p]);
-      nw[p] += sumsq8(wv[slot][p]);
+      if (norms) nw[p] += sumsq8(wv[slot][p]);
     }
     if (kb + 2u < NJ) load(kb + 2u, (kb + 2u) % kRing);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -172,28 +171,25 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
     }
     __builtin_amdgcn_sched_barrier(0);  // one 128-K block per schedule region
   }
-  // row norms: the 16 threads of a row hold its 16 column slices
+  if (norms) {  // router-row norms: the 16 threads of a row hold its 16 column slices
 #pragma unroll
-  for (uint32_t p = 0; p < 4; ++p) {
-    float a = nx[p], b = nw[p];
-    a += __shfl_xor(a, 1u); b += __shfl_xor(b, 1u);
-    a += __shfl_xor(a, 2u); b += __shfl_xor(b, 2u);
-    a += __shfl_xor(a, 4u); b += __shfl_xor(b, 4u);
-    a += __shfl_xor(a, 8u); b += __shfl_xor(b, 8u);
-    if ((tid & 15u) == 0) {
-      s_nx[16u * p + srow] = sqrtf(a) * kNormSlack;
-      s_nw[16u * p + srow] = sqrtf(b) * kNormSlack;
+    for (uint32_t p = 0; p < 4; ++p) {
+      float b = nw[p];
+      b += __shfl_xor(b, 1u);
+      b += __shfl_xor(b, 2u);
+      b += __shfl_xor(b, 4u);
+      b += __shfl_xor(b, 8u);
+      const uint32_t r = r0 + 16u * p + srow;
+      if ((tid & 15u) == 0 && r < rows) wnorm[r] = sqrtf(b) * kNormSlack;
     }
   }
-  __syncthreads();
 #pragma unroll
   for (uint32_t n = 0; n < 4; ++n) {
     const uint32_t r = r0 + 16u * n + rl;
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) {
-      const uint32_t tl = 16u * wave + 4u * g + i, t = t0 + tl;
-      if (t < T && r < rows)
-        screen[(size_t)t * RP + r] = make_float2(acc[n][i], kScreenMargin * s_nx[tl] * s_nw[16u * n + rl]);
+      const uint32_t t = t0 + 16u * wave + 4u * g + i;
+      if (t < T && r < rows) screen[(size_t)t * RP + r] = acc[n][i];
     }
   }
 }
@@ -201,7 +197,9 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
 // ---------------------------------------------------------------------------
 // route_select: workgroup of 8 waves for 16 tokens (a wave handles tokens
 // w and w + 8 in turn; 256 VGPRs per wave keep the exact phase in registers).
-//  1. bounds zlo/zhi of z = f32(bf16(L)) + bias from L in [a - m, a + m] (bf16
+//  0. the token row is staged in LDS, quantised (1x128) and its norm taken;
+//  1. bounds zlo/zhi of z = f32(bf16(L)) + bias from L in [a - m, a + m],
+//     m = 2^-10 ||x|| ||w_e|| (norms rounded up; bf16
 //     rounding and the bias add are monotone); theta = K-th largest zlo;
 //     candidates = {e : zhi_e >= theta} contain the true top-K, since every
 //     other expert lies strictly below K experts;
@@ -209,13 +207,14 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
 //     16-lane group at a time (the token row staged in LDS);
 //  3. top-K over the candidates' exact z (descending, ties to the lower expert
 //     index), weights, shared expert append (as the exact top-k kernel);
-//  4. logits row (the input quant of the token is done while staging its row);
+//  4. logits row;
 //  5. per workgroup: in-workgroup rank of every route among the workgroup's
 //     routes to the same expert (token order) and the per-expert histogram.
 template <uint32_t NJ, uint32_t EMAX>
 __device__ __forceinline__ void route_select(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
-    const float2* __restrict__ screen, uint16_t* __restrict__ logits, int32_t* __restrict__ ids,
+    const float* __restrict__ screen, const float* __restrict__ wnorm, uint16_t* __restrict__ logits,
+    int32_t* __restrict__ ids,
     float* __restrict__ weights, uint8_t* __restrict__ xq, float* __restrict__ xs,
     int32_t* __restrict__ hist, int32_t* __restrict__ lrank, uint32_t T, uint32_t E, uint32_t K,
     uint32_t S, uint32_t RP) {
@@ -241,8 +240,22 @@ __device__ __forceinline__ void route_select(
   for (uint32_t tt = wave; tt < kTok; tt += kThreads / 64u) {
     const uint32_t t = blockIdx.x * kTok + tt;
     if (t >= T) break;  // uniform per wave; later tokens are past T too
+    // 0. token row -> LDS, its 1x128 quant and its norm
+    float xx = 0.0f;
+#pragma unroll
+    for (uint32_t p = 0; p < H / 512u; ++p) {
+      const uint32_t i0 = 512u * p + 8u * lane;
+      const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)t * H + i0);
+      s_x[tt][64u * p + lane] = v;
+      quant8(v, xq + (size_t)t * H + i0, xs + (size_t)t * NJ + (i0 >> 7), s == 0);
+      xx += sumsq8(v);
+    }
+#pragma unroll
+    for (uint32_t off = 1; off < 64u; off <<= 1) xx += __shfl_xor(xx, off);
+    const float mx = kScreenMargin * sqrtf(xx) * kNormSlack;
+
     // 1. certified candidates
-    const float2* srow = screen + (size_t)t * RP;
+    const float* srow = screen + (size_t)t * RP;
     uint32_t clo[P], chi[P];
     float aval[P];
 #pragma unroll
@@ -251,11 +264,12 @@ __device__ __forceinline__ void route_select(
       clo[j] = chi[j] = 0u;
       aval[j] = 0.0f;
       if (e < E) {
-        const float2 am = srow[e];
+        const float a = srow[e];
+        const float m = mx * wnorm[e];
         const float b = bias[e];
-        aval[j] = am.x;
-        clo[j] = nk::order_bits(nk::bf16_f32(nk::bf16_rne(am.x - am.y)) + b);
-        chi[j] = nk::order_bits(nk::bf16_f32(nk::bf16_rne(am.x + am.y)) + b);
+        aval[j] = a;
+        clo[j] = nk::order_bits(nk::bf16_f32(nk::bf16_rne(a - m)) + b);
+        chi[j] = nk::order_bits(nk::bf16_f32(nk::bf16_rne(a + m)) + b);
       }
     }
     // theta = K-th largest zlo: the largest code with at least K codes >= it,
@@ -280,16 +294,8 @@ __device__ __forceinline__ void route_select(
       n += (uint32_t)__popcll(bal);
     }
 
-    // 2. token row -> LDS (and its 1x128 quant); exact logits: jobs 0..n-1 are
-    // the candidates, job n the shared-gate row
-#pragma unroll
-    for (uint32_t p = 0; p < H / 512u; ++p) {
-      const uint32_t i0 = 512u * p + 8u * lane;
-      const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)t * H + i0);
-      s_x[tt][64u * p + lane] = v;
-      quant8(v, xq + (size_t)t * H + i0, xs + (size_t)t * NJ + (i0 >> 7), s == 0);
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's row is in LDS
+    // 2. exact logits: jobs 0..n-1 are the candidates, job n the shared-gate row
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's row and list are in LDS
     __builtin_amdgcn_wave_barrier();
     const uint32_t jobs = n + S;
 #pragma unroll 1
@@ -419,10 +425,10 @@ __device__ __forceinline__ void route_select(
 
 #define NK_ROUTE_SCREEN(HV)                                                                       \
   NK_KERNEL __launch_bounds__(256) void netra_moe_route_screen_h##HV##_gfx950(                    \
-      const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, float2* __restrict__ screen, \
-      uint32_t T, uint32_t H, uint32_t rows, uint32_t RP) {                                       \
+      const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, float* __restrict__ screen,  \
+      float* __restrict__ wnorm, uint32_t T, uint32_t H, uint32_t rows, uint32_t RP) {            \
     (void)H;                                                                                      \
-    nkroute::route_screen<HV / 128>(x, w, screen, T, rows, RP);                                   \
+    nkroute::route_screen<HV / 128>(x, w, screen, wnorm, T, rows, RP);                            \
   }
 NK_ROUTE_SCREEN(512)
 NK_ROUTE_SCREEN(1024)
@@ -431,14 +437,14 @@ NK_ROUTE_SCREEN(2048)
 #define NK_ROUTE_SELECT(HV, EMAXV)                                                                \
   NK_KERNEL __launch_bounds__(512) void netra_moe_route_select_h##HV##_e##EMAXV##_gfx950(         \
       const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,                             \
-      const float* __restrict__ bias, const float2* __restrict__ screen,                          \
-      uint16_t* __restrict__ logits, int32_t* __restrict__ ids, float* __restrict__ weights,      \
+      const float* __restrict__ bias, const float* __restrict__ screen,                           \
+      const float* __restrict__ wnorm, uint16_t* __restrict__ logits, int32_t* __restrict__ ids, float* __restrict__ weights,      \
       uint8_t* __restrict__ xq, float* __restrict__ xs, int32_t* __restrict__ hist,               \
       int32_t* __restrict__ lrank, uint32_t T, uint32_t H, uint32_t E, uint32_t K, uint32_t S,    \
       uint32_t RP) {                                                                              \
     (void)H;                                                                                      \
-    nkroute::route_select<HV / 128, EMAXV>(x, w, bias, screen, logits, ids, weights, xq, xs,      \
-                                           hist, lrank, T, E, K, S, RP);                          \
+    nkroute::route_select<HV / 128, EMAXV>(x, w, bias, screen, wnorm, logits, ids, weights, xq,   \
+                                           xs, hist, lrank, T, E, K, S, RP);                      \
   }
 NK_ROUTE_SELECT(512, 256)
 NK_ROUTE_SELECT(1024, 256)

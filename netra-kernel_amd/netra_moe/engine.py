@@ -142,7 +142,8 @@ def tensor_table(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> dic
     if front == "exact":
         specs.append(TensorSpec("mask", "u64", (cfg.Etot, cfg.mask_words_per_expert), "temporary"))
     else:
-        specs += [TensorSpec("screen", "f32", (T, 2 * screen_row_pad(cfg)), "temporary"),
+        specs += [TensorSpec("screen", "f32", (T, screen_row_pad(cfg)), "temporary"),
+                  TensorSpec("route_wnorm", "f32", (screen_row_pad(cfg),), "temporary"),
                   TensorSpec("route_base", "i32", (screen_groups(cfg), cfg.Etot), "temporary"),
                   TensorSpec("route_rank", "i32", (T * cfg.Ktot,), "temporary")]
     if path == "stream":
@@ -181,17 +182,17 @@ def _screen_front(cfg: MoEConfig) -> list[dict]:
     RP = screen_row_pad(cfg)
     return [
         dict(name="moe.route_screen", symbol=f"netra_moe_route_screen_h{H}_gfx950",
-             grid=((T + 63) // 64, RP // 64, 1), block=(256, 1, 1), lds=2 * 2 * 64 * 136 * 2 + 2 * 64 * 4, dyn=0,
-             args=["x", "router_w", "screen", u(T), u(H), u(cfg.router_rows), u(RP)],
-             reads=["x", "router_w"], writes=["screen"],
+             grid=((T + 63) // 64, RP // 64, 1), block=(256, 1, 1), lds=2 * 2 * 64 * 136 * 2, dyn=0,
+             args=["x", "router_w", "screen", "route_wnorm", u(T), u(H), u(cfg.router_rows), u(RP)],
+             reads=["x", "router_w"], writes=["screen", "route_wnorm"],
              refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150"]),
         dict(name="moe.route_select", symbol=f"netra_moe_route_select_h{H}_e{screen_emax(cfg)}_gfx950",
              grid=(G, 1, 1), block=(512, 1, 1),
-             lds=SCREEN_TOKENS * H * 2 + 2 * SCREEN_TOKENS * (2 * screen_emax(cfg) + 1) + SCREEN_TOKENS * 64 * 4
+             lds=SCREEN_TOKENS * H * 2 + 2 * SCREEN_TOKENS * (2 * screen_emax(cfg) + 1) + SCREEN_TOKENS * 64 * 12
              + 4 * (screen_emax(cfg) + 1), dyn=0,
-             args=["x", "router_w", "router_bias", "screen", "logits", "topk_ids", "topk_weights", "x_q",
+             args=["x", "router_w", "router_bias", "screen", "route_wnorm", "logits", "topk_ids", "topk_weights", "x_q",
                    "x_scale", "route_base", "route_rank", u(T), u(H), u(cfg.E), u(cfg.K), u(cfg.S), u(RP)],
-             reads=["x", "router_w", "router_bias", "screen"],
+             reads=["x", "router_w", "router_bias", "screen", "route_wnorm"],
              writes=["logits", "topk_ids", "topk_weights", "x_q", "x_scale", "route_base", "route_rank"],
              refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150",
                    "runtime/gfx950/routing/decode/qwen36_shared_gate_append_bridge.hip:76-112"]),

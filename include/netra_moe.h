@@ -22,9 +22,10 @@
 //   netra_moe_topk_gfx950(logits, bias f32[E], ids i32[T,Ktot], weights f32[T,Ktot],
 //       mask; T, E, K, S, W)   grid ceil(T/4), block 256 (one wave per token)
 //   netra_moe_sort_gfx950(ids, mask, sorted_ids i32[CAP*64], sorted_expert i32[CAP],
-//       tile_map i32[CAPT], num_valid i32[4], counts i32[E+S]; T, Ktot, Etot, W, CAP)
+//       tile_map i32[CAPT], pair_map i32[CAP], num_valid i32[4], counts i32[E+S];
+//       T, Ktot, Etot, W, CAP)
 //       grid 1, block 1024, dynamic LDS 4*B + (8*Etot*W if that stays <= 160 KiB),
-//       B = Etot*W + 3*Etot + 34 + CAP rounded up to even
+//       B = Etot*W + 4*Etot + 51 + CAP rounded up to even
 //   prefill ("screen") front end, H in {512,1024,2048}, EMAX in {256,512}:
 //   netra_moe_route_screen_h<H>_gfx950(x, w, screen f32[T,RP], wnorm f32[RP];
 //       T, H, rows, RP)   grid (ceil(T/64), RP/64), block 256, RP = rows
@@ -33,8 +34,8 @@
 //       weights, xq, xs, route_base i32[G,Etot], route_rank i32[T*Ktot];
 //       T, H, E, K, S, RP)   grid G = ceil(T/16), block 512
 //   netra_moe_sort_scan_gfx950(route_base, sorted_ids, sorted_expert, tile_map,
-//       num_valid, counts; T, Ktot, Etot, G, CAP)   grid 1, block 1024,
-//       dynamic LDS 4*(1024 + 3*Etot + 34 + CAP)
+//       pair_map, num_valid, counts; T, Ktot, Etot, G, CAP)   grid 1, block 1024,
+//       dynamic LDS 4*(1024 + 4*Etot + 51 + CAP)
 //   netra_moe_sort_scatter_gfx950(ids, route_base, route_rank, sorted_ids;
 //       T, Ktot, Etot, CAP)   grid ceil(T*Ktot/256), block 256
 //   decode ("stream") GEMMs, H in {512,1024,2048,4096}, I in {256,512,1024,2048}:
@@ -49,7 +50,11 @@
 //   prefill ("tile") GEMMs, H in {512,1024,2048,4096}, I in {256,512,1024}:
 //   netra_moe_gate_up_tile_h<H>_gfx950(xq, xs, w13, w13s, sorted_ids, sorted_expert,
 //       num_valid, hq e4m3[CAP*64,I], hs f32[CAP*64,I/128]; T, H, I, Ktot, Etot)
-//       grid 8*ceil(CAP*I/128/8), block 256 (items assigned XCD-major)
+//       grid 8*ceil(CAP*I/128/8), block 256 (items assigned XCD-major); used for H = 4096
+//   netra_moe_gate_up_lds_h<H>_gfx950(xq, xs, w13, w13s, sorted_ids, sorted_expert,
+//       num_valid, pair_map, hq, hs; T, H, I, Ktot, Etot)   H in {512,1024,2048},
+//       grid 8*ceil(CAP*I/128/8), block 512, static LDS <= 155 KiB, T*H < 2^31;
+//       one item per (block pair, 128 h columns), assigned XCD-major
 //   netra_moe_down_tile_i<I>_gfx950(hq, hs, w2, w2s, sorted_ids, sorted_expert, num_valid,
 //       partial bf16[T*Ktot,H]; T, H, I, Ktot, Etot)   grid 8*ceil(CAP*H/128/8), block 256
 //   netra_moe_combine_gfx950(partial f32, weights, out bf16[T,H]; T, H, Ktot)

@@ -25,9 +25,13 @@ HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 # Packed fp32 VALU ops are disabled for all device code; exact fp32 contract
 # order needs contraction off (fmaf is written explicitly where wanted).
+# MFMAs take the VGPR form: otherwise the scaled-accumulate GEMM loops route
+# every product through one AGPR quad and read it back, which serialises the
+# matrix core on its own results.
 DEVICE_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall", "-Wno-unused-parameter",
 ]
 

@@ -1,0 +1,305 @@
+// Prefill gate/up GEMM with both operands staged through an LDS ring.
+//
+// A work item is (pair p, column group ng): the up to two 64-row blocks
+// pair_map[p], pair_map[p] + 1 of one expert (128 routes) against that
+// expert's 128 h columns [128 ng, 128 ng + 128) of gate and of up (256 W13
+// rows), so each weight tile read serves 128 routes. Per 128-K block (a
+// "step") the workgroup needs 16 KiB of activation rows and 32 KiB of weight
+// tiles; both are copied global -> LDS by buffer loads with the
+// LDS-destination bit (each wave instruction moves 1 KiB: lane l's 16 bytes
+// land at M0 + 16 l), two steps ahead of use, into a ring of three stages, so
+// no VGPRs hold operands in flight. Each step's copies for the next-but-one
+// step are spread over its row tiles, so the load path works while the
+// matrix core does. (A persistent variant that also ran the ring across work
+// items measured slower: its step loop could not be unrolled without spills.)
+//
+// The copies are inline assembly waited for by explicit vmcnt counts: every
+// wave issues the same six copies per step and nothing else in the K loop
+// touches vector memory, so "this wave's copies for step kb are done" is
+// vmcnt <= 6 (the next step's copies). A barrier then makes every wave's
+// copies visible to all, and (being after every read of the stage about to be
+// refilled) keeps refills behind reads.
+//
+// The 8 waves split the 128 x 256 tile as 2 (row blocks) x 4 (32 h columns:
+// 16 gate rows twice, 16 up rows twice); each holds 4 x 4 accumulators. Per
+// step: acc += (w_s * a_s) * mfma. Epilogue: h = bf16(silu(g) * u) with the
+// hardware exp2 / reciprocal / bf16 conversion (the GEMM outputs are checked
+// within a tolerance), 1x128 FP8 requant, bytes through LDS to 16-byte stores.
+// Both LDS operand layouts are the tile16x128 operand layout, so every
+// ds_read_b128 is 1 KiB contiguous across the wave.
+//
+// (reference: kernels/gfx950/templates/moe/decode/gate_up_mfma.inc:12-161,
+// silu_quant.inc:16-236; oracle tools/benchmark/export_qwen36_moe_stage1_capture.py:80-97)
+#pragma once
+#include <type_traits>
+
+#include "moe_numerics.h"
+
+#define NK_KERNEL extern "C" __global__
+
+namespace nklds {
+
+using nk::u32x4;
+using nk::v4f;
+using nk::v8i;
+
+constexpr uint32_t kThreads = 512;
+constexpr uint32_t kStages = 3;
+constexpr uint32_t kRowsPerBlock = 64;
+constexpr uint32_t kRows = 128;                   // two blocks
+constexpr uint32_t kABytes = 8u * 2048u;          // 8 row tiles
+constexpr uint32_t kBBytes = 16u * 2048u;         // 8 gate + 8 up weight tiles
+constexpr uint32_t kStageBytes = kABytes + kBBytes;
+constexpr uint32_t kCopiesPerWave = 6;            // per step: A tile (2) + gate tile (2) + up tile (2)
+constexpr uint32_t kFar = 0x80000000u;            // an offset past the activation range (T * H < 2^31): zeros
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Raw buffer descriptor (base, num_records bytes, raw dword format) in SGPRs.
+__device__ __forceinline__ u32x4 rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  u32x4 r;
+  r.x = (uint32_t)a;
+  r.y = (uint32_t)(a >> 32) & 0xffffu;
+  r.z = bytes;
+  r.w = 0x00020000u;
+  return r;
+}
+
+// 16 bytes per lane, global (rsrc + voff + soff) -> LDS (m0 + 16 * lane).
+// Offsets at or past num_records read as zeros without a memory access.
+__device__ __forceinline__ void copy16(uint32_t m0, u32x4 r, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(r), "s"(soff)
+               : "memory");
+}
+
+template <uint32_t N>
+__device__ __forceinline__ void wait_copies() {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// Barrier for LDS hand-off: waits for this wave's LDS traffic, not for its
+// copies in flight (a full __syncthreads would drain those).
+__device__ __forceinline__ void barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__device__ __forceinline__ v8i lds_operand(const uint8_t* tile, uint32_t lane) {
+  const uint4 lo = *reinterpret_cast<const uint4*>(tile + lane * 16u);
+  const uint4 hi = *reinterpret_cast<const uint4*>(tile + 1024u + lane * 16u);
+  v8i r;
+  r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
+  r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
+  return r;
+}
+
+// Item of workgroup i among n items, XCD-major (the hardware deals workgroup
+// ids to the eight XCDs in turn); false when i has none.
+__device__ __forceinline__ bool xcd_item(uint32_t i, uint32_t n, uint32_t& item) {
+  const uint32_t per = (n + 7u) / 8u;
+  item = (i % 8u) * per + i / 8u;
+  return i / 8u < per && item < n;
+}
+
+template <uint32_t KB>  // H / 128
+__device__ __forceinline__ void gate_up_lds(
+    const uint8_t* __restrict__ xq, const float* __restrict__ xs, const uint8_t* __restrict__ w13,
+    const float* __restrict__ w13s, const int32_t* __restrict__ sorted_ids,
+    const int32_t* __restrict__ sorted_expert, const int32_t* __restrict__ num_valid,
+    const int32_t* __restrict__ pair_map, uint8_t* __restrict__ hq, float* __restrict__ hs, uint32_t T,
+    uint32_t I, uint32_t Ktot, uint32_t Etot) {
+  constexpr uint32_t H = 128u * KB;
+  __shared__ __align__(16) uint8_t s_stage[kStages][kStageBytes];
+  __shared__ __align__(16) float s_as[KB][kRows];  // a_s(row, kb), rows contiguous per step
+  __shared__ int32_t s_tok[kRows];
+  __shared__ float s_amax[2][4][kRowsPerBlock];
+  __shared__ float s_scale[kRows];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
+  const uint32_t NG = I / 128u;
+  uint32_t item;
+  if (!xcd_item(blockIdx.x, (uint32_t)num_valid[3] * NG, item)) return;
+  const uint32_t p = item / NG, ng = item - p * NG;
+  const uint32_t nblocks = (uint32_t)num_valid[0] / kRowsPerBlock;
+  const uint32_t b0 = (uint32_t)pair_map[p];
+  if (b0 >= nblocks) return;
+  const int32_t e = sorted_expert[b0];
+  if (e < 0 || (uint32_t)e >= Etot) return;
+  const bool two = b0 + 1u < nblocks && sorted_expert[b0 + 1u] == e;
+  if (tid < kRows) {
+    int32_t tk = -1;
+    if (tid < kRowsPerBlock || two) {
+      const int32_t id = sorted_ids[b0 * kRowsPerBlock + tid];
+      const uint32_t t = (uint32_t)id & 0xffffffu, slot = (uint32_t)id >> 24;
+      tk = (t < T && slot < Ktot) ? (int32_t)t : -1;
+    }
+    s_tok[tid] = tk;
+  }
+  __syncthreads();
+  const uint32_t m = wave >> 2, n = wave & 3u;  // row block, 32-column quarter
+  const uint32_t nvalid = (uint32_t)__popcll(__ballot(s_tok[m * kRowsPerBlock + lane] >= 0));
+  const uint32_t ntiles = (nvalid + 15u) >> 4;
+  // activation scales of the 128 rows (zeros for padding rows)
+  for (uint32_t i = tid; i < kRows * KB; i += kThreads) {
+    const uint32_t row = i / KB, kb = i - row * KB;
+    const int32_t tk = s_tok[row];
+    s_as[kb][row] = tk >= 0 ? xs[(size_t)tk * KB + kb] : 0.0f;
+  }
+  const float* wse = w13s + (size_t)e * (2u * I / 128u) * KB;
+  const float* wsg = wse + (size_t)ng * KB;               // gate rows' 128-row block
+  const float* wsu = wse + (size_t)(I / 128u + ng) * KB;  // up rows' block
+  // copy sources: wave w moves A row tile w and weight tiles w of gate and of up
+  const int32_t atok = s_tok[wave * 16u + (lane & 15u)];
+  const uint32_t apiece = (2u * (lane >> 4)) * 16u;  // bytes of the lane's first 16-byte piece
+  const uint32_t avoff0 = atok >= 0 ? (uint32_t)atok * H + apiece : kFar;
+  const uint32_t avoff1 = atok >= 0 ? avoff0 + 16u : kFar;
+  const u32x4 ra = rsrc(xq, T * H);
+  const uint8_t* w13e = w13 + (size_t)e * 2u * I * H;
+  const u32x4 rg = rsrc(nk::tile_base(w13e, ng * 8u + wave, 0, KB), KB * 2048u);
+  const u32x4 ru = rsrc(nk::tile_base(w13e, (I >> 4) + ng * 8u + wave, 0, KB), KB * 2048u);
+  const uint32_t bvoff = lane * 16u;
+  const uint32_t lds0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_offset(&s_stage[0][0]));
+  // copy q = 0..5 of step kb (A halves, gate halves, up halves) into its stage
+  auto issue_part = [&](uint32_t kb, uint32_t q) __attribute__((always_inline)) {
+    const uint32_t st = lds0 + (kb % kStages) * kStageBytes;
+    const uint32_t half = (q & 1u) * 1024u;
+    if (q < 2u) copy16(st + wave * 2048u + half, ra, q ? avoff1 : avoff0, kb * 128u);
+    else if (q < 4u) copy16(st + kABytes + wave * 2048u + half, rg, bvoff + half, kb * 2048u);
+    else copy16(st + kABytes + (8u + wave) * 2048u + half, ru, bvoff + half, kb * 2048u);
+  };
+  auto issue = [&](uint32_t kb) __attribute__((always_inline)) {
+#pragma unroll
+    for (uint32_t q = 0; q < kCopiesPerWave; ++q) issue_part(kb, q);
+  };
+  __syncthreads();  // s_as complete; every wave has read s_tok
+  issue(0);
+  if (KB > 1) issue(1);
+  const uint32_t g = lane >> 4;
+  v4f acc[4][4];
+#pragma unroll
+  for (uint32_t i = 0; i < 4; ++i)
+#pragma unroll
+    for (uint32_t c = 0; c < 4; ++c) acc[i][c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  auto kloop = [&](auto ntc) __attribute__((always_inline)) {
+    constexpr uint32_t NT = decltype(ntc)::value;
+#pragma unroll
+    for (uint32_t kb = 0; kb < KB; ++kb) {
+      if (kb + 1u < KB) wait_copies<kCopiesPerWave>(); else wait_copies<0>();
+      barrier();
+      // the next-but-one step's copies: two before each of the first NT - 1
+      // row tiles, the rest before the last
+      constexpr uint32_t kPer = NT > 1 ? 2u : kCopiesPerWave;
+      uint32_t q = 0;
+      auto some_copies = [&](uint32_t count) __attribute__((always_inline)) {
+#pragma unroll
+        for (uint32_t u = 0; u < kCopiesPerWave; ++u)
+          if (u < count && q < kCopiesPerWave && kb + 2u < KB) { issue_part(kb + 2u, q); ++q; }
+      };
+      if (NT > 0) {
+        const uint8_t* st = s_stage[kb % kStages];
+        v8i bw[4];
+#pragma unroll
+        for (uint32_t c = 0; c < 4; ++c)  // gate tiles 2n, 2n + 1, up tiles 8 + 2n, 8 + 2n + 1
+          bw[c] = lds_operand(st + kABytes + ((c >> 1) * 8u + 2u * n + (c & 1u)) * 2048u, lane);
+        const float sg = wsg[kb], su = wsu[kb];
+#pragma unroll
+        for (uint32_t i = 0; i < NT; ++i) {
+          const uint32_t rt = 4u * m + i;
+          const v8i af = lds_operand(st + rt * 2048u, lane);
+          const float4 as4 = *reinterpret_cast<const float4*>(&s_as[kb][rt * 16u + g * 4u]);
+          some_copies(i + 1u < NT ? kPer : kCopiesPerWave);
+          v4f d[4];
+#pragma unroll
+          for (uint32_t c = 0; c < 4; ++c) d[c] = nk::mfma_e4m3_16x16x128(af, bw[c]);
+          const float as[4] = {as4.x, as4.y, as4.z, as4.w};
+#pragma unroll
+          for (uint32_t c = 0; c < 4; ++c)
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) acc[i][c][j] = fmaf((c < 2 ? sg : su) * as[j], d[c][j], acc[i][c][j]);
+        }
+      } else {
+        some_copies(kCopiesPerWave);
+      }
+    }
+  };
+  switch (ntiles) {
+    case 0: kloop(std::integral_constant<uint32_t, 0>{}); break;
+    case 1: kloop(std::integral_constant<uint32_t, 1>{}); break;
+    case 2: kloop(std::integral_constant<uint32_t, 2>{}); break;
+    case 3: kloop(std::integral_constant<uint32_t, 3>{}); break;
+    default: kloop(std::integral_constant<uint32_t, 4>{}); break;
+  }
+  // Epilogue: h = bf16(silu(g) * u); amax per row over the 128-column group;
+  // FP8 bytes through LDS (stage 0, free once every wave is past the K loop).
+  float h[4][2][4];
+#pragma unroll
+  for (uint32_t i = 0; i < 4; ++i) {
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+      float mx = 0.0f;
+#pragma unroll
+      for (uint32_t c = 0; c < 2; ++c) {
+        const float v = nk::bf16_round_hw(nk::silu_hw(acc[i][c][j]) * acc[i][2u + c][j]);
+        h[i][c][j] = v;
+        mx = fmaxf(mx, fabsf(v));
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 1u));
+      mx = fmaxf(mx, __shfl_xor(mx, 2u));
+      mx = fmaxf(mx, __shfl_xor(mx, 4u));
+      mx = fmaxf(mx, __shfl_xor(mx, 8u));
+      if ((lane & 15u) == 0) s_amax[m][n][i * 16u + g * 4u + j] = mx;
+    }
+  }
+  __syncthreads();
+  if (tid < kRows) {
+    const uint32_t mb = tid >> 6, r = tid & 63u;
+    float mx = nk::kAmaxFloor;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) mx = fmaxf(mx, s_amax[mb][q][r]);
+    const float scale = mx * nk::inv_e4m3_max();
+    s_scale[tid] = scale;
+    if (s_tok[tid] >= 0) hs[(size_t)(b0 * kRowsPerBlock + tid) * (I / 128u) + ng] = scale;
+  }
+  __syncthreads();
+  constexpr uint32_t kOut = 144;  // LDS bytes per output row (128 + 16)
+  uint8_t* s_out = s_stage[0];
+  const uint32_t ocol = n * 32u + (lane & 15u);
+#pragma unroll
+  for (uint32_t i = 0; i < 4; ++i) {
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+      const uint32_t row = m * kRowsPerBlock + i * 16u + g * 4u + j;
+      const float inv = 1.0f / s_scale[row];
+      const uint32_t q2 = nk::e4m3x4(h[i][0][j] * inv, h[i][1][j] * inv, 0.0f, 0.0f);
+      s_out[row * kOut + ocol] = (uint8_t)q2;
+      s_out[row * kOut + ocol + 16u] = (uint8_t)(q2 >> 8);
+    }
+  }
+  __syncthreads();
+  {  // 128 rows x 128 bytes: 4 threads per row, two 16-byte pieces each
+    const uint32_t row = tid >> 2, c0 = (tid & 3u) * 32u;
+    if (s_tok[row] >= 0) {
+      uint8_t* dst = hq + (size_t)(b0 * kRowsPerBlock + row) * I + ng * 128u + c0;
+      *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(&s_out[row * kOut + c0]);
+      *reinterpret_cast<uint4*>(dst + 16) = *reinterpret_cast<const uint4*>(&s_out[row * kOut + c0 + 16u]);
+    }
+  }
+}
+}  // namespace nklds
+
+#define NK_GATE_UP_LDS(HV)                                                                         \
+  NK_KERNEL __launch_bounds__(512) void netra_moe_gate_up_lds_h##HV##_gfx950(                      \
+      const uint8_t* __restrict__ xq, const float* __restrict__ xs, const uint8_t* __restrict__ w13, \
+      const float* __restrict__ w13s, const int32_t* __restrict__ sorted_ids,                      \
+      const int32_t* __restrict__ sorted_expert, const int32_t* __restrict__ num_valid,            \
+      const int32_t* __restrict__ pair_map, uint8_t* __restrict__ hq, float* __restrict__ hs,      \
+      uint32_t T, uint32_t H, uint32_t I, uint32_t Ktot, uint32_t Etot) {                          \
+    (void)H;                                                                                       \
+    nklds::gate_up_lds<HV / 128>(xq, xs, w13, w13s, sorted_ids, sorted_expert, num_valid,          \
+                                 pair_map, hq, hs, T, I, Ktot, Etot);                              \
+  }
+NK_GATE_UP_LDS(512)
+NK_GATE_UP_LDS(1024)
+NK_GATE_UP_LDS(2048)

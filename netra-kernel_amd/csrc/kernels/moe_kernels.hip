@@ -15,4 +15,5 @@
 #include "moe_route_prefill.hip"
 #include "moe_gemm_stream.hip"
 #include "moe_gemm_tile.hip"
+#include "moe_gemm_lds.hip"
 #include "moe_misc.hip"

@@ -87,6 +87,17 @@ __device__ __forceinline__ float nexp(float x) {
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + nexp(-g)); }
+
+// Epilogue forms for the GEMMs, whose outputs are checked against the oracle
+// within a tolerance (their fp32 accumulation order differs from it anyway):
+// SiLU through the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32, about
+// 1 ulp each), and bf16 rounding through the gfx950 conversion
+// (v_cvt_pk_bf16_f32, round to nearest even, the same value as bf16_rne for
+// every non-NaN input).
+__device__ __forceinline__ float silu_hw(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
+}
+__device__ __forceinline__ float bf16_round_hw(float x) { return (float)(__bf16)x; }
 __device__ __forceinline__ float sigmoid(float z) { return 1.0f / (1.0f + nexp(-z)); }
 
 // 32 contiguous FP8 bytes as one MFMA operand (two 16-byte loads).

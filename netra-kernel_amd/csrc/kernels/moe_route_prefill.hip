@@ -461,20 +461,22 @@ NK_ROUTE_SELECT(2048, 512)
 // 64 experts, then the wave totals), tiles of 16 rows likewise. hist is then
 // overwritten in place with the absolute sorted row of the first route of
 // (g, e): block_off[e] * 64 + routes of e in workgroups before g. Also writes
-// sorted_expert, tile_map, num_valid = {padded rows, routes, tiles, 0} and
+// sorted_expert, tile_map, pair_map (first block of each pair of consecutive
+// blocks of one expert), num_valid = {padded rows, routes, tiles, pairs} and
 // the padding rows (Ktot << 24) | T of sorted_ids (the scatter fills the rest).
-// Dynamic LDS: 4 * (1024 + 3 * Etot + 34 + CAP) bytes.
+// Dynamic LDS: 4 * (1024 + 4 * Etot + 51 + CAP) bytes.
 NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_scan_gfx950(
     int32_t* __restrict__ hist, int32_t* __restrict__ sorted_ids, int32_t* __restrict__ sorted_expert,
-    int32_t* __restrict__ tile_map, int32_t* __restrict__ num_valid, int32_t* __restrict__ counts,
-    uint32_t T, uint32_t Ktot, uint32_t Etot, uint32_t G, uint32_t cap_blocks) {
+    int32_t* __restrict__ tile_map, int32_t* __restrict__ pair_map, int32_t* __restrict__ num_valid,
+    int32_t* __restrict__ counts, uint32_t T, uint32_t Ktot, uint32_t Etot, uint32_t G, uint32_t cap_blocks) {
   extern __shared__ uint32_t lds[];
   uint32_t* part = lds;                      // [1024]
   uint32_t* cnt = part + 1024;               // [Etot]
   uint32_t* block_off = cnt + Etot;          // [Etot + 1]
   uint32_t* tile_off = block_off + Etot + 1; // [Etot + 1]
-  uint32_t* chunk = tile_off + Etot + 1;     // [32]
-  int32_t* owner = reinterpret_cast<int32_t*>(chunk + 32);  // [cap_blocks]
+  uint32_t* pair_off = tile_off + Etot + 1;  // [Etot + 1]
+  uint32_t* chunk = pair_off + Etot + 1;     // [48]
+  int32_t* owner = reinterpret_cast<int32_t*>(chunk + 48);  // [cap_blocks]
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   if (Etot == 0u || Etot > 1024u) return;
   const uint32_t Q = 1024u / Etot >= 4u ? 4u : 1024u / Etot;
@@ -500,26 +502,28 @@ NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_scan_gfx950(
   }
   __syncthreads();
   const uint32_t run = tid < Etot ? cnt[tid] : 0u;
-  const uint32_t vb = (run + 63u) >> 6, vt = (run + 15u) >> 4;
-  uint32_t ib = vb, it = vt;
+  const uint32_t vb = (run + 63u) >> 6, vt = (run + 15u) >> 4, vp = (vb + 1u) >> 1;
+  uint32_t ib = vb, it = vt, ip = vp;
 #pragma unroll
   for (uint32_t off = 1; off < 64; off <<= 1) {
     const uint32_t ob = __shfl_up(ib, off);
     const uint32_t ot = __shfl_up(it, off);
-    if (lane >= off) { ib += ob; it += ot; }
+    const uint32_t op = __shfl_up(ip, off);
+    if (lane >= off) { ib += ob; it += ot; ip += op; }
   }
-  if (lane == 63u) { chunk[wave] = ib; chunk[16u + wave] = it; }
+  if (lane == 63u) { chunk[wave] = ib; chunk[16u + wave] = it; chunk[32u + wave] = ip; }
   __syncthreads();
-  uint32_t cb = 0, ct = 0, total = 0, total_t = 0;
+  uint32_t cb = 0, ct = 0, cp = 0, total = 0, total_t = 0, total_p = 0;
 #pragma unroll
   for (uint32_t c = 0; c < 16u; ++c) {
-    const uint32_t b = chunk[c], t = chunk[16u + c];
-    if (c < wave) { cb += b; ct += t; }
+    const uint32_t b = chunk[c], t = chunk[16u + c], q = chunk[32u + c];
+    if (c < wave) { cb += b; ct += t; cp += q; }
     total += b;
     total_t += t;
+    total_p += q;
   }
-  if (tid < Etot) { block_off[tid] = cb + ib - vb; tile_off[tid] = ct + it - vt; }
-  if (tid == 0) { block_off[Etot] = total; tile_off[Etot] = total_t; }
+  if (tid < Etot) { block_off[tid] = cb + ib - vb; tile_off[tid] = ct + it - vt; pair_off[tid] = cp + ip - vp; }
+  if (tid == 0) { block_off[Etot] = total; tile_off[Etot] = total_t; pair_off[Etot] = total_p; }
   const uint32_t cap_tiles = (T * Ktot + 15u) / 16u + Etot;
   if (total > cap_blocks || total_t > cap_tiles) {  // impossible for route_screen histograms; write nothing
     if (tid == 0) { num_valid[0] = 0; num_valid[1] = -1; num_valid[2] = 0; num_valid[3] = 0; }
@@ -540,12 +544,14 @@ NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_scan_gfx950(
     for (uint32_t b = b0; b < b1; ++b) owner[b] = (int32_t)tid;
     const uint32_t i0 = tile_off[tid], i1 = tile_off[tid + 1u];
     for (uint32_t i = i0; i < i1; ++i) tile_map[i] = (int32_t)(b0 * 4u + (i - i0));
+    const uint32_t p0 = pair_off[tid], p1 = pair_off[tid + 1u];
+    for (uint32_t i = p0; i < p1; ++i) pair_map[i] = (int32_t)(b0 + 2u * (i - p0));
   }
   if (tid == 0) {
     num_valid[0] = (int32_t)(total * 64u);
     num_valid[1] = (int32_t)(T * Ktot);
     num_valid[2] = (int32_t)total_t;
-    num_valid[3] = 0;
+    num_valid[3] = (int32_t)total_p;
   }
   __syncthreads();
   for (uint32_t b = tid; b < cap_blocks; b += 1024u) sorted_expert[b] = owner[b];

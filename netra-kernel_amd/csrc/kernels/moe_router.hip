@@ -248,7 +248,10 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_topk_gfx950(
 // expert's tokens hold (Ktot << 24) | T; unused block entries hold -1. Also
 // lists the non-empty 16-row tiles, expert by expert: tile_map[i] = block * 4 +
 // tile-in-block for i < num_valid[2] (the decode GEMMs take one tile per work
-// item). num_valid = {padded rows, routes, tiles, 0}. The routing ids of the
+// item), and the 128-row chunks: pair_map[i] = first block of the i-th pair
+// of consecutive blocks of one expert (an expert's last block may stand
+// alone), i < num_valid[3]. num_valid = {padded rows, routes, tiles, pairs}.
+// The routing ids of the
 // first kSortPrefetch rounds are loaded before the count so their latency
 // overlaps, and when it fits (sort_mask_in_lds) the bitmask is kept in LDS for
 // the scatter. Dynamic LDS: sort_lds_words(...) * 4 bytes.
@@ -256,7 +259,7 @@ constexpr uint32_t kSortPrefetch = 4;
 constexpr uint32_t kSortLdsLimit = 160u * 1024u;
 
 __host__ __device__ constexpr uint32_t sort_base_words(uint32_t Etot, uint32_t W, uint32_t cap) {
-  return (Etot * W + 3u * Etot + 2u + 32u + cap + 1u) & ~1u;  // even: the mask copy is 8-byte aligned
+  return (Etot * W + 4u * Etot + 3u + 48u + cap + 1u) & ~1u;  // even: the mask copy is 8-byte aligned
 }
 __host__ __device__ constexpr bool sort_mask_in_lds(uint32_t Etot, uint32_t W, uint32_t cap) {
   return 4u * (sort_base_words(Etot, W, cap) + 2u * Etot * W) <= kSortLdsLimit;
@@ -265,7 +268,7 @@ __host__ __device__ constexpr bool sort_mask_in_lds(uint32_t Etot, uint32_t W, u
 NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_gfx950(
     const int32_t* __restrict__ ids, const unsigned long long* __restrict__ mask,
     int32_t* __restrict__ sorted_ids, int32_t* __restrict__ sorted_expert,
-    int32_t* __restrict__ tile_map, int32_t* __restrict__ num_valid,
+    int32_t* __restrict__ tile_map, int32_t* __restrict__ pair_map, int32_t* __restrict__ num_valid,
     int32_t* __restrict__ counts, uint32_t T, uint32_t Ktot, uint32_t Etot, uint32_t W,
     uint32_t cap_blocks) {
   extern __shared__ uint32_t lds[];
@@ -273,8 +276,9 @@ NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_gfx950(
   uint32_t* block_off = prefix + Etot * W;                 // [Etot + 1]
   uint32_t* cnt = block_off + Etot + 1;                    // [Etot]
   uint32_t* tile_off = cnt + Etot;                         // [Etot + 1]
-  uint32_t* chunk = tile_off + Etot + 1;                   // [32]: wave totals (blocks, tiles)
-  int32_t* owner = reinterpret_cast<int32_t*>(chunk + 32); // [cap_blocks]
+  uint32_t* pair_off = tile_off + Etot + 1;                // [Etot + 1]
+  uint32_t* chunk = pair_off + Etot + 1;                   // [48]: wave totals (blocks, tiles, pairs)
+  int32_t* owner = reinterpret_cast<int32_t*>(chunk + 48); // [cap_blocks]
   unsigned long long* mcopy =
       reinterpret_cast<unsigned long long*>(lds + sort_base_words(Etot, W, cap_blocks));  // [Etot * W]
   const bool mlds = sort_mask_in_lds(Etot, W, cap_blocks);
@@ -299,27 +303,29 @@ NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_gfx950(
     cnt[tid] = run;
     counts[tid] = (int32_t)run;
   }
-  const uint32_t vb = (run + 63u) >> 6, vt = (run + 15u) >> 4;
-  uint32_t ib = vb, it = vt;
+  const uint32_t vb = (run + 63u) >> 6, vt = (run + 15u) >> 4, vp = (vb + 1u) >> 1;
+  uint32_t ib = vb, it = vt, ip = vp;
 #pragma unroll
   for (uint32_t off = 1; off < 64; off <<= 1) {
     const uint32_t ob = __shfl_up(ib, off);
     const uint32_t ot = __shfl_up(it, off);
-    if (lane >= off) { ib += ob; it += ot; }
+    const uint32_t op = __shfl_up(ip, off);
+    if (lane >= off) { ib += ob; it += ot; ip += op; }
   }
-  if (lane == 63u) { chunk[wave] = ib; chunk[16u + wave] = it; }
+  if (lane == 63u) { chunk[wave] = ib; chunk[16u + wave] = it; chunk[32u + wave] = ip; }
   for (uint32_t b = tid; b < cap_blocks; b += 1024u) owner[b] = -1;
   __syncthreads();
-  uint32_t cb = 0, ct = 0, total = 0, total_t = 0;
+  uint32_t cb = 0, ct = 0, cp = 0, total = 0, total_t = 0, total_p = 0;
 #pragma unroll
   for (uint32_t c = 0; c < 16u; ++c) {
-    const uint32_t b = chunk[c], t = chunk[16u + c];
-    if (c < wave) { cb += b; ct += t; }
+    const uint32_t b = chunk[c], t = chunk[16u + c], q = chunk[32u + c];
+    if (c < wave) { cb += b; ct += t; cp += q; }
     total += b;
     total_t += t;
+    total_p += q;
   }
-  if (tid < Etot) { block_off[tid] = cb + ib - vb; tile_off[tid] = ct + it - vt; }
-  if (tid == 0) { block_off[Etot] = total; tile_off[Etot] = total_t; }
+  if (tid < Etot) { block_off[tid] = cb + ib - vb; tile_off[tid] = ct + it - vt; pair_off[tid] = cp + ip - vp; }
+  if (tid == 0) { block_off[Etot] = total; tile_off[Etot] = total_t; pair_off[Etot] = total_p; }
   const uint32_t cap_tiles = (T * Ktot + 15u) / 16u + Etot;
   if (total > cap_blocks || total_t > cap_tiles) {  // impossible for ids from the top-k kernel; write nothing
     if (tid == 0) { num_valid[0] = 0; num_valid[1] = -1; num_valid[2] = 0; num_valid[3] = 0; }
@@ -331,12 +337,14 @@ NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_gfx950(
     for (uint32_t b = b0; b < b1; ++b) owner[b] = (int32_t)tid;
     const uint32_t i0 = tile_off[tid], i1 = tile_off[tid + 1u];
     for (uint32_t i = i0; i < i1; ++i) tile_map[i] = (int32_t)(b0 * 4u + (i - i0));
+    const uint32_t p0 = pair_off[tid], p1 = pair_off[tid + 1u];
+    for (uint32_t i = p0; i < p1; ++i) pair_map[i] = (int32_t)(b0 + 2u * (i - p0));
   }
   if (tid == 0) {
     num_valid[0] = (int32_t)(total * 64u);
     num_valid[1] = (int32_t)routes;
     num_valid[2] = (int32_t)total_t;
-    num_valid[3] = 0;
+    num_valid[3] = (int32_t)total_p;
   }
   __syncthreads();
 

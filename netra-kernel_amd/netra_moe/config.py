@@ -76,10 +76,11 @@ class MoEConfig:
     @property
     def sort_lds_bytes(self) -> int:
         """Dynamic LDS of the sort kernel (sort_base_words / sort_mask_in_lds
-        in moe_router.hip): prefix, offsets, wave totals and block owners, plus
+        in moe_router.hip): prefix, block / tile / pair offsets, wave totals and
+        block owners, plus
         a copy of the routing bitmask when the total stays within 160 KiB."""
         ew = self.Etot * self.mask_words_per_expert
-        base = (ew + 3 * self.Etot + 2 + 32 + self.cap_blocks + 1) & ~1
+        base = (ew + 4 * self.Etot + 3 + 48 + self.cap_blocks + 1) & ~1
         with_mask = 4 * (base + 2 * ew)
         return with_mask if with_mask <= 160 * 1024 else 4 * base
 

@@ -55,6 +55,7 @@ STREAM_I = (256, 512, 1024, 2048)    # netra_moe_down_stream_i<I>_gfx950
 TILE_H = (512, 1024, 2048, 4096)     # netra_moe_gate_up_tile_h<H>_gfx950
 TILE_I = (256, 512, 1024)            # netra_moe_down_tile_i<I>_gfx950
 TILE_GU_WAVES = 4                    # waves of netra_moe_gate_up_tile_h<H>_gfx950 (its launch bound)
+LDS_GU_H = (512, 1024, 2048)         # netra_moe_gate_up_lds_h<H>_gfx950: 128-row pairs, LDS operand ring
 # Persistent stream kernels: 256 CUs x 4 SIMDs x resident waves per SIMD
 # (NK_GATE_UP_WAVES_PER_EU = 2, NK_DOWN_WAVES_PER_EU = 4) / 4 waves per group.
 STREAM_GRID_GATE_UP = 512
@@ -136,6 +137,7 @@ def tensor_table(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> dic
         TensorSpec("sorted_ids", "i32", (cfg.cap_rows,), "temporary"),
         TensorSpec("sorted_expert", "i32", (cfg.cap_blocks,), "temporary"),
         TensorSpec("tile_map", "i32", (cfg.cap_tiles,), "temporary"),
+        TensorSpec("pair_map", "i32", (cfg.cap_blocks,), "temporary"),
         TensorSpec("num_valid", "i32", (4,), "temporary"),
         TensorSpec("expert_counts", "i32", (cfg.Etot,), "temporary"),
     ]
@@ -198,11 +200,12 @@ def _screen_front(cfg: MoEConfig) -> list[dict]:
                    "runtime/gfx950/routing/decode/qwen36_shared_gate_append_bridge.hip:76-112"]),
         dict(name="moe.sort_scan", symbol="netra_moe_sort_scan_gfx950",
              grid=(1, 1, 1), block=(1024, 1, 1), lds=0,
-             dyn=4 * (1024 + 3 * cfg.Etot + 34 + cfg.cap_blocks),
-             args=["route_base", "sorted_ids", "sorted_expert", "tile_map", "num_valid", "expert_counts",
-                   u(T), u(cfg.Ktot), u(cfg.Etot), u(G), u(cfg.cap_blocks)],
+             dyn=4 * (1024 + 4 * cfg.Etot + 51 + cfg.cap_blocks),
+             args=["route_base", "sorted_ids", "sorted_expert", "tile_map", "pair_map", "num_valid",
+                   "expert_counts", u(T), u(cfg.Ktot), u(cfg.Etot), u(G), u(cfg.cap_blocks)],
              reads=["route_base"],
-             writes=["route_base", "sorted_ids", "sorted_expert", "tile_map", "num_valid", "expert_counts"],
+             writes=["route_base", "sorted_ids", "sorted_expert", "tile_map", "pair_map", "num_valid",
+                     "expert_counts"],
              refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]),
         dict(name="moe.sort_scatter", symbol="netra_moe_sort_scatter_gfx950",
              grid=((T * cfg.Ktot + 255) // 256, 1, 1), block=(256, 1, 1), lds=0, dyn=0,
@@ -240,11 +243,11 @@ def operations(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> list[
                    "tools/benchmark/export_qwen36_shared_gate_append_capture.py:97-107,134-139"]),
         dict(name="moe.sort", symbol="netra_moe_sort_gfx950",
              grid=(1, 1, 1), block=(1024, 1, 1), lds=0, dyn=cfg.sort_lds_bytes,
-             args=["topk_ids", "mask", "sorted_ids", "sorted_expert", "tile_map", "num_valid",
+             args=["topk_ids", "mask", "sorted_ids", "sorted_expert", "tile_map", "pair_map", "num_valid",
                    "expert_counts",
                    u(T), u(cfg.Ktot), u(cfg.Etot), u(W), u(cfg.cap_blocks)],
              reads=["topk_ids", "mask"],
-             writes=["sorted_ids", "sorted_expert", "tile_map", "num_valid", "expert_counts"],
+             writes=["sorted_ids", "sorted_expert", "tile_map", "pair_map", "num_valid", "expert_counts"],
              refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]),
     ]
     if front == "screen":
@@ -273,15 +276,30 @@ def operations(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> list[
                  refs=["kernels/gfx950/templates/moe/decode/down_reduce_mfma_2wave.inc:14-291"]),
         ]
     else:
+        if H in LDS_GU_H:
+            if T * H >= 1 << 31:
+                raise ValueError("netra_moe_gate_up_lds needs T * H < 2^31 (32-bit activation offsets)")
+            gate_up = dict(
+                name="moe.gate_up", symbol=f"netra_moe_gate_up_lds_h{H}_gfx950",
+                grid=(xcd_grid(cfg.cap_blocks * (I // 128)), 1, 1), block=(512, 1, 1),
+                lds=3 * 48 * 1024 + 128 * (H // 128) * 4 + 128 * 4 + 2 * 4 * 64 * 4 + 128 * 4, dyn=0,
+                args=["x_q", "x_scale", "w13", "w13_scale", *common, "pair_map", "h_q", "h_scale",
+                      u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
+                reads=["x_q", "x_scale", "w13", "w13_scale", *common, "pair_map"], writes=["h_q", "h_scale"],
+                refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/gate_up.inc",
+                      "kernels/gfx950/templates/moe/prefill/fused_splitk2/silu_quant.inc"])
+        else:
+            gate_up = dict(
+                name="moe.gate_up", symbol=f"netra_moe_gate_up_tile_h{H}_gfx950",
+                grid=(xcd_grid(cfg.cap_blocks * (I // 128)), 1, 1), block=(64 * TILE_GU_WAVES, 1, 1),
+                lds=2 * 64 * 144 + 2 * 64 * (H // 128) * 4 + 64 * 4 + TILE_GU_WAVES * 64 * 4 + 64 * 4, dyn=0,
+                args=["x_q", "x_scale", "w13", "w13_scale", *common, "h_q", "h_scale",
+                      u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
+                reads=["x_q", "x_scale", "w13", "w13_scale", *common], writes=["h_q", "h_scale"],
+                refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/gate_up.inc",
+                      "kernels/gfx950/templates/moe/prefill/fused_splitk2/silu_quant.inc"])
         ops += [
-            dict(name="moe.gate_up", symbol=f"netra_moe_gate_up_tile_h{H}_gfx950",
-                 grid=(xcd_grid(cfg.cap_blocks * (I // 128)), 1, 1), block=(64 * TILE_GU_WAVES, 1, 1),
-                 lds=2 * 64 * 144 + 2 * 64 * (H // 128) * 4 + 64 * 4 + TILE_GU_WAVES * 64 * 4 + 64 * 4, dyn=0,
-                 args=["x_q", "x_scale", "w13", "w13_scale", *common, "h_q", "h_scale",
-                       u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
-                 reads=["x_q", "x_scale", "w13", "w13_scale", *common], writes=["h_q", "h_scale"],
-                 refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/gate_up.inc",
-                       "kernels/gfx950/templates/moe/prefill/fused_splitk2/silu_quant.inc"]),
+            gate_up,
             dict(name="moe.down", symbol=f"netra_moe_down_tile_i{I}_gfx950",
                  grid=(xcd_grid(cfg.cap_blocks * (H // 128)), 1, 1), block=(256, 1, 1),
                  lds=max(64 * (I + 16), 64 * 272) + 64 * (I // 128) * 4 + 64 * 4, dyn=0,

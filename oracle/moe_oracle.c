@@ -247,11 +247,13 @@ int64_t orc_capacity_blocks(int64_t T, int64_t Ktot, int64_t Etot, int64_t BM) {
  * (expert, token) order.  Pads fill every unused row with (Ktot << 24) | T;
  * unused expert-block entries are -1.  The non-empty 16-row tiles are listed
  * expert by expert as block * 4 + tile-in-block (tile_map, capacity
- * ceil(routes / 16) + Etot, may be NULL).
- * num_valid = {padded rows, routes, tiles, 0}. */
+ * ceil(routes / 16) + Etot, may be NULL), and each expert's blocks two at a
+ * time by the first of the two (pair_map, capacity cap_blocks, may be NULL;
+ * an expert's last block stands alone when its block count is odd).
+ * num_valid = {padded rows, routes, tiles, pairs}. */
 int64_t orc_sort(const int32_t* ids, int64_t T, int64_t Ktot, int64_t Etot, int64_t BM,
                  int64_t cap_blocks, int32_t* sorted_ids, int32_t* sorted_expert,
-                 int32_t* tile_map, int32_t* num_valid, int32_t* counts) {
+                 int32_t* tile_map, int32_t* pair_map, int32_t* num_valid, int32_t* counts) {
   int64_t* off = (int64_t*)calloc((size_t)Etot, sizeof(int64_t));
   int64_t* cur = (int64_t*)calloc((size_t)Etot, sizeof(int64_t));
   for (int64_t e = 0; e < Etot; ++e) counts[e] = 0;
@@ -278,10 +280,16 @@ int64_t orc_sort(const int32_t* ids, int64_t T, int64_t Ktot, int64_t Etot, int6
       if (tile_map) tile_map[tiles] = (int32_t)(off[e] * (BM / 16) + j);
       ++tiles;
     }
+  int64_t pairs = 0;
+  for (int64_t e = 0; e < Etot; ++e)
+    for (int64_t j = 0; j < (counts[e] + BM - 1) / BM; j += 2) {
+      if (pair_map) pair_map[pairs] = (int32_t)(off[e] + j);
+      ++pairs;
+    }
   num_valid[0] = (int32_t)(blocks * BM);
   num_valid[1] = (int32_t)(T * Ktot);
   num_valid[2] = (int32_t)tiles;
-  num_valid[3] = 0;
+  num_valid[3] = (int32_t)pairs;
   free(off);
   free(cur);
   return blocks * BM;

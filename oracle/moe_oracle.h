@@ -50,11 +50,12 @@ void orc_topk(const uint16_t* logits, const float* bias, int64_t T, int64_t E,
 int64_t orc_capacity_blocks(int64_t T, int64_t Ktot, int64_t Etot, int64_t BM);
 /* Returns the number of padded rows (num_valid_ids[0]) or -1 on bad input.
  * tile_map (may be NULL) lists non-empty 16-row tiles as block * 4 + tile;
- * num_valid = {padded rows, routes, tiles, 0}. */
+ * pair_map (may be NULL) lists each expert's blocks two at a time by the
+ * first block of the two; num_valid = {padded rows, routes, tiles, pairs}. */
 int64_t orc_sort(const int32_t* ids, int64_t T, int64_t Ktot, int64_t Etot,
                  int64_t BM, int64_t cap_blocks, int32_t* sorted_ids,
-                 int32_t* sorted_expert, int32_t* tile_map, int32_t* num_valid,
-                 int32_t* counts);
+                 int32_t* sorted_expert, int32_t* tile_map, int32_t* pair_map,
+                 int32_t* num_valid, int32_t* counts);
 
 /* ---- grouped GEMMs (a6 + a7, a8) ---------------------------------------- */
 /* Gate/up + SiLU.mul + 1x128 requant over sorted rows.

@@ -44,7 +44,7 @@ def lib() -> ctypes.CDLL:
         L.orc_router_logits.argtypes = [P, P, I64, I64, I64, P, I]
         L.orc_topk.argtypes = [P, P, I64, I64, I64, I64, P, P]
         L.orc_capacity_blocks.argtypes = [I64, I64, I64, I64]; L.orc_capacity_blocks.restype = I64
-        L.orc_sort.argtypes = [P, I64, I64, I64, I64, I64, P, P, P, P, P]; L.orc_sort.restype = I64
+        L.orc_sort.argtypes = [P, I64, I64, I64, I64, I64, P, P, P, P, P, P]; L.orc_sort.restype = I64
         L.orc_gate_up.argtypes = [P, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P, I]
         L.orc_down_combine.argtypes = [P, P, P, P, P, P, I64, P, I64, I64, I64, I64, I64, P, P, P, I]
         L.orc_moe_tokens.argtypes = [P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, P, P, I]
@@ -131,21 +131,22 @@ def capacity_blocks(T: int, Ktot: int, Etot: int, bm: int = BLOCK_M) -> int:
 
 def sort(ids: np.ndarray, Etot: int, cap_blocks: int | None = None, bm: int = BLOCK_M,
          with_tiles: bool = False):
-    """a4: (sorted_ids, sorted_expert, num_valid, counts[, tile_map])."""
+    """a4: (sorted_ids, sorted_expert, num_valid, counts[, tile_map, pair_map])."""
     ids = np.ascontiguousarray(ids, dtype=np.int32)
     T, Ktot = ids.shape
     cap = cap_blocks if cap_blocks is not None else capacity_blocks(T, Ktot, Etot, bm)
     sid = np.empty(cap * bm, np.int32)
     sexp = np.empty(cap, np.int32)
     tmap = np.full((T * Ktot + 15) // 16 + Etot, -1, np.int32)
+    pmap = np.full(cap, -1, np.int32)
     nv = np.empty(4, np.int32)
     counts = np.empty(Etot, np.int32)
-    rows = lib().orc_sort(_p(ids), T, Ktot, Etot, bm, cap, _p(sid), _p(sexp), _p(tmap), _p(nv),
-                          _p(counts))
+    rows = lib().orc_sort(_p(ids), T, Ktot, Etot, bm, cap, _p(sid), _p(sexp), _p(tmap), _p(pmap),
+                          _p(nv), _p(counts))
     if rows < 0:
         raise ValueError("invalid routing ids or capacity too small")
     if with_tiles:
-        return sid, sexp, nv, counts, tmap
+        return sid, sexp, nv, counts, tmap, pmap
     return sid, sexp, nv, counts
 
 

@@ -13,7 +13,7 @@ from netra_moe.layer import MoELayer
 from netra_moe import weights as W
 
 ROUTING = ("logits", "topk_ids", "topk_weights", "x_q", "x_scale", "sorted_ids",
-           "sorted_expert", "tile_map", "num_valid", "expert_counts", "partial")
+           "sorted_expert", "tile_map", "pair_map", "num_valid", "expert_counts", "partial")
 PATH_INTERMEDIATES = {"stream": ("h", "h_q", "h_scale"), "tile": ("h_q", "h_scale")}
 FRONT_INTERMEDIATES = {"exact": ("mask",), "screen": ()}
 
@@ -84,10 +84,10 @@ def oracle_routing(cfg: MoEConfig, host: dict) -> dict:
     logits = oracle.router_logits(host["x"], host["router_w"])
     ids, wts = oracle.topk(logits, host["router_bias"], cfg.E, cfg.K, cfg.S)
     x_q, x_s = oracle.quant_rows_bf16(host["x"])
-    sid, sexp, nv, counts, tmap = oracle.sort(ids, cfg.Etot, cfg.cap_blocks, with_tiles=True)
+    sid, sexp, nv, counts, tmap, pmap = oracle.sort(ids, cfg.Etot, cfg.cap_blocks, with_tiles=True)
     return dict(logits=logits, topk_ids=ids, topk_weights=wts, x_q=x_q, x_scale=x_s,
                 sorted_ids=sid, sorted_expert=sexp, num_valid=nv, expert_counts=counts,
-                tile_map=tmap)
+                tile_map=tmap, pair_map=pmap)
 
 
 def sample_tokens(cfg: MoEConfig, n: int) -> np.ndarray:

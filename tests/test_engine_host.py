@@ -162,6 +162,9 @@ def test_prefill_engines_use_the_screen_front_end(tmp_path):
     screen, select = doc["operations"][0], doc["operations"][1]
     assert screen["launch"]["grid"] == [64, 5, 1]  # 4096 / 64 tokens x 320 / 64 router rows
     assert select["launch"]["grid"] == [256, 1, 1] and select["launch"]["lds_bytes"] <= 160 * 1024
+    gate_up = doc["operations"][4]
+    assert gate_up["kernel_symbol"] == "netra_moe_gate_up_lds_h2048_gfx950"
+    assert gate_up["launch"]["block"] == [512, 1, 1] and gate_up["launch"]["lds_bytes"] <= 160 * 1024
 
 
 def test_profiles_select_exact_shapes_and_refuse_neighbours():

@@ -84,6 +84,8 @@ def test_counts_sort_permutation_bit_exact(case):
     np.testing.assert_array_equal(got["sorted_ids"], ref["sorted_ids"])
     ntiles = int(ref["num_valid"][2])
     np.testing.assert_array_equal(got["tile_map"][:ntiles], ref["tile_map"][:ntiles])
+    npairs = int(ref["num_valid"][3])
+    np.testing.assert_array_equal(got["pair_map"][:npairs], ref["pair_map"][:npairs])
 
 
 def test_gate_up_silu_quant_rows(case):

@@ -117,17 +117,19 @@ def _brute_sort(ids, Etot, bm=64):
     counts = [0] * Etot
     for e in ids.reshape(-1):
         counts[e] += 1
-    rows, experts, tiles = [], [], []
+    rows, experts, tiles, pairs = [], [], [], []
     for e in range(Etot):
         mine = sorted((t, s) for t in range(T) for s in range(Ktot) if ids[t, s] == e)
         nb = -(-len(mine) // bm)
+        first = len(experts)
         for b in range(nb):
             experts.append(e)
         for j in range(-(-len(mine) // 16)):
-            tiles.append((len(experts) - nb) * (bm // 16) + j)
+            tiles.append(first * (bm // 16) + j)
+        pairs += list(range(first, first + nb, 2))  # consecutive blocks of e, two at a time
         ent = [(s << 24) | t for t, s in mine]
         rows += ent + [(Ktot << 24) | T] * (nb * bm - len(ent))
-    return rows, experts, counts, tiles
+    return rows, experts, counts, tiles, pairs
 
 
 @pytest.mark.parametrize("T,K,E,S,seed", [(16, 2, 16, 0, 1), (64, 8, 256, 1, 2), (5, 3, 7, 1, 3), (1, 8, 256, 1, 4)])
@@ -135,10 +137,11 @@ def test_sort_matches_brute_force(T, K, E, S, seed):
     rng = np.random.default_rng(seed)
     ids = np.stack([np.concatenate([rng.choice(E, K, replace=False), [E] * S]) for _ in range(T)]).astype(np.int32)
     Etot, Ktot = E + S, K + S
-    sid, sexp, nv, counts, tmap = oracle.sort(ids, Etot, with_tiles=True)
-    rows, experts, cnt, tiles = _brute_sort(ids, Etot)
+    sid, sexp, nv, counts, tmap, pmap = oracle.sort(ids, Etot, with_tiles=True)
+    rows, experts, cnt, tiles, pairs = _brute_sort(ids, Etot)
     assert counts.tolist() == cnt and sum(cnt) == T * Ktot
-    assert nv.tolist() == [len(rows), T * Ktot, len(tiles), 0]
+    assert nv.tolist() == [len(rows), T * Ktot, len(tiles), len(pairs)]
+    assert pmap[: len(pairs)].tolist() == pairs
     assert sid[: len(rows)].tolist() == rows
     assert np.all(sid[len(rows):] == ((Ktot << 24) | T))
     assert sexp[: len(experts)].tolist() == experts and np.all(sexp[len(experts):] == -1)

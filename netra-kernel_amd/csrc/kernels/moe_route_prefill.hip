@@ -455,8 +455,8 @@ NK_ROUTE_SELECT(2048, 512)
 
 // ---------------------------------------------------------------------------
 // sort_scan (one 1024-thread workgroup): hist[g][e] holds the routes of
-// route_screen workgroup g to expert e. Teams of Q = min(4, 1024 / Etot)
-// threads own one expert each and split the G workgroups; counts[e] is the
+// route_select workgroup g to expert e. Teams of (Etot rounded up to 64)
+// threads, one thread per expert, split the G workgroups; counts[e] is the
 // total, experts get ceil(count / 64) blocks in expert order (wave scans of
 // 64 experts, then the wave totals), tiles of 16 rows likewise. hist is then
 // overwritten in place with the absolute sorted row of the first route of
@@ -479,13 +479,16 @@ NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_scan_gfx950(
   int32_t* owner = reinterpret_cast<int32_t*>(chunk + 48);  // [cap_blocks]
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   if (Etot == 0u || Etot > 1024u) return;
-  const uint32_t Q = 1024u / Etot >= 4u ? 4u : 1024u / Etot;
-  const uint32_t e = tid / Q, q = tid - e * Q;
-  const bool member = e < Etot;
-  const uint32_t g0 = (G * q) / Q, g1 = (G * (q + 1u)) / Q;
+  // Teams of Ep (experts rounded up to a whole wave) threads split the G
+  // groups; a wave reads 64 consecutive experts of one group row, and each
+  // thread keeps 32 loads of its column in flight.
+  const uint32_t Ep = (Etot + 63u) & ~63u, NTm = 1024u / Ep;
+  const uint32_t k = tid / Ep, e = tid - k * Ep;
+  const bool member = k < NTm && e < Etot;
+  const uint32_t g0 = (G * k) / NTm, g1 = (G * (k + 1u)) / NTm;
   uint32_t sum = 0u;
   if (member) {
-#pragma unroll 16
+#pragma unroll 32
     for (uint32_t g = g0; g < g1; ++g) sum += (uint32_t)hist[(size_t)g * Etot + e];
   }
   part[tid] = sum;
@@ -493,12 +496,12 @@ NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_scan_gfx950(
   __syncthreads();
   uint32_t before = 0u, total_e = 0u;
   if (member) {
-    for (uint32_t u = 0; u < Q; ++u) {
-      const uint32_t v = part[e * Q + u];
-      before += u < q ? v : 0u;
+    for (uint32_t u = 0; u < NTm; ++u) {
+      const uint32_t v = part[u * Ep + e];
+      before += u < k ? v : 0u;
       total_e += v;
     }
-    if (q == 0) { cnt[e] = total_e; counts[e] = (int32_t)total_e; }
+    if (k == 0) { cnt[e] = total_e; counts[e] = (int32_t)total_e; }
   }
   __syncthreads();
   const uint32_t run = tid < Etot ? cnt[tid] : 0u;
@@ -532,20 +535,19 @@ NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_scan_gfx950(
   __syncthreads();
   if (member) {  // absolute base rows, in place
     uint32_t pos = block_off[e] * 64u + before;
-#pragma unroll 16
+#pragma unroll 32
     for (uint32_t g = g0; g < g1; ++g) {
       const uint32_t v = (uint32_t)hist[(size_t)g * Etot + e];
       hist[(size_t)g * Etot + e] = (int32_t)pos;
       pos += v;
     }
-  }
-  if (tid < Etot) {
-    const uint32_t b0 = block_off[tid], b1 = block_off[tid + 1u];
-    for (uint32_t b = b0; b < b1; ++b) owner[b] = (int32_t)tid;
-    const uint32_t i0 = tile_off[tid], i1 = tile_off[tid + 1u];
-    for (uint32_t i = i0; i < i1; ++i) tile_map[i] = (int32_t)(b0 * 4u + (i - i0));
-    const uint32_t p0 = pair_off[tid], p1 = pair_off[tid + 1u];
-    for (uint32_t i = p0; i < p1; ++i) pair_map[i] = (int32_t)(b0 + 2u * (i - p0));
+    // the expert's block owners and its tile / pair lists, split over the teams
+    const uint32_t b0 = block_off[e], b1 = block_off[e + 1u];
+    for (uint32_t b = b0 + k; b < b1; b += NTm) owner[b] = (int32_t)e;
+    const uint32_t i0 = tile_off[e], i1 = tile_off[e + 1u];
+    for (uint32_t i = i0 + k; i < i1; i += NTm) tile_map[i] = (int32_t)(b0 * 4u + (i - i0));
+    const uint32_t p0 = pair_off[e], p1 = pair_off[e + 1u];
+    for (uint32_t i = p0 + k; i < p1; i += NTm) pair_map[i] = (int32_t)(b0 + 2u * (i - p0));
   }
   if (tid == 0) {
     num_valid[0] = (int32_t)(total * 64u);
@@ -555,11 +557,14 @@ NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_scan_gfx950(
   }
   __syncthreads();
   for (uint32_t b = tid; b < cap_blocks; b += 1024u) sorted_expert[b] = owner[b];
+  // padding rows (Ktot << 24) | T: each expert's rows after its routes, then
+  // every row of the unused blocks
   const int32_t pad = (int32_t)((Ktot << 24) | T);
-  for (uint32_t p = tid; p < cap_blocks * 64u; p += 1024u) {
-    const int32_t o = owner[p >> 6];
-    if (o < 0 || p >= block_off[o] * 64u + cnt[o]) sorted_ids[p] = pad;
+  for (uint32_t idx = tid; idx < Etot * 64u; idx += 1024u) {
+    const uint32_t x = idx >> 6, row = block_off[x] * 64u + cnt[x] + (idx & 63u);
+    if (row < block_off[x + 1u] * 64u) sorted_ids[row] = pad;
   }
+  for (uint32_t p = total * 64u + tid; p < cap_blocks * 64u; p += 1024u) sorted_ids[p] = pad;
 }
 
 // sort_scatter: route r = (t, s) to expert e lands at base[t / 16][e] +

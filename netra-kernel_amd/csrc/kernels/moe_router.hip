@@ -349,11 +349,13 @@ NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_gfx950(
   __syncthreads();
 
   for (uint32_t b = tid; b < cap_blocks; b += 1024u) sorted_expert[b] = owner[b];
+  // padding rows: each expert's rows after its routes, then the unused blocks
   const int32_t pad = (int32_t)((Ktot << 24) | T);
-  for (uint32_t p = tid; p < cap_blocks * 64u; p += 1024u) {
-    const int32_t e = owner[p >> 6];
-    if (e < 0 || p >= block_off[e] * 64u + cnt[e]) sorted_ids[p] = pad;
+  for (uint32_t idx = tid; idx < Etot * 64u; idx += 1024u) {
+    const uint32_t x = idx >> 6, row = block_off[x] * 64u + cnt[x] + (idx & 63u);
+    if (row < block_off[x + 1u] * 64u) sorted_ids[row] = pad;
   }
+  for (uint32_t p = total * 64u + tid; p < cap_blocks * 64u; p += 1024u) sorted_ids[p] = pad;
   auto scatter = [&](uint32_t r, int32_t eid) {
     const uint32_t e = (uint32_t)eid;
     if (e >= Etot) return;

@@ -39,6 +39,8 @@
 //   netra_moe_sort_scatter_gfx950(ids, route_base, route_rank, sorted_ids;
 //       T, Ktot, Etot, CAP)   grid ceil(T*Ktot/256), block 256
 //   decode ("stream") GEMMs, H in {512,1024,2048,4096}, I in {256,512,1024,2048}:
+//   (every w13 below is in the gate/up-interleaved tile16x128 layout of
+//   netra_moe_pack_tiles_gate_up)
 //   netra_moe_gate_up_stream_h<H>_gfx950(xq, xs, w13 e4m3[Etot,2I,H],
 //       w13s f32[Etot,2I/128,H/128], sorted_ids, sorted_expert, tile_map, num_valid,
 //       h bf16[CAP*64,I] (tiled); T, H, I, Ktot, Etot)   grid 512, block 256 (persistent)
@@ -98,6 +100,13 @@ int netra_moe_quant_blocks(const float* w, uint8_t* q, float* s, uint32_t groups
 // layout of this build's kernels. Same error convention as above.
 int netra_moe_pack_tiles(const uint8_t* src, uint8_t* dst, uint32_t groups, uint32_t n,
                          uint32_t k, hipStream_t stream);
+
+// The same for W13 (n = 2I: gate rows, then up rows; n % 32 == 0), with the
+// row tiles interleaved: gate tile t at 2 t, up tile t at 2 t + 1, so each
+// gate/up pair the gate/up kernels stream together is contiguous. The gate/up
+// kernels read W13 only in this layout. Same error convention as above.
+int netra_moe_pack_tiles_gate_up(const uint8_t* src, uint8_t* dst, uint32_t groups, uint32_t n,
+                                 uint32_t k, hipStream_t stream);
 
 // Conversion self-check: writes the contract's integer E4M3 encoding (sw) and
 // the hardware conversion used by the hot kernels (hw) of n fp32 inputs.

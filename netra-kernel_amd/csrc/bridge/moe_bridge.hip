@@ -39,7 +39,21 @@ extern "C" int netra_moe_pack_tiles(const uint8_t* src, uint8_t* dst, uint32_t g
   const uint64_t tiles = static_cast<uint64_t>(groups) * (n / 16u) * (k / 128u);
   if (tiles > 0xfffffffcull) return fail(-1, "netra_moe_pack_tiles: too many tiles");
   hipLaunchKernelGGL(netra_moe_pack_tiles_gfx950, dim3(static_cast<uint32_t>((tiles + 3u) / 4u)),
-                     dim3(256), 0, stream, src, dst, groups, n, k);
+                     dim3(256), 0, stream, src, dst, groups, n, k, 0u);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(static_cast<int>(err), hipGetErrorString(err));
+  g_last_error.clear();
+  return 0;
+}
+
+extern "C" int netra_moe_pack_tiles_gate_up(const uint8_t* src, uint8_t* dst, uint32_t groups,
+                                            uint32_t n, uint32_t k, hipStream_t stream) {
+  if (!src || !dst || src == dst || groups == 0 || n == 0 || k == 0 || n % 32u || k % 128u)
+    return fail(-1, "netra_moe_pack_tiles_gate_up: null/aliased pointers or n % 32, k % 128 != 0");
+  const uint64_t tiles = static_cast<uint64_t>(groups) * (n / 16u) * (k / 128u);
+  if (tiles > 0xfffffffcull) return fail(-1, "netra_moe_pack_tiles_gate_up: too many tiles");
+  hipLaunchKernelGGL(netra_moe_pack_tiles_gfx950, dim3(static_cast<uint32_t>((tiles + 3u) / 4u)),
+                     dim3(256), 0, stream, src, dst, groups, n, k, 1u);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(static_cast<int>(err), hipGetErrorString(err));
   g_last_error.clear();

@@ -157,8 +157,8 @@ __device__ __forceinline__ void gate_up_lds(
   const uint32_t avoff1 = atok >= 0 ? avoff0 + 16u : kFar;
   const u32x4 ra = rsrc(xq, T * H);
   const uint8_t* w13e = w13 + (size_t)e * 2u * I * H;
-  const u32x4 rg = rsrc(nk::tile_base(w13e, ng * 8u + wave, 0, KB), KB * 2048u);
-  const u32x4 ru = rsrc(nk::tile_base(w13e, (I >> 4) + ng * 8u + wave, 0, KB), KB * 2048u);
+  // gate tile t and up tile t are adjacent (gate/up-interleaved W13): one range
+  const u32x4 rg = rsrc(nk::tile_base(w13e, 2u * (ng * 8u + wave), 0, KB), 2u * KB * 2048u);
   const uint32_t bvoff = lane * 16u;
   const uint32_t lds0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_offset(&s_stage[0][0]));
   // copy q = 0..5 of step kb (A halves, gate halves, up halves) into its stage
@@ -167,7 +167,7 @@ __device__ __forceinline__ void gate_up_lds(
     const uint32_t half = (q & 1u) * 1024u;
     if (q < 2u) copy16(st + wave * 2048u + half, ra, q ? avoff1 : avoff0, kb * 128u);
     else if (q < 4u) copy16(st + kABytes + wave * 2048u + half, rg, bvoff + half, kb * 2048u);
-    else copy16(st + kABytes + (8u + wave) * 2048u + half, ru, bvoff + half, kb * 2048u);
+    else copy16(st + kABytes + (8u + wave) * 2048u + half, rg, bvoff + half, (KB + kb) * 2048u);
   };
   auto issue = [&](uint32_t kb) __attribute__((always_inline)) {
 #pragma unroll

@@ -17,6 +17,8 @@
 // Symbols: netra_moe_gate_up_stream_h<H>_gfx950, netra_moe_requant_h_gfx950,
 // netra_moe_down_stream_i<I>_gfx950.
 #pragma once
+#include <type_traits>
+
 #include "moe_numerics.h"
 
 #define NK_KERNEL extern "C" __global__
@@ -32,9 +34,22 @@
 
 namespace nkstream {
 
+// f(integral_constant<0>) ... f(integral_constant<N - 1>), expanded at compile time.
+template <uint32_t N, uint32_t I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<uint32_t, I>{});
+    static_for<N, I + 1u>(f);
+  }
+}
+
 struct Range {
   uint32_t beg, end;
 };
+
+// Barrier for LDS hand-off only: waits for this wave's LDS traffic, not for its
+// outstanding global loads (__syncthreads would wait for those too).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ uint32_t wave_id() {
   return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -80,14 +95,23 @@ __device__ __forceinline__ void load_tile(TileRows& tr, const int32_t* __restric
 // oracle tools/benchmark/export_qwen36_moe_stage1_capture.py:80-97)
 //
 // Item (tile, c): h columns [16 c, 16 c + 16) of one 16-row tile, i.e. W13
-// rows n (gate) and I + n (up). Steps of kGuChunk 128-wide K blocks; per block
-// acc += w_s * (a_s * mfma) (mfma.inc:20-24) in ascending K order. After the
-// last step h = bf16_rne(silu(g) * u) for every valid row.
+// rows n (gate) and I + n (up), over the full K extent; per 128-wide K block
+// acc += w_s * (a_s * mfma) (mfma.inc:20-24) in ascending K order, and after
+// the last block h = bf16_rne(silu(g) * u) for every valid row.
+//
+// Work is dealt in groups of Q = 4 P consecutive columns of one tile (P, the
+// items per wave, a power of two with Q dividing the tile's I / 16 columns):
+// workgroup w takes groups w, w + gridDim.x, ... For a group it stages the
+// tile's FP8 activation rows (16 x H, in the MFMA operand layout) and their
+// scales in LDS once, and each wave then streams only the W13 tiles of its P
+// columns, in steps of kGuChunk K blocks, one step ahead. (Loading
+// the 16 gathered activation rows from L2 at every step as well doubled the
+// cache-line requests per step and held the weight stream at ~5.1 TB/s.)
 constexpr uint32_t kGuChunk = 2;
 
 struct GateUpStep {
-  nk::v8i g[kGuChunk], u[kGuChunk], a[kGuChunk];
-  float sg[kGuChunk], su[kGuChunk];
+  nk::v8i g[kGuChunk], u[kGuChunk];
+  float ws;  // lane i < KB: gate block scale of K block i; KB <= i < 2 KB: up block scale of K block i - KB
 };
 
 template <uint32_t KB>
@@ -100,110 +124,128 @@ __device__ __forceinline__ void gate_up_stream(
   using namespace nkstream;
   constexpr uint32_t H = 128 * KB;
   constexpr uint32_t NCH = KB / kGuChunk;
-  constexpr uint32_t SPL = (KB + 3) / 4;  // activation scales per lane per item
-  static_assert(KB % (2 * kGuChunk) == 0, "H must be a multiple of 512");
-  // Activation scales of the current and next item: [wave][slot][row * KB + kb].
-  __shared__ float s_xs[4][2][16 * KB];
-  const uint32_t lane = threadIdx.x & 63u;
+  static_assert(KB % (2 * kGuChunk) == 0, "H must be a multiple of 512 (an even step count)");
+  __shared__ __align__(16) uint8_t s_a[KB * 2048u];  // the tile's activations, operand layout per K block
+  __shared__ float s_xs[16 * KB];                    // their scales, [row][kb]
+  __shared__ __align__(16) uint16_t s_h[4][16 * 16];  // per wave: one item's h block
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = wave_id();
-  const uint32_t kofs = (lane >> 4) * 32u;
   const uint32_t cols = I / 16u;
-  const Range r = wave_range((uint32_t)num_valid[2] * cols);
-  const uint32_t steps = (r.end - r.beg) * NCH;
-  if (steps == 0) return;
+  const uint32_t items = (uint32_t)num_valid[2] * cols;
+  const uint32_t waves_total = gridDim.x * (blockDim.x >> 6);
+  uint32_t P = 1u;  // items per wave
+  while (P * waves_total < items && 8u * P <= cols) P <<= 1;
+  const uint32_t Q = 4u * P, groups = items / Q;
+  const uint32_t nsteps = P * NCH;
 
-  // Lane l fetches row l & 15's scales for K blocks [(l >> 4) * SPL, +SPL).
-  auto fetch_meta = [&](TileRows& m, float (&xsv)[SPL], uint32_t item) {
-    load_tile(m, tile_map, sorted_ids, sorted_expert, item / cols, T, Ktot, Etot, false);
-    const int32_t t = m.row < 0 ? 0 : m.row;
-    const uint32_t k0 = (lane >> 4) * SPL;
-#pragma unroll
-    for (uint32_t i = 0; i < SPL; ++i) xsv[i] = (k0 + i < KB) ? xs[(size_t)t * KB + k0 + i] : 0.0f;
-  };
-  auto store_scales = [&](const float (&xsv)[SPL], uint32_t slot) {
-    const uint32_t k0 = (lane >> 4) * SPL;
-#pragma unroll
-    for (uint32_t i = 0; i < SPL; ++i)
-      if (k0 + i < KB) s_xs[wave][slot][(lane & 15u) * KB + k0 + i] = xsv[i];
-  };
-  auto issue = [&](GateUpStep& st, const TileRows& m, uint32_t s) {
-    const uint32_t item = r.beg + s / NCH, ch = s % NCH;
-    const uint32_t c = item % cols;
-    const int32_t ta = __shfl(m.row, lane & 15u);
-    const uint8_t* arow = xq + (size_t)(ta < 0 ? 0 : ta) * H + kofs;
-#pragma unroll
-    for (uint32_t i = 0; i < kGuChunk; ++i) st.a[i] = nk::load_fp8x32(arow + (ch * kGuChunk + i) * 128u);
+  nk::v4f ag = {0.0f, 0.0f, 0.0f, 0.0f}, au = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
+  for (uint32_t grp = blockIdx.x; grp < groups; grp += gridDim.x) {
+    const uint32_t item0 = grp * Q, tile = item0 / cols;
+    const uint32_t c0 = item0 - tile * cols + wave * P;  // this wave's first column
+    TileRows m;
+    load_tile(m, tile_map, sorted_ids, sorted_expert, tile, T, Ktot, Etot, false);
     const uint8_t* we = w13 + (size_t)m.expert * 2u * I * H;
     const float* wse = w13s + (size_t)m.expert * (2u * I / 128u) * KB;
+    // Weight scales come in with a vector load (in order with the weights on
+    // the vector-memory counter): scalar loads would share the LDS counter,
+    // and their out-of-order returns make every LDS wait a full drain.
+    auto issue = [&](GateUpStep& st, uint32_t s) __attribute__((always_inline)) {
+      const uint32_t c = c0 + s / NCH, ch = s % NCH;
 #pragma unroll
-    for (uint32_t i = 0; i < kGuChunk; ++i) {
-      const uint32_t kb = ch * kGuChunk + i;
-      st.g[i] = nk::load_tile_operand(nk::tile_base(we, c, kb, KB), lane);
-      st.u[i] = nk::load_tile_operand(nk::tile_base(we, I / 16u + c, kb, KB), lane);
-      st.sg[i] = wse[(c >> 3) * KB + kb];                 // 128-row scale block of rows 16c..
-      st.su[i] = wse[((I / 16u + c) >> 3) * KB + kb];
-    }
-  };
-  nk::v4f ag = {0.0f, 0.0f, 0.0f, 0.0f}, au = {0.0f, 0.0f, 0.0f, 0.0f};
-  auto compute = [&](const GateUpStep& st, const TileRows& m, uint32_t slot, uint32_t s) {
-    const uint32_t ch = s % NCH;
-#pragma unroll
-    for (uint32_t i = 0; i < kGuChunk; ++i) {
-      const uint32_t kb = ch * kGuChunk + i;
-      const nk::v4f dg = nk::mfma_e4m3_16x16x128(st.a[i], st.g[i]);
-      const nk::v4f du = nk::mfma_e4m3_16x16x128(st.a[i], st.u[i]);
-#pragma unroll
-      for (uint32_t j = 0; j < 4; ++j) {
-        const float as = s_xs[wave][slot][((lane >> 4) * 4u + j) * KB + kb];
-        ag[j] = ag[j] + st.sg[i] * (as * dg[j]);
-        au[j] = au[j] + st.su[i] * (as * du[j]);
+      for (uint32_t i = 0; i < kGuChunk; ++i) {
+        const uint32_t kb = ch * kGuChunk + i;
+        st.g[i] = nk::load_tile_operand(nk::tile_base(we, 2u * c, kb, KB), lane);        // gate tile c
+        st.u[i] = nk::load_tile_operand(nk::tile_base(we, 2u * c + 1u, kb, KB), lane);   // up tile c
       }
-    }
-    if (ch == NCH - 1u) {
-      const uint32_t c = (r.beg + s / NCH) % cols;
+      // 128-row scale blocks of gate rows 16c.. and up rows I + 16c..
+      const uint32_t sl = lane < 2u * KB ? lane : 0u;
+      st.ws = wse[((sl < KB ? c : I / 16u + c) >> 3) * KB + (sl < KB ? sl : sl - KB)];
+    };
+    // Stage the tile: 16 rows x H bytes in 16-byte pieces (a wave moves half a
+    // row per instruction); lane l of K block kb's operand holds row l & 15,
+    // bytes (l >> 4) * 32 .. +31 (lo half at l * 16, hi half at 1024 + l * 16).
+    // The pieces are loaded before the first two weight steps are issued, so
+    // waiting for them does not drain the weight stream.
+    constexpr uint32_t kPieces = H / 256u, kScales = (16u * KB + 255u) / 256u;
+    uint4 av[kPieces];
 #pragma unroll
-      for (uint32_t j = 0; j < 4; ++j) {
-        const uint32_t row = (lane >> 4) * 4u + j;
-        if (__shfl(m.row, row) >= 0)
-          h[nk::h_tile_index(m.row0 + row, c * 16u + (lane & 15u), I / 128u)] =
-              nk::bf16_rne(nk::silu(ag[j]) * au[j]);
-      }
-      ag = nk::v4f{0.0f, 0.0f, 0.0f, 0.0f};
-      au = nk::v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t q = 0; q < kPieces; ++q) {
+      const uint32_t p = tid + q * 256u, row = p / (H / 16u), k = (p % (H / 16u)) * 16u;
+      const int32_t t = __shfl(m.row, row);
+      av[q] = *reinterpret_cast<const uint4*>(xq + (size_t)(t < 0 ? 0 : t) * H + k);
     }
-  };
+    float xv[kScales];
+#pragma unroll
+    for (uint32_t q = 0; q < kScales; ++q) {
+      const uint32_t i = tid + q * 256u;
+      const int32_t t = __shfl(m.row, (i / KB) & 15u);
+      xv[q] = i < 16u * KB ? xs[(size_t)(t < 0 ? 0 : t) * KB + i % KB] : 0.0f;
+    }
+    GateUpStep b0, b1;
+    issue(b0, 0u);
+    lds_barrier();  // the previous group's waves are done with s_a
+#pragma unroll
+    for (uint32_t q = 0; q < kPieces; ++q) {
+      const uint32_t p = tid + q * 256u, row = p / (H / 16u), k = (p % (H / 16u)) * 16u;
+      const uint32_t kb = k >> 7, kk = k & 127u;
+      *reinterpret_cast<uint4*>(&s_a[kb * 2048u + ((kk >> 4) & 1u) * 1024u + ((kk >> 5) * 16u + row) * 16u]) = av[q];
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < kScales; ++q)
+      if (tid + q * 256u < 16u * KB) s_xs[tid + q * 256u] = xv[q];
+    lds_barrier();
 
-  // Item k (slot k & 1): its metadata and scales were fetched at the start of
-  // item k - 1, its scales stored and its first step issued during the last
-  // step of item k - 1; inside the item step ch + 1 is issued before step ch
-  // computes.
-  GateUpStep sx, sy;
-  TileRows ma, mb;
-  float xa[SPL], xb[SPL];
-  auto item_body = [&](uint32_t k, const TileRows& cur, uint32_t slot, TileRows& nxt,
-                       float (&xnxt)[SPL]) {
-    const bool more = k + 1u < r.end;
-    if (more) fetch_meta(nxt, xnxt, k + 1u);
-#pragma unroll 1
-    for (uint32_t ch = 0; ch < NCH; ch += 2u) {
-      const uint32_t s = (k - r.beg) * NCH + ch;
-      issue(sy, cur, s + 1u);
-      compute(sx, cur, slot, s);
-      if (ch + 2u < NCH) {
-        issue(sx, cur, s + 2u);
-      } else if (more) {
-        store_scales(xnxt, slot ^ 1u);
-        issue(sx, nxt, s + 2u);
+    auto compute = [&](const GateUpStep& st, uint32_t s) __attribute__((always_inline)) {
+      const uint32_t ch = s % NCH;
+#pragma unroll
+      for (uint32_t i = 0; i < kGuChunk; ++i) {
+        const uint32_t kb = ch * kGuChunk + i;
+        const nk::v8i a = nk::load_tile_operand(s_a + kb * 2048u, lane);
+        const nk::v4f dg = nk::mfma_e4m3_16x16x128(a, st.g[i]);
+        const nk::v4f du = nk::mfma_e4m3_16x16x128(a, st.u[i]);
+        const float sg = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(st.ws), (int)kb));
+        const float su = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(st.ws), (int)(KB + kb)));
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+          const float as = s_xs[((lane >> 4) * 4u + j) * KB + kb];
+          ag[j] = ag[j] + sg * (as * dg[j]);
+          au[j] = au[j] + su * (as * du[j]);
+        }
       }
-      compute(sy, cur, slot, s + 1u);
+      if (ch == NCH - 1u) {
+        // h of the item's 16 x 16 block: through the wave's LDS slot so that
+        // it leaves as 32 pieces of 8 columns (16 bytes) of the tiled h
+        // layout, one store instruction instead of four 2-byte scatters
+        const uint32_t c = c0 + s / NCH;
+        uint16_t* sh = s_h[wave];
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j)
+          sh[((lane >> 4) * 4u + j) * 16u + (lane & 15u)] = nk::bf16_rne(nk::silu(ag[j]) * au[j]);
+        const uint32_t r = (lane >> 1) & 15u, xh = lane & 1u;
+        const uint4 v = *reinterpret_cast<const uint4*>(&sh[r * 16u + xh * 8u]);
+        const bool ok = __shfl(m.row, r) >= 0;
+        // columns c * 16 + xh * 8 .. +7 of row r: nk::h_tile_index of the first
+        const size_t dst = nk::h_tile_index(m.row0 + r, c * 16u + xh * 8u, I / 128u);
+        if (lane < 32u && ok) *reinterpret_cast<uint4*>(h + dst) = v;
+        ag = nk::v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        au = nk::v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+    };
+    // Two step buffers, two steps per iteration (nsteps is even): step s + 1
+    // is in flight while step s computes. No load is issued under a branch:
+    // the compiler's load-counter bookkeeping merges branch paths
+    // conservatively and would drain the prefetch at the join, so the last
+    // prefetch reloads the final step instead of being skipped.
+#pragma unroll 1
+    for (uint32_t s = 0; s < nsteps; s += 2u) {
+      issue(b1, s + 1u);
+      __builtin_amdgcn_sched_barrier(0);  // keep step s + 1's loads ahead of step s's MFMAs
+      compute(b0, s);
+      issue(b0, s + 2u < nsteps ? s + 2u : nsteps - 1u);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(b1, s + 1u);
     }
-  };
-  fetch_meta(ma, xa, r.beg);
-  store_scales(xa, 0u);
-  issue(sx, ma, 0);
-  for (uint32_t k = r.beg; k < r.end; k += 2u) {
-    item_body(k, ma, 0u, mb, xb);
-    if (k + 1u < r.end) item_body(k + 1u, mb, 1u, ma, xa);
   }
 }
 
@@ -302,7 +344,7 @@ struct DownStep {
   nk::v8i a;
   float4 as;
   nk::v8i w[2];
-  float s[2];
+  float ws;  // lane 0: w_s of the first 16-row tile's block, lane 1: of the second (vector load)
 };
 
 template <uint32_t KB>
@@ -334,20 +376,23 @@ __device__ __forceinline__ void down_stream(
     const uint8_t* we = w2 + (size_t)m.expert * H * I;
     const float* wse = w2s + (size_t)m.expert * (H / 128u) * KB;
 #pragma unroll
-    for (uint32_t t2 = 0; t2 < 2; ++t2) {
+    for (uint32_t t2 = 0; t2 < 2; ++t2)
       st.w[t2] = nk::load_tile_operand(nk::tile_base(we, c * 2u + t2, kb, KB), lane);
-      st.s[t2] = wse[((c * 2u + t2) >> 3) * KB + kb];   // 128-row scale block of the tile
-    }
+    // 128-row scale blocks of the two tiles, by a vector load (scalar loads
+    // would share the LDS/scalar counter and drain on every wait)
+    st.ws = wse[((c * 2u + (lane & 1u)) >> 3) * KB + kb];
   };
   nk::v4f acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
   auto compute = [&](const DownStep& st, const TileRows& m, uint32_t s) {
     const float as[4] = {st.as.x, st.as.y, st.as.z, st.as.w};
     const nk::v4f d0 = nk::mfma_e4m3_16x16x128(st.a, st.w[0]);
     const nk::v4f d1 = nk::mfma_e4m3_16x16x128(st.a, st.w[1]);
+    const float s0 = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(st.ws), 0));
+    const float s1 = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(st.ws), 1));
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j) {
-      acc0[j] = acc0[j] + st.s[0] * (as[j] * d0[j]);
-      acc1[j] = acc1[j] + st.s[1] * (as[j] * d1[j]);
+      acc0[j] = acc0[j] + s0 * (as[j] * d0[j]);
+      acc1[j] = acc1[j] + s1 * (as[j] * d1[j]);
     }
     if (s % NCH == NCH - 1u) {
       const uint32_t c = (r.beg + s / NCH) % cols;
@@ -365,25 +410,43 @@ __device__ __forceinline__ void down_stream(
     }
   };
 
-  DownStep sx, sy;
-  TileRows ma, mb;
-  auto item_body = [&](uint32_t k, const TileRows& cur, TileRows& nxt) {
-    if (k + 1u < r.end) fetch_meta(nxt, k + 1u);
-#pragma unroll 1
-    for (uint32_t ch = 0; ch < NCH; ch += 2u) {
-      const uint32_t s = (k - r.beg) * NCH + ch;
-      issue(sy, cur, s + 1u);
-      compute(sx, cur, s);
-      if (ch + 2u < NCH) issue(sx, cur, s + 2u);
-      else if (k + 1u < r.end) issue(sx, nxt, s + 2u);
-      compute(sy, cur, s + 1u);
-    }
+  // Two step buffers, two steps per iteration (NCH is even, so an iteration
+  // never straddles items): step s + 1 is in flight while step s computes.
+  // No load is issued under a branch (the compiler's load-counter bookkeeping
+  // merges branch paths conservatively and would drain the prefetch): the
+  // metadata of the item after the current one is reloaded every iteration
+  // and adopted by value selects, and the last prefetch reloads the final step.
+  DownStep b0, b1;
+  TileRows cur, nxt;
+  fetch_meta(cur, r.beg);
+  nxt = cur;
+  auto select = [](bool p, const TileRows& a, const TileRows& b) __attribute__((always_inline)) {
+    TileRows t;
+    t.row0 = p ? a.row0 : b.row0;
+    t.expert = p ? a.expert : b.expert;
+    t.row = p ? a.row : b.row;
+    return t;
   };
-  fetch_meta(ma, r.beg);
-  issue(sx, ma, 0);
-  for (uint32_t k = r.beg; k < r.end; k += 2u) {
-    item_body(k, ma, mb);
-    if (k + 1u < r.end) item_body(k + 1u, mb, ma);
+  issue(b0, cur, 0u);
+#pragma unroll 1
+  for (uint32_t s = 0; s < steps; s += 2u) {
+    const uint32_t rel = s / NCH, ch = s % NCH;
+    cur = select(ch == 0u && s > 0u, nxt, cur);  // a new item: its metadata came one item ahead
+    TileRows cand;
+    fetch_meta(cand, r.beg + rel + 1u < r.end ? r.beg + rel + 1u : r.end - 1u);
+    issue(b1, cur, s + 1u);
+    __builtin_amdgcn_sched_barrier(0);  // keep step s + 1's loads ahead of step s's MFMAs
+    compute(b0, cur, s);
+    // step s + 2: this item's, the next item's (whose metadata was fetched at
+    // this item's first iteration), or past the end (the last step again)
+    const bool last = s + 2u >= steps;
+    // (with NCH == 2 the next item starts at step s + 2 already: use the
+    // metadata just fetched, waiting for it)
+    const TileRows m2 = select(ch + 2u < NCH || last, cur, NCH == 2u ? cand : nxt);
+    issue(b0, m2, last ? steps - 1u : s + 2u);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(b1, cur, s + 1u);
+    nxt = select(ch == 0u, cand, nxt);
   }
 }
 

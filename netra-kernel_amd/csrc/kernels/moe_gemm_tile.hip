@@ -51,7 +51,8 @@ __device__ __forceinline__ v8i lds_fp8x32(const uint8_t* p) {
 //
 // Item (b, ng): expert block b, h columns [128 ng, 128 ng + 128), WAVES waves.
 // Wave w owns the CPW = 128 / WAVES h columns n = 128 ng + CPW w .. +CPW-1:
-// CPW / 16 W13 tiles of gate rows and as many of up rows (I + n), against the
+// CPW / 16 W13 tiles of gate rows and as many of up rows (I + n; stored
+// gate/up-interleaved, so a wave's tiles are one contiguous range), against the
 // block's non-empty 16-row tiles. Weight operands are prefetched AHEAD 128-K
 // blocks ahead (a ring in registers, raw buffer loads with scalar offsets),
 // activation rows two blocks ahead of their LDS store. Per 128-K block:
@@ -108,8 +109,9 @@ __device__ __forceinline__ void gate_up_tile(
   const uint32_t n0 = ng * 128u + wave * CPW;
   // gate / up tile strips: CT row tiles x KB tiles of 2 KiB, contiguous in the tile16x128 layout
   const uint8_t* w13e = w13 + (size_t)e * 2u * I * H;
-  const __amdgpu_buffer_rsrc_t wg = nk::buffer_rsrc(nk::tile_base(w13e, n0 >> 4, 0, KB), CT * KB * 2048u);
-  const __amdgpu_buffer_rsrc_t wu = nk::buffer_rsrc(nk::tile_base(w13e, (I + n0) >> 4, 0, KB), CT * KB * 2048u);
+  // gate/up-interleaved W13: gate tile t at 2 t, up tile t at 2 t + 1; the
+  // wave's CT pairs are one contiguous range
+  const __amdgpu_buffer_rsrc_t wgu = nk::buffer_rsrc(nk::tile_base(w13e, 2u * (n0 >> 4), 0, KB), 2u * CT * KB * 2048u);
   const float* wse = w13s + (size_t)e * (2u * I / 128u) * KB;
   const float* wsg = wse + (size_t)ng * KB;               // gate rows' 128-row block
   const float* wsu = wse + (size_t)(I / 128u + ng) * KB;  // up rows' block
@@ -137,8 +139,8 @@ __device__ __forceinline__ void gate_up_tile(
     auto load_b = [&](uint32_t kb, v8i (&dst)[2 * CT]) __attribute__((always_inline)) {
 #pragma unroll
       for (uint32_t c = 0; c < CT; ++c) {
-        dst[c] = nk::load_tile_operand(wg, (c * KB + kb) * 2048u, lane);
-        dst[CT + c] = nk::load_tile_operand(wu, (c * KB + kb) * 2048u, lane);
+        dst[c] = nk::load_tile_operand(wgu, (2u * c * KB + kb) * 2048u, lane);
+        dst[CT + c] = nk::load_tile_operand(wgu, ((2u * c + 1u) * KB + kb) * 2048u, lane);
       }
     };
 #pragma unroll

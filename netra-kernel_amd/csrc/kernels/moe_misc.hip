@@ -155,10 +155,12 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_e4m3_check_gfx950(
 // Weight layout change: row-major e4m3 [groups, n, k] -> tile16x128 (see
 // nk::tile_base). One wave per 16 x 128 tile; lane l moves row l & 15,
 // columns (l >> 4) * 32 .. +15 to tile offset l * 16 and columns +16 .. +31
-// to 1024 + l * 16.
+// to 1024 + l * 16. With gate_up != 0 (W13: gate rows, then as many up rows)
+// the row tiles are stored interleaved, gate tile t at 2 t and up tile t at
+// 2 t + 1 (nk::gu_tile), so a gate/up tile pair is 2 x k/128 tiles contiguous.
 NK_KERNEL __launch_bounds__(256) void netra_moe_pack_tiles_gfx950(
     const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t groups, uint32_t n,
-    uint32_t k) {
+    uint32_t k, uint32_t gate_up) {
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t tile = blockIdx.x * 4u + (threadIdx.x >> 6);
   const uint32_t nt = n / 16u, kb = k / 128u;
@@ -167,7 +169,8 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_pack_tiles_gfx950(
   const uint8_t* s = src + ((size_t)g * n + rt * 16u + (lane & 15u)) * k + cb * 128u + (lane >> 4) * 32u;
   const uint4 lo = *reinterpret_cast<const uint4*>(s);
   const uint4 hi = *reinterpret_cast<const uint4*>(s + 16);
-  uint8_t* d = dst + (size_t)tile * 2048u + lane * 16u;
+  const uint32_t prt = gate_up ? nk::gu_tile(rt, n) : rt;
+  uint8_t* d = dst + (((size_t)g * nt + prt) * kb + cb) * 2048u + lane * 16u;
   *reinterpret_cast<uint4*>(d) = lo;
   *reinterpret_cast<uint4*>(d + 1024) = hi;
 }

@@ -115,6 +115,14 @@ __device__ __forceinline__ v8i load_fp8x32(const uint8_t* p) {
 // K extent is contiguous. Lane l's MFMA operand (row l & 15, columns
 // (l >> 4) * 32 .. +31) is split in two 16-byte halves stored at l * 16 and
 // 1024 + l * 16: each of the wave's two 16-byte loads reads 1 KiB contiguous.
+// W13 stores its row tiles gate/up interleaved: logical row tile t of a
+// [2I, K] matrix (gate rows 0 .. I-1, up rows I .. 2I-1) is stored at
+// 2 t (gate) or 2 (t - I/16) + 1 (up), n2i = 2I rows.
+__host__ __device__ __forceinline__ uint32_t gu_tile(uint32_t t, uint32_t n2i) {
+  const uint32_t half = n2i / 32u;  // gate row tiles
+  return t < half ? 2u * t : 2u * (t - half) + 1u;
+}
+
 __device__ __forceinline__ const uint8_t* tile_base(const uint8_t* matrix, uint32_t row_tile,
                                                     uint32_t kb, uint32_t kblocks) {
   return matrix + ((size_t)row_tile * kblocks + kb) * 2048u;

@@ -33,6 +33,8 @@ def bridge_library() -> ctypes.CDLL:
         lib.netra_moe_quant_blocks.restype = ctypes.c_int
         lib.netra_moe_pack_tiles.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_uint32] * 3 + [ctypes.c_void_p]
         lib.netra_moe_pack_tiles.restype = ctypes.c_int
+        lib.netra_moe_pack_tiles_gate_up.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_uint32] * 3 + [ctypes.c_void_p]
+        lib.netra_moe_pack_tiles_gate_up.restype = ctypes.c_int
         lib.netra_moe_e4m3_check.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_uint32, ctypes.c_void_p]
         lib.netra_moe_e4m3_check.restype = ctypes.c_int
         lib.netra_moe_copy.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_uint64, ctypes.c_void_p]
@@ -60,19 +62,20 @@ def quantize_blocks(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return q, s
 
 
-def pack_tiles(q: torch.Tensor) -> torch.Tensor:
-    """Row-major e4m3 bytes [G, N, K] on the GPU -> the kernels' tile16x128 layout."""
+def pack_tiles(q: torch.Tensor, gate_up: bool = False) -> torch.Tensor:
+    """Row-major e4m3 bytes [G, N, K] on the GPU -> the kernels' tile16x128 layout
+    (gate_up: W13, row tiles gate/up-interleaved, netra_moe_pack_tiles_gate_up)."""
     if q.dim() != 3 or q.dtype != torch.uint8 or not q.is_cuda or not q.is_contiguous():
         raise ValueError("pack_tiles needs a contiguous uint8 [G, N, K] GPU tensor")
     g, n, k = q.shape
-    if n % 16 or k % 128:
-        raise ValueError("N must be a multiple of 16 and K of 128")
+    if n % (32 if gate_up else 16) or k % 128:
+        raise ValueError("N must be a multiple of 16 (32 for W13) and K of 128")
     out = torch.empty_like(q)
     lib = bridge_library()
-    rc = lib.netra_moe_pack_tiles(q.data_ptr(), out.data_ptr(), g, n, k,
-                                  torch.cuda.current_stream(q.device).cuda_stream)
+    fn = lib.netra_moe_pack_tiles_gate_up if gate_up else lib.netra_moe_pack_tiles
+    rc = fn(q.data_ptr(), out.data_ptr(), g, n, k, torch.cuda.current_stream(q.device).cuda_stream)
     if rc != 0:
-        raise RuntimeError(f"netra_moe_pack_tiles failed ({rc}): {lib.netra_moe_last_error().decode()}")
+        raise RuntimeError(f"weight packing failed ({rc}): {lib.netra_moe_last_error().decode()}")
     return out
 
 
@@ -89,19 +92,33 @@ def device_copy(src: torch.Tensor, dst: torch.Tensor) -> None:
         raise RuntimeError(f"netra_moe_copy failed ({rc}): {lib.netra_moe_last_error().decode()}")
 
 
-def pack_tiles_host(q: np.ndarray) -> np.ndarray:
+def gu_order(nt: int) -> np.ndarray:
+    """Stored row-tile order of a gate/up-interleaved W13 with nt row tiles:
+    position 2t holds gate tile t, 2t + 1 holds up tile t (logical nt/2 + t)."""
+    half = nt // 2
+    return np.stack([np.arange(half), np.arange(half) + half], axis=1).reshape(-1)
+
+
+def pack_tiles_host(q: np.ndarray, gate_up: bool = False) -> np.ndarray:
     """Host restatement of the tile16x128 layout: [G, N, K] ->
     [G, N/16, K/128, half, lane, 16 bytes] with lane = (k % 128) // 32 * 16 + n % 16
-    and half = (k % 32) // 16 (returned with the original shape)."""
+    and half = (k % 32) // 16 (returned with the original shape); with gate_up the
+    row tiles are stored in gu_order."""
     g, n, k = q.shape
     t = q.reshape(g, n // 16, 16, k // 128, 4, 2, 16).transpose(0, 1, 3, 5, 4, 2, 6)
+    t = np.ascontiguousarray(t)
+    if gate_up:
+        t = t[:, gu_order(n // 16)]
     return np.ascontiguousarray(t).reshape(g, n, k)
 
 
-def unpack_tiles_host(q: np.ndarray) -> np.ndarray:
+def unpack_tiles_host(q: np.ndarray, gate_up: bool = False) -> np.ndarray:
     """Inverse of pack_tiles_host: tile16x128 bytes [G, N, K] -> row-major."""
     g, n, k = q.shape
-    t = q.reshape(g, n // 16, k // 128, 2, 4, 16, 16).transpose(0, 1, 5, 2, 4, 3, 6)
+    t = q.reshape(g, n // 16, k // 128, 2, 4, 16, 16)
+    if gate_up:
+        t = t[:, np.argsort(gu_order(n // 16))]
+    t = t.transpose(0, 1, 5, 2, 4, 3, 6)
     return np.ascontiguousarray(t).reshape(g, n, k)
 
 
@@ -150,11 +167,12 @@ def synthetic_expert_weights_f32(cfg: MoEConfig, seed: int, device: torch.device
 
 def prepare_expert_weights(w13: torch.Tensor, w2: torch.Tensor, keep_row_major: bool = False):
     """fp32 W13 [Etot, 2I, H], W2 [Etot, H, I] on the GPU -> the layer's weight
-    tensors (e4m3 in the tile16x128 layout + fp32 128x128 block scales). With
+    tensors (e4m3 in the tile16x128 layout, W13 gate/up-interleaved, + fp32
+    128x128 block scales). With
     keep_row_major the row-major e4m3 bytes are returned as well."""
     q13, s13 = quantize_blocks(w13)
     q2, s2 = quantize_blocks(w2)
-    out = {"w13": pack_tiles(q13), "w13_scale": s13, "w2": pack_tiles(q2), "w2_scale": s2}
+    out = {"w13": pack_tiles(q13, gate_up=True), "w13_scale": s13, "w2": pack_tiles(q2), "w2_scale": s2}
     if keep_row_major:
         out["w13_row_major"], out["w2_row_major"] = q13, q2
     return out

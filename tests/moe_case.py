@@ -43,7 +43,7 @@ def make_inputs(cfg: MoEConfig, device: torch.device, weights_on_gpu: bool | Non
         w13, w2 = W.synthetic_expert_weights_f32(cfg, WEIGHT_SEED, "cpu")
         rm13, s13 = oracle.quant_blocks_f32(w13.numpy())
         rm2, s2 = oracle.quant_blocks_f32(w2.numpy())
-        wq = {"w13": torch.from_numpy(W.pack_tiles_host(rm13)).to(device),
+        wq = {"w13": torch.from_numpy(W.pack_tiles_host(rm13, gate_up=True)).to(device),
               "w13_scale": torch.from_numpy(s13).to(device),
               "w2": torch.from_numpy(W.pack_tiles_host(rm2)).to(device),
               "w2_scale": torch.from_numpy(s2).to(device)}

@@ -68,5 +68,7 @@ def test_pack_tiles_kernel_matches_host_layout():
     g = np.random.default_rng(3)
     q = g.integers(0, 256, size=(3, 64, 384), dtype=np.uint8)
     out = W.pack_tiles(torch.from_numpy(q).to(DEV))
+    out_gu = W.pack_tiles(torch.from_numpy(q).to(DEV), gate_up=True)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(out.cpu().numpy(), W.pack_tiles_host(q))
+    np.testing.assert_array_equal(out_gu.cpu().numpy(), W.pack_tiles_host(q, gate_up=True))

@@ -1,4 +1,5 @@
-"""HIP path vs the CPU oracle on identical seeded inputs, all five configs.
+"""HIP path vs the CPU oracle on identical seeded inputs: the five benchmark
+configs and two extra shapes, each through both GEMM paths.
 
 Bars: router logits (every logit on the exact front end; the selected and
 shared-gate logits on the screen front end, the others within the screen's
@@ -17,7 +18,7 @@ import oracle
 from conftest import gpu_available
 from moe_case import make_inputs, oracle_routing, run_gpu, sample_tokens
 from netra_moe import weights as W
-from netra_moe.config import BASELINE_CONFIGS
+from netra_moe.config import BASELINE_CONFIGS, MoEConfig
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a GPU")]
 
@@ -25,13 +26,21 @@ TOL = 2e-2
 DEV = torch.device("cuda", 0)
 
 
-CASES = [(name, path) for name in BASELINE_CONFIGS for path in ("stream", "tile")]
+# Shapes beyond the benchmark configs, so every kernel instantiation family is
+# exercised: H = 4096 (exact front end, register-operand tile gate/up) and
+# H = 1024 with I = 1024 (the other GEMM widths).
+EXTRA_CONFIGS = {
+    "shape_h4096": MoEConfig("shape_h4096", T=48, H=4096, E=32, K=4, I=256, S=1, seed=1101),
+    "shape_h1024_i1024": MoEConfig("shape_h1024_i1024", T=40, H=1024, E=24, K=3, I=1024, S=1, seed=1102),
+}
+CONFIGS = {**BASELINE_CONFIGS, **EXTRA_CONFIGS}
+CASES = [(name, path) for name in CONFIGS for path in ("stream", "tile")]
 
 
 @pytest.fixture(scope="module", params=CASES, ids=[f"{n}-{p}" for n, p in CASES])
 def case(request):
     name, path = request.param
-    cfg = BASELINE_CONFIGS[name]
+    cfg = CONFIGS[name]
     print(f"\n[parity] config={cfg.name} path={path} T={cfg.T} H={cfg.H} E={cfg.E} K={cfg.K} S={cfg.S}",
           flush=True)
     x, gpu_w, host = make_inputs(cfg, DEV)

@@ -37,22 +37,19 @@ def log(msg: str) -> None:
 
 def gate_up_bytes(cfg, touched: int, path: str) -> int:
     """Algorithmic HBM bytes of one gate/up launch: touched experts' W13 + scales,
-    x_q + x scales, and h (bf16 on the decode path; e4m3 + 1x128 scales on the
-    prefill path) for every route row."""
+    x_q + x scales, and h (e4m3 + 1x128 scales, both paths) for every route row."""
     w = touched * (2 * cfg.I * cfg.H + 4 * (2 * cfg.I // 128) * (cfg.H // 128))
     acts = cfg.T * cfg.H + 4 * cfg.T * (cfg.H // 128)
-    if path == "stream":
-        outs = 2 * cfg.routes * cfg.I
-    else:
-        outs = cfg.routes * cfg.I + 4 * cfg.routes * (cfg.I // 128)
+    outs = cfg.routes * cfg.I + 4 * cfg.routes * (cfg.I // 128)
     return w + acts + outs
 
 
 def down_bytes(cfg, touched: int, path: str) -> int:
-    """Touched experts' W2 + scales, h in, fp32 partial rows out."""
+    """Touched experts' W2 + scales, h in, route partial rows out."""
     w = touched * (cfg.H * cfg.I + 4 * (cfg.H // 128) * (cfg.I // 128))
-    h = 2 * cfg.routes * cfg.I if path == "stream" else cfg.routes * cfg.I + 4 * cfg.routes * (cfg.I // 128)
-    return w + h + 4 * cfg.routes * cfg.H
+    h = cfg.routes * cfg.I + 4 * cfg.routes * (cfg.I // 128)
+    part = (4 if path == "stream" else 2) * cfg.routes * cfg.H  # fp32 / bf16 route partials
+    return w + h + part
 
 
 def time_graph(layers, steps: int, warmup: int, torch):
@@ -70,10 +67,10 @@ def time_graph(layers, steps: int, warmup: int, torch):
     return start.elapsed_time(end) / steps, wall * 1e3 / steps
 
 
-# Operations that rewrite an input in place (sort_scan turns route_select's
-# histograms into row bases): timed behind the operation that produces that
+# Operations that rewrite an input in place (sort_count turns route_select's
+# histograms into row prefixes): timed behind the operation that produces that
 # input, minus that operation's own time.
-IN_PLACE_INPUT_FROM = {"sort_scan": "route_select"}
+IN_PLACE_INPUT_FROM = {"sort_count": "route_select"}
 
 
 def time_operation(layers, op: str, steps: int, torch):

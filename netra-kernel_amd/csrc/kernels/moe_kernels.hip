@@ -4,8 +4,8 @@
 // Layer pipeline, one engine operation per kernel, fixed grids with
 // device-side early exit so a whole layer call is one capturable HIP graph:
 //   front end, exact:  router (logits + input quant) -> topk -> sort
-//   front end, screen: route_screen -> sort_scan -> sort_scatter
-//   then gate_up_{stream|tile} -> down_{stream|tile} -> combine
+//   front end, screen: route_screen -> route_select -> sort_count -> sort_place
+//   then gate_up_{stream|lds|tile} -> down_{stream|tile} -> combine
 // Every kernel takes plain pointers followed by u32 shape constants, in the
 // order documented in include/netra_moe.h. Host code validates shapes before
 // a launch; kernels also bound-check data-dependent indices (expert ids,

@@ -155,17 +155,6 @@ __device__ __forceinline__ v8i load_tile_operand(__amdgpu_buffer_rsrc_t r, uint3
   return v;
 }
 
-// Tiled activation layout for h (bf16, [rows, I]) between the decode GEMMs:
-// per 16-row tile and 128-column block, lane l's 32 values (row l & 15,
-// columns (l >> 4) * 32 .. +31) form four 16-byte pieces; piece q of every
-// lane lies at ((tile * kblocks + kb) * 4 + q) * 1024 + l * 16 bytes, so the
-// consumer's four loads each read 1 KiB contiguous.
-__device__ __forceinline__ size_t h_tile_index(uint32_t row, uint32_t col, uint32_t kblocks) {
-  const uint32_t kb = col >> 7, cc = col & 127u, e = cc & 31u;
-  const uint32_t lane = (cc >> 5) * 16u + (row & 15u);
-  return ((((size_t)(row >> 4) * kblocks + kb) * 4u + (e >> 3)) * 64u + lane) * 8u + (e & 7u);
-}
-
 // D = A(16x128 e4m3) * B(128x16 e4m3), fp32 accumulate. Lane l supplies row
 // (l & 15) of A / column (l & 15) of B over K bytes [(l >> 4) * 32, +32); it
 // receives D rows (l >> 4) * 4 + j, column (l & 15), j = 0..3.

@@ -5,11 +5,13 @@
 //                 the bound m = 2^-10 ||x|| ||w|| on |L - a| (Cauchy-Schwarz),
 //                 exact contract logits of the candidates and the shared-gate
 //                 row, top-k + weights + shared-expert append, input quant,
-//                 logits out; per 16-token workgroup expert histogram and the
+//                 logits out; per workgroup expert histogram and the
 //                 in-workgroup rank of every route
-//   sort_scan     per-expert totals, 64-row block layout, padding, and the
-//                 absolute row base of every (workgroup, expert) pair
-//   sort_scatter  sorted ids = base + in-workgroup rank
+//   sort_count    per expert (one workgroup each): prefix sums of its
+//                 histogram row over the route_select workgroups, and its total
+//   sort_place    expert layout (64-row blocks, padding, tile and pair lists)
+//                 rebuilt by every workgroup from the totals; sorted ids =
+//                 block base + prefix + in-workgroup rank
 // The results equal those of the exact front end (moe_router.hip): top-k ids,
 // weights, counts and the sorted layout are the same bits. Logits of the
 // experts that were not candidates are the screen's values rounded to bf16.
@@ -21,7 +23,6 @@
 namespace nkroute {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-constexpr uint32_t kTok = 16;       // tokens per route_select workgroup (route_base granularity)
 constexpr uint32_t kMaxSlots = 64;  // K + S <= 64
 // Screen margin: |L - a| <= 2^-10 * ||x|| ||w||. Both the contract's fp32
 // chains (< 140 roundings of relative size 2^-24) and the MFMA's fp32
@@ -195,8 +196,8 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
 }
 
 // ---------------------------------------------------------------------------
-// route_select: workgroup of 8 waves for 16 tokens (a wave handles tokens
-// w and w + 8 in turn; 256 VGPRs per wave keep the exact phase in registers).
+// route_select: workgroup of W waves for W tokens, one token per wave (the
+// engine picks W so that the grid covers the chip: 4 for T <= 1024, else 8).
 //  0. the token row is staged in LDS, quantised (1x128) and its norm taken;
 //  1. bounds zlo/zhi of z = f32(bf16(L)) + bias from L in [a - m, a + m],
 //     m = 2^-10 ||x|| ||w_e|| (norms rounded up; bf16
@@ -208,9 +209,11 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
 //  3. top-K over the candidates' exact z (descending, ties to the lower expert
 //     index), weights, shared expert append (as the exact top-k kernel);
 //  4. logits row;
-//  5. per workgroup: in-workgroup rank of every route among the workgroup's
-//     routes to the same expert (token order) and the per-expert histogram.
-template <uint32_t NJ, uint32_t EMAX>
+//  5. per workgroup g: in-workgroup rank of every route among the workgroup's
+//     routes to the same expert (token order), and the per-expert histogram
+//     hist[e][g] (expert-major, so each expert's counts are contiguous for
+//     the sort's per-expert scan).
+template <uint32_t NJ, uint32_t EMAX, uint32_t W>
 __device__ __forceinline__ void route_select(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
     const float* __restrict__ screen, const float* __restrict__ wnorm, uint16_t* __restrict__ logits,
@@ -221,15 +224,15 @@ __device__ __forceinline__ void route_select(
   constexpr uint32_t H = 128u * NJ;
   constexpr uint32_t P = EMAX / 64u;  // experts per lane
   static_assert(EMAX % 64u == 0 && P <= 8u, "shape");
-  __shared__ uint4 s_x[kTok][16u * NJ];         // the tokens' rows (bf16)
-  __shared__ uint16_t s_cand[kTok][EMAX];
-  __shared__ uint16_t s_exact[kTok][EMAX + 1];  // exact logit bits, candidate order; shared row last
-  __shared__ int32_t s_ids[kTok][kMaxSlots];
-  __shared__ uint2 s_sel[kTok][kMaxSlots];       // (expert, code) by slot
+  __shared__ uint4 s_x[W][16u * NJ];         // the tokens' rows (bf16)
+  __shared__ uint16_t s_cand[W][EMAX];
+  __shared__ uint16_t s_exact[W][EMAX + 1];  // exact logit bits, candidate order; shared row last
+  __shared__ int32_t s_ids[W][kMaxSlots];
+  __shared__ uint2 s_sel[W][kMaxSlots];       // (expert, code) by slot
   __shared__ uint32_t s_hist[EMAX + 1];
   const uint32_t rows = E + S, Ktot = K + S;
   if (E > EMAX || K == 0 || K > E || Ktot > kMaxSlots || S > 1u) return;  // uniform
-  constexpr uint32_t kThreads = 512u;
+  constexpr uint32_t kThreads = 64u * W;
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
   for (uint32_t e = tid; e <= EMAX; e += kThreads) s_hist[e] = 0u;
@@ -237,8 +240,8 @@ __device__ __forceinline__ void route_select(
   const uint32_t s = lane & 15u, g = lane >> 4;
 
 #pragma unroll 1
-  for (uint32_t tt = wave; tt < kTok; tt += kThreads / 64u) {
-    const uint32_t t = blockIdx.x * kTok + tt;
+  for (uint32_t tt = wave; tt < W; tt += W) {  // one token per wave
+    const uint32_t t = blockIdx.x * W + tt;
     if (t >= T) break;  // uniform per wave; later tokens are past T too
     // 0. token row -> LDS, its 1x128 quant and its norm
     float xx = 0.0f;
@@ -408,8 +411,8 @@ __device__ __forceinline__ void route_select(
   __syncthreads();
 
   // 5. in-workgroup ranks and histogram
-  const uint32_t t0 = blockIdx.x * kTok;
-  for (uint32_t r = tid; r < kTok * Ktot; r += kThreads) {
+  const uint32_t t0 = blockIdx.x * W;
+  for (uint32_t r = tid; r < W * Ktot; r += kThreads) {
     const uint32_t tk = r / Ktot, sl = r - tk * Ktot;
     if (t0 + tk >= T) break;
     const int32_t e = s_ids[tk][sl];
@@ -418,7 +421,7 @@ __device__ __forceinline__ void route_select(
       for (uint32_t v = 0; v < Ktot; ++v) rank += s_ids[u][v] == e ? 1u : 0u;
     lrank[(size_t)(t0 + tk) * Ktot + sl] = (int32_t)rank;
   }
-  for (uint32_t e = tid; e < rows; e += kThreads) hist[(size_t)blockIdx.x * rows + e] = (int32_t)s_hist[e];
+  for (uint32_t e = tid; e < rows; e += kThreads) hist[(size_t)e * gridDim.x + blockIdx.x] = (int32_t)s_hist[e];
 }
 
 }  // namespace nkroute
@@ -434,149 +437,168 @@ NK_ROUTE_SCREEN(512)
 NK_ROUTE_SCREEN(1024)
 NK_ROUTE_SCREEN(2048)
 
-#define NK_ROUTE_SELECT(HV, EMAXV)                                                                \
-  NK_KERNEL __launch_bounds__(512) void netra_moe_route_select_h##HV##_e##EMAXV##_gfx950(         \
+#define NK_ROUTE_SELECT(HV, EMAXV, WV)                                                            \
+  NK_KERNEL __launch_bounds__(64 * WV) void netra_moe_route_select_h##HV##_e##EMAXV##_w##WV##_gfx950( \
       const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,                             \
       const float* __restrict__ bias, const float* __restrict__ screen,                           \
-      const float* __restrict__ wnorm, uint16_t* __restrict__ logits, int32_t* __restrict__ ids, float* __restrict__ weights,      \
-      uint8_t* __restrict__ xq, float* __restrict__ xs, int32_t* __restrict__ hist,               \
-      int32_t* __restrict__ lrank, uint32_t T, uint32_t H, uint32_t E, uint32_t K, uint32_t S,    \
-      uint32_t RP) {                                                                              \
+      const float* __restrict__ wnorm, uint16_t* __restrict__ logits, int32_t* __restrict__ ids,  \
+      float* __restrict__ weights, uint8_t* __restrict__ xq, float* __restrict__ xs,              \
+      int32_t* __restrict__ hist, int32_t* __restrict__ lrank, uint32_t T, uint32_t H, uint32_t E, \
+      uint32_t K, uint32_t S, uint32_t RP) {                                                      \
     (void)H;                                                                                      \
-    nkroute::route_select<HV / 128, EMAXV>(x, w, bias, screen, wnorm, logits, ids, weights, xq,   \
-                                           xs, hist, lrank, T, E, K, S, RP);                      \
+    nkroute::route_select<HV / 128, EMAXV, WV>(x, w, bias, screen, wnorm, logits, ids, weights,   \
+                                               xq, xs, hist, lrank, T, E, K, S, RP);              \
   }
-NK_ROUTE_SELECT(512, 256)
-NK_ROUTE_SELECT(1024, 256)
-NK_ROUTE_SELECT(2048, 256)
-NK_ROUTE_SELECT(512, 512)
-NK_ROUTE_SELECT(1024, 512)
-NK_ROUTE_SELECT(2048, 512)
+#define NK_ROUTE_SELECT_W(HV, EMAXV) NK_ROUTE_SELECT(HV, EMAXV, 4) NK_ROUTE_SELECT(HV, EMAXV, 8)
+NK_ROUTE_SELECT_W(512, 256)
+NK_ROUTE_SELECT_W(1024, 256)
+NK_ROUTE_SELECT_W(2048, 256)
+NK_ROUTE_SELECT_W(512, 512)
+NK_ROUTE_SELECT_W(1024, 512)
+NK_ROUTE_SELECT_W(2048, 512)
 
 // ---------------------------------------------------------------------------
-// sort_scan (one 1024-thread workgroup): hist[g][e] holds the routes of
-// route_select workgroup g to expert e. Teams of (Etot rounded up to 64)
-// threads, one thread per expert, split the G workgroups; counts[e] is the
-// total, experts get ceil(count / 64) blocks in expert order (wave scans of
-// 64 experts, then the wave totals), tiles of 16 rows likewise. hist is then
-// overwritten in place with the absolute sorted row of the first route of
-// (g, e): block_off[e] * 64 + routes of e in workgroups before g. Also writes
-// sorted_expert, tile_map, pair_map (first block of each pair of consecutive
-// blocks of one expert), num_valid = {padded rows, routes, tiles, pairs} and
-// the padding rows (Ktot << 24) | T of sorted_ids (the scatter fills the rest).
-// Dynamic LDS: 4 * (1024 + 4 * Etot + 51 + CAP) bytes.
-NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_scan_gfx950(
-    int32_t* __restrict__ hist, int32_t* __restrict__ sorted_ids, int32_t* __restrict__ sorted_expert,
-    int32_t* __restrict__ tile_map, int32_t* __restrict__ pair_map, int32_t* __restrict__ num_valid,
-    int32_t* __restrict__ counts, uint32_t T, uint32_t Ktot, uint32_t Etot, uint32_t G, uint32_t cap_blocks) {
-  extern __shared__ uint32_t lds[];
-  uint32_t* part = lds;                      // [1024]
-  uint32_t* cnt = part + 1024;               // [Etot]
-  uint32_t* block_off = cnt + Etot;          // [Etot + 1]
-  uint32_t* tile_off = block_off + Etot + 1; // [Etot + 1]
-  uint32_t* pair_off = tile_off + Etot + 1;  // [Etot + 1]
-  uint32_t* chunk = pair_off + Etot + 1;     // [48]
-  int32_t* owner = reinterpret_cast<int32_t*>(chunk + 48);  // [cap_blocks]
+// sort_count: workgroup e (256 threads) turns expert e's histogram row
+// hist[e][0 .. G) (G route_select workgroups) into exclusive prefix sums in
+// place, i.e. the rows of expert e that precede each workgroup's routes, and
+// writes counts[e], the expert's total.
+NK_KERNEL __launch_bounds__(256) void netra_moe_sort_count_gfx950(
+    int32_t* __restrict__ hist, int32_t* __restrict__ counts, uint32_t G, uint32_t Etot) {
+  __shared__ uint32_t s_wave[4];
+  const uint32_t e = blockIdx.x;
+  if (e >= Etot) return;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  if (Etot == 0u || Etot > 1024u) return;
-  // Teams of Ep (experts rounded up to a whole wave) threads split the G
-  // groups; a wave reads 64 consecutive experts of one group row, and each
-  // thread keeps 32 loads of its column in flight.
-  const uint32_t Ep = (Etot + 63u) & ~63u, NTm = 1024u / Ep;
-  const uint32_t k = tid / Ep, e = tid - k * Ep;
-  const bool member = k < NTm && e < Etot;
-  const uint32_t g0 = (G * k) / NTm, g1 = (G * (k + 1u)) / NTm;
-  uint32_t sum = 0u;
-  if (member) {
-#pragma unroll 32
-    for (uint32_t g = g0; g < g1; ++g) sum += (uint32_t)hist[(size_t)g * Etot + e];
-  }
-  part[tid] = sum;
-  for (uint32_t b = tid; b < cap_blocks; b += 1024u) owner[b] = -1;
-  __syncthreads();
-  uint32_t before = 0u, total_e = 0u;
-  if (member) {
-    for (uint32_t u = 0; u < NTm; ++u) {
-      const uint32_t v = part[u * Ep + e];
-      before += u < k ? v : 0u;
-      total_e += v;
-    }
-    if (k == 0) { cnt[e] = total_e; counts[e] = (int32_t)total_e; }
-  }
-  __syncthreads();
-  const uint32_t run = tid < Etot ? cnt[tid] : 0u;
-  const uint32_t vb = (run + 63u) >> 6, vt = (run + 15u) >> 4, vp = (vb + 1u) >> 1;
-  uint32_t ib = vb, it = vt, ip = vp;
+  int32_t* row = hist + (size_t)e * G;
+  uint32_t carry = 0u;
+  for (uint32_t g0 = 0; g0 < G; g0 += 256u) {  // uniform trip count
+    const uint32_t g = g0 + tid;
+    const uint32_t v = g < G ? (uint32_t)row[g] : 0u;
+    uint32_t inc = v;
 #pragma unroll
-  for (uint32_t off = 1; off < 64; off <<= 1) {
-    const uint32_t ob = __shfl_up(ib, off);
-    const uint32_t ot = __shfl_up(it, off);
-    const uint32_t op = __shfl_up(ip, off);
-    if (lane >= off) { ib += ob; it += ot; ip += op; }
-  }
-  if (lane == 63u) { chunk[wave] = ib; chunk[16u + wave] = it; chunk[32u + wave] = ip; }
-  __syncthreads();
-  uint32_t cb = 0, ct = 0, cp = 0, total = 0, total_t = 0, total_p = 0;
-#pragma unroll
-  for (uint32_t c = 0; c < 16u; ++c) {
-    const uint32_t b = chunk[c], t = chunk[16u + c], q = chunk[32u + c];
-    if (c < wave) { cb += b; ct += t; cp += q; }
-    total += b;
-    total_t += t;
-    total_p += q;
-  }
-  if (tid < Etot) { block_off[tid] = cb + ib - vb; tile_off[tid] = ct + it - vt; pair_off[tid] = cp + ip - vp; }
-  if (tid == 0) { block_off[Etot] = total; tile_off[Etot] = total_t; pair_off[Etot] = total_p; }
-  const uint32_t cap_tiles = (T * Ktot + 15u) / 16u + Etot;
-  if (total > cap_blocks || total_t > cap_tiles) {  // impossible for route_screen histograms; write nothing
-    if (tid == 0) { num_valid[0] = 0; num_valid[1] = -1; num_valid[2] = 0; num_valid[3] = 0; }
-    return;
-  }
-  __syncthreads();
-  if (member) {  // absolute base rows, in place
-    uint32_t pos = block_off[e] * 64u + before;
-#pragma unroll 32
-    for (uint32_t g = g0; g < g1; ++g) {
-      const uint32_t v = (uint32_t)hist[(size_t)g * Etot + e];
-      hist[(size_t)g * Etot + e] = (int32_t)pos;
-      pos += v;
+    for (uint32_t off = 1; off < 64u; off <<= 1) {
+      const uint32_t o = __shfl_up(inc, off);
+      if (lane >= off) inc += o;
     }
-    // the expert's block owners and its tile / pair lists, split over the teams
-    const uint32_t b0 = block_off[e], b1 = block_off[e + 1u];
-    for (uint32_t b = b0 + k; b < b1; b += NTm) owner[b] = (int32_t)e;
-    const uint32_t i0 = tile_off[e], i1 = tile_off[e + 1u];
-    for (uint32_t i = i0 + k; i < i1; i += NTm) tile_map[i] = (int32_t)(b0 * 4u + (i - i0));
-    const uint32_t p0 = pair_off[e], p1 = pair_off[e + 1u];
-    for (uint32_t i = p0 + k; i < p1; i += NTm) pair_map[i] = (int32_t)(b0 + 2u * (i - p0));
+    if (lane == 63u) s_wave[wave] = inc;
+    __syncthreads();
+    uint32_t before = carry, total = 0u;
+#pragma unroll
+    for (uint32_t w = 0; w < 4u; ++w) {
+      const uint32_t x = s_wave[w];
+      before += w < wave ? x : 0u;
+      total += x;
+    }
+    if (g < G) row[g] = (int32_t)(before + inc - v);
+    carry += total;
+    __syncthreads();  // s_wave is rewritten by the next round
   }
-  if (tid == 0) {
-    num_valid[0] = (int32_t)(total * 64u);
-    num_valid[1] = (int32_t)(T * Ktot);
-    num_valid[2] = (int32_t)total_t;
-    num_valid[3] = (int32_t)total_p;
-  }
-  __syncthreads();
-  for (uint32_t b = tid; b < cap_blocks; b += 1024u) sorted_expert[b] = owner[b];
-  // padding rows (Ktot << 24) | T: each expert's rows after its routes, then
-  // every row of the unused blocks
-  const int32_t pad = (int32_t)((Ktot << 24) | T);
-  for (uint32_t idx = tid; idx < Etot * 64u; idx += 1024u) {
-    const uint32_t x = idx >> 6, row = block_off[x] * 64u + cnt[x] + (idx & 63u);
-    if (row < block_off[x + 1u] * 64u) sorted_ids[row] = pad;
-  }
-  for (uint32_t p = total * 64u + tid; p < cap_blocks * 64u; p += 1024u) sorted_ids[p] = pad;
+  if (tid == 0) counts[e] = (int32_t)carry;
 }
 
-// sort_scatter: route r = (t, s) to expert e lands at base[t / 16][e] +
-// lrank[r], written as (s << 24) | t. Grid ceil(T * Ktot / 256), block 256.
-NK_KERNEL __launch_bounds__(256) void netra_moe_sort_scatter_gfx950(
+// sort_place: every workgroup rebuilds the expert layout from counts (experts
+// in order get ceil(count / 64) blocks, ceil(count / 16) 16-row tiles and
+// ceil(blocks / 2) block pairs: an exclusive scan over the experts, each
+// thread summing a contiguous run of them), then
+//  - scatters its 256 routes: route r = (t, s) of expert e lands at row
+//    block_off[e] * 64 + base[e][t / W] + lrank[r], written as (s << 24) | t;
+//  - for experts e = blockIdx.x, + gridDim.x, ...: sorted_expert of its
+//    blocks, its tile_map and pair_map entries, and its padding rows
+//    (Ktot << 24) | T after its routes;
+//  - a grid-stride share of the unused blocks: sorted_expert -1, every row
+//    padding;
+//  - workgroup 0: num_valid = {padded rows, routes, tiles, pairs}.
+// Grid ceil(T * Ktot / 256) x 256 threads; dynamic LDS 4 * (4 * Etot + 3) bytes.
+NK_KERNEL __launch_bounds__(256) void netra_moe_sort_place_gfx950(
     const int32_t* __restrict__ ids, const int32_t* __restrict__ base, const int32_t* __restrict__ lrank,
-    int32_t* __restrict__ sorted_ids, uint32_t T, uint32_t Ktot, uint32_t Etot, uint32_t cap_blocks) {
-  const uint32_t r = blockIdx.x * 256u + threadIdx.x;
-  if (r >= T * Ktot) return;
-  const uint32_t e = (uint32_t)ids[r];
-  if (e >= Etot) return;
-  const uint32_t t = r / Ktot, s = r - t * Ktot;
-  const uint32_t pos = (uint32_t)base[(size_t)(t / nkroute::kTok) * Etot + e] + (uint32_t)lrank[r];
-  if (pos < cap_blocks * 64u) sorted_ids[pos] = (int32_t)((s << 24) | t);
+    const int32_t* __restrict__ counts, int32_t* __restrict__ sorted_ids,
+    int32_t* __restrict__ sorted_expert, int32_t* __restrict__ tile_map, int32_t* __restrict__ pair_map,
+    int32_t* __restrict__ num_valid, uint32_t T, uint32_t Ktot, uint32_t Etot, uint32_t G, uint32_t W,
+    uint32_t cap_blocks) {
+  extern __shared__ uint32_t lds[];
+  uint32_t* cnt = lds;                        // [Etot]
+  uint32_t* block_off = cnt + Etot;           // [Etot + 1]
+  uint32_t* tile_off = block_off + Etot + 1;  // [Etot + 1]
+  uint32_t* pair_off = tile_off + Etot + 1;   // [Etot + 1]
+  __shared__ uint32_t s_wave[3][4];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  if (Etot == 0u || Etot > 1024u) return;
+  const uint32_t routes = T * Ktot;
+  const uint32_t r = blockIdx.x * 256u + tid;
+  int32_t my_e = -1, my_rank = 0;  // this thread's route, loaded ahead of the scan
+  if (r < routes) {
+    my_e = ids[r];
+    my_rank = lrank[r];
+  }
+  const uint32_t ept = (Etot + 255u) / 256u, e0 = tid * ept;
+  uint32_t sb = 0u, st = 0u, sp = 0u;
+  for (uint32_t i = 0; i < ept; ++i) {
+    const uint32_t e = e0 + i;
+    const uint32_t c = e < Etot ? (uint32_t)counts[e] : 0u;
+    if (e < Etot) cnt[e] = c;
+    const uint32_t vb = (c + 63u) >> 6;
+    sb += vb;
+    st += (c + 15u) >> 4;
+    sp += (vb + 1u) >> 1;
+  }
+  uint32_t ib = sb, it = st, ip = sp;
+#pragma unroll
+  for (uint32_t off = 1; off < 64u; off <<= 1) {
+    const uint32_t ob = __shfl_up(ib, off), ot = __shfl_up(it, off), op = __shfl_up(ip, off);
+    if (lane >= off) { ib += ob; it += ot; ip += op; }
+  }
+  if (lane == 63u) { s_wave[0][wave] = ib; s_wave[1][wave] = it; s_wave[2][wave] = ip; }
+  __syncthreads();
+  uint32_t ob = ib - sb, ot = it - st, op = ip - sp, tb = 0u, tt = 0u, tp = 0u;
+#pragma unroll
+  for (uint32_t w = 0; w < 4u; ++w) {
+    if (w < wave) { ob += s_wave[0][w]; ot += s_wave[1][w]; op += s_wave[2][w]; }
+    tb += s_wave[0][w];
+    tt += s_wave[1][w];
+    tp += s_wave[2][w];
+  }
+  for (uint32_t i = 0; i < ept; ++i) {
+    const uint32_t e = e0 + i;
+    if (e < Etot) {
+      block_off[e] = ob;
+      tile_off[e] = ot;
+      pair_off[e] = op;
+      const uint32_t c = cnt[e], vb = (c + 63u) >> 6;
+      ob += vb;
+      ot += (c + 15u) >> 4;
+      op += (vb + 1u) >> 1;
+    }
+  }
+  if (tid == 0) { block_off[Etot] = tb; tile_off[Etot] = tt; pair_off[Etot] = tp; }
+  __syncthreads();
+  const uint32_t cap_tiles = (routes + 15u) / 16u + Etot;
+  if (tb > cap_blocks || tt > cap_tiles) {  // impossible for route_select histograms; write nothing
+    if (blockIdx.x == 0 && tid == 0) { num_valid[0] = 0; num_valid[1] = -1; num_valid[2] = 0; num_valid[3] = 0; }
+    return;
+  }
+  const int32_t pad = (int32_t)((Ktot << 24) | T);
+  if (r < routes && (uint32_t)my_e < Etot) {
+    const uint32_t t = r / Ktot, s = r - t * Ktot, g = t / W;
+    const uint32_t pos = block_off[my_e] * 64u + (g < G ? (uint32_t)base[(size_t)my_e * G + g] : 0u) +
+                         (uint32_t)my_rank;
+    if (pos < cap_blocks * 64u) sorted_ids[pos] = (int32_t)((s << 24) | t);
+  }
+  for (uint32_t e = blockIdx.x; e < Etot; e += gridDim.x) {
+    const uint32_t b0 = block_off[e], b1 = block_off[e + 1u];
+    for (uint32_t b = b0 + tid; b < b1; b += 256u) sorted_expert[b] = (int32_t)e;
+    const uint32_t i0 = tile_off[e], i1 = tile_off[e + 1u];
+    for (uint32_t i = i0 + tid; i < i1; i += 256u) tile_map[i] = (int32_t)(b0 * 4u + (i - i0));
+    const uint32_t p0 = pair_off[e], p1 = pair_off[e + 1u];
+    for (uint32_t i = p0 + tid; i < p1; i += 256u) pair_map[i] = (int32_t)(b0 + 2u * (i - p0));
+    const uint32_t row = b0 * 64u + cnt[e] + tid;  // at most 63 rows after the expert's routes
+    if (row < b1 * 64u) sorted_ids[row] = pad;
+  }
+  const uint32_t stride = gridDim.x * 256u;
+  for (uint32_t p = tb * 64u + blockIdx.x * 256u + tid; p < cap_blocks * 64u; p += stride) sorted_ids[p] = pad;
+  for (uint32_t b = tb + blockIdx.x * 256u + tid; b < cap_blocks; b += stride) sorted_expert[b] = -1;
+  if (blockIdx.x == 0 && tid == 0) {
+    num_valid[0] = (int32_t)(tb * 64u);
+    num_valid[1] = (int32_t)routes;
+    num_valid[2] = (int32_t)tt;
+    num_valid[3] = (int32_t)tp;
+  }
 }

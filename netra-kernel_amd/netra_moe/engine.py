@@ -56,11 +56,14 @@ TILE_H = (512, 1024, 2048, 4096)     # netra_moe_gate_up_tile_h<H>_gfx950
 TILE_I = (256, 512, 1024)            # netra_moe_down_tile_i<I>_gfx950
 TILE_GU_WAVES = 4                    # waves of netra_moe_gate_up_tile_h<H>_gfx950 (its launch bound)
 LDS_GU_H = (512, 1024, 2048)         # netra_moe_gate_up_lds_h<H>_gfx950: 128-row pairs, LDS operand ring
-# Persistent stream kernels: 256 CUs x 4 SIMDs x resident waves per SIMD
-# (NK_GATE_UP_WAVES_PER_EU = 2, NK_DOWN_WAVES_PER_EU = 4) / 4 waves per group.
-STREAM_GRID_GATE_UP = 512
-STREAM_GRID_DOWN = 1024
-STREAM_GRID_REQUANT = 256
+# Stream kernel grids (measured at T=64 on one MI355X): gate/up fills the chip
+# once, 256 CUs x 4 SIMDs x 2 resident waves (NK_GATE_UP_WAVES_PER_EU) / 8
+# waves per workgroup; down runs 2048 four-wave workgroups, about twice what
+# is resident at once, so each wave streams fewer steps (47 us against 49 us
+# for 1024 workgroups and 49 us for 512).
+STREAM_GRID_GATE_UP = 256
+STREAM_GU_THREADS = 512
+STREAM_GRID_DOWN = 2048
 
 
 def resolve_path(cfg: MoEConfig, path: str = "auto") -> str:
@@ -85,7 +88,7 @@ def xcd_grid(items: int) -> int:
 FRONTS = ("exact", "screen")
 SCREEN_H = (512, 1024, 2048)          # netra_moe_route_screen_h<H>_gfx950 / route_select_h<H>_e<EMAX>
 SCREEN_EMAX = (256, 512)              # expert capacities of the route_select kernels
-SCREEN_TOKENS = 16                    # tokens per route_select workgroup (nkroute::kTok)
+SCREEN_SELECT_WAVES = (4, 8)          # route_select_h<H>_e<EMAX>_w<W>: W waves, one token each
 
 
 def resolve_front(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> str:
@@ -112,8 +115,14 @@ def screen_emax(cfg: MoEConfig) -> int:
     return next(e for e in SCREEN_EMAX if cfg.E <= e)
 
 
+def screen_tokens(cfg: MoEConfig) -> int:
+    """Tokens (= waves) per route_select workgroup: small workgroups while
+    they are needed to spread T tokens over the chip's 256 CUs."""
+    return 4 if cfg.T <= 1024 else 8
+
+
 def screen_groups(cfg: MoEConfig) -> int:
-    return (cfg.T + SCREEN_TOKENS - 1) // SCREEN_TOKENS
+    return (cfg.T + screen_tokens(cfg) - 1) // screen_tokens(cfg)
 
 
 def tensor_table(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> dict[str, TensorSpec]:
@@ -146,11 +155,10 @@ def tensor_table(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> dic
     else:
         specs += [TensorSpec("screen", "f32", (T, screen_row_pad(cfg)), "temporary"),
                   TensorSpec("route_wnorm", "f32", (screen_row_pad(cfg),), "temporary"),
-                  TensorSpec("route_base", "i32", (screen_groups(cfg), cfg.Etot), "temporary"),
+                  TensorSpec("route_base", "i32", (cfg.Etot, screen_groups(cfg)), "temporary"),
                   TensorSpec("route_rank", "i32", (T * cfg.Ktot,), "temporary")]
     if path == "stream":
-        specs += [TensorSpec("h", "bf16", (cfg.cap_rows, I), "temporary"),
-                  TensorSpec("h_q", "e4m3", (cfg.cap_rows, I), "temporary"),
+        specs += [TensorSpec("h_q", "e4m3", (cfg.cap_rows, I), "temporary"),
                   TensorSpec("h_scale", "f32", (cfg.cap_rows // 16, I // 128, 16), "temporary")]
     else:
         specs += [TensorSpec("h_q", "e4m3", (cfg.cap_rows, I), "temporary"),
@@ -160,8 +168,8 @@ def tensor_table(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> dic
 
 
 EXACT_FRONT_OPS = ("router", "topk", "sort")
-SCREEN_FRONT_OPS = ("route_screen", "route_select", "sort_scan", "sort_scatter")
-PATH_OPS = {"stream": ("gate_up", "requant", "down", "combine"), "tile": ("gate_up", "down", "combine")}
+SCREEN_FRONT_OPS = ("route_screen", "route_select", "sort_count", "sort_place")
+PATH_OPS = {"stream": ("gate_up", "down", "combine"), "tile": ("gate_up", "down", "combine")}
 
 
 def op_names(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> tuple[str, ...]:
@@ -181,6 +189,7 @@ def _screen_front(cfg: MoEConfig) -> list[dict]:
     T, H = cfg.T, cfg.H
     u = lambda v: ("u32", int(v))  # noqa: E731
     G = screen_groups(cfg)
+    Wt = screen_tokens(cfg)
     RP = screen_row_pad(cfg)
     return [
         dict(name="moe.route_screen", symbol=f"netra_moe_route_screen_h{H}_gfx950",
@@ -188,31 +197,31 @@ def _screen_front(cfg: MoEConfig) -> list[dict]:
              args=["x", "router_w", "screen", "route_wnorm", u(T), u(H), u(cfg.router_rows), u(RP)],
              reads=["x", "router_w"], writes=["screen", "route_wnorm"],
              refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150"]),
-        dict(name="moe.route_select", symbol=f"netra_moe_route_select_h{H}_e{screen_emax(cfg)}_gfx950",
-             grid=(G, 1, 1), block=(512, 1, 1),
-             lds=SCREEN_TOKENS * H * 2 + 2 * SCREEN_TOKENS * (2 * screen_emax(cfg) + 1) + SCREEN_TOKENS * 64 * 12
-             + 4 * (screen_emax(cfg) + 1), dyn=0,
+        dict(name="moe.route_select",
+             symbol=f"netra_moe_route_select_h{H}_e{screen_emax(cfg)}_w{Wt}_gfx950",
+             grid=(G, 1, 1), block=(64 * Wt, 1, 1),
+             lds=Wt * (H * 2 + 2 * (2 * screen_emax(cfg) + 1) + 64 * 12) + 4 * (screen_emax(cfg) + 1), dyn=0,
              args=["x", "router_w", "router_bias", "screen", "route_wnorm", "logits", "topk_ids", "topk_weights", "x_q",
                    "x_scale", "route_base", "route_rank", u(T), u(H), u(cfg.E), u(cfg.K), u(cfg.S), u(RP)],
              reads=["x", "router_w", "router_bias", "screen", "route_wnorm"],
              writes=["logits", "topk_ids", "topk_weights", "x_q", "x_scale", "route_base", "route_rank"],
              refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150",
                    "runtime/gfx950/routing/decode/qwen36_shared_gate_append_bridge.hip:76-112"]),
-        dict(name="moe.sort_scan", symbol="netra_moe_sort_scan_gfx950",
-             grid=(1, 1, 1), block=(1024, 1, 1), lds=0,
-             dyn=4 * (1024 + 4 * cfg.Etot + 51 + cfg.cap_blocks),
-             args=["route_base", "sorted_ids", "sorted_expert", "tile_map", "pair_map", "num_valid",
-                   "expert_counts", u(T), u(cfg.Ktot), u(cfg.Etot), u(G), u(cfg.cap_blocks)],
-             reads=["route_base"],
-             writes=["route_base", "sorted_ids", "sorted_expert", "tile_map", "pair_map", "num_valid",
-                     "expert_counts"],
+        dict(name="moe.sort_count", symbol="netra_moe_sort_count_gfx950",
+             grid=(cfg.Etot, 1, 1), block=(256, 1, 1), lds=4 * 4, dyn=0,
+             args=["route_base", "expert_counts", u(G), u(cfg.Etot)],
+             reads=["route_base"], writes=["route_base", "expert_counts"],
              refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]),
-        dict(name="moe.sort_scatter", symbol="netra_moe_sort_scatter_gfx950",
-             grid=((T * cfg.Ktot + 255) // 256, 1, 1), block=(256, 1, 1), lds=0, dyn=0,
-             args=["topk_ids", "route_base", "route_rank", "sorted_ids",
-                   u(T), u(cfg.Ktot), u(cfg.Etot), u(cfg.cap_blocks)],
-             reads=["topk_ids", "route_base", "route_rank"], writes=["sorted_ids"],
-             refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]),
+        dict(name="moe.sort_place", symbol="netra_moe_sort_place_gfx950",
+             grid=((T * cfg.Ktot + 255) // 256, 1, 1), block=(256, 1, 1), lds=4 * 12,
+             dyn=4 * (4 * cfg.Etot + 3),
+             args=["topk_ids", "route_base", "route_rank", "expert_counts", "sorted_ids", "sorted_expert",
+                   "tile_map", "pair_map", "num_valid",
+                   u(T), u(cfg.Ktot), u(cfg.Etot), u(G), u(Wt), u(cfg.cap_blocks)],
+             reads=["topk_ids", "route_base", "route_rank", "expert_counts"],
+             writes=["sorted_ids", "sorted_expert", "tile_map", "pair_map", "num_valid"],
+             refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112",
+                   "manifests/gfx950/models/qwen36-35b-c64-fp8.json:43-49"]),
     ]
 
 
@@ -256,17 +265,13 @@ def operations(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> list[
     if path == "stream":
         ops += [
             dict(name="moe.gate_up", symbol=f"netra_moe_gate_up_stream_h{H}_gfx950",
-                 grid=(STREAM_GRID_GATE_UP, 1, 1), block=(256, 1, 1), lds=0, dyn=0,
+                 grid=(STREAM_GRID_GATE_UP, 1, 1), block=(STREAM_GU_THREADS, 1, 1), lds=0, dyn=0,
                  args=["x_q", "x_scale", "w13", "w13_scale", "sorted_ids", "sorted_expert",
-                       "tile_map", "num_valid", "h",
+                       "tile_map", "num_valid", "h_q", "h_scale",
                        u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
-                 reads=["x_q", "x_scale", "w13", "w13_scale", *common, "tile_map"], writes=["h"],
-                 refs=["kernels/gfx950/templates/moe/decode/gate_up_mfma.inc:12-161"]),
-            dict(name="moe.requant", symbol="netra_moe_requant_h_gfx950",
-                 grid=(STREAM_GRID_REQUANT, 1, 1), block=(256, 1, 1), lds=0, dyn=0,
-                 args=["h", "h_q", "h_scale", "tile_map", "num_valid", u(I)],
-                 reads=["h", "tile_map", "num_valid"], writes=["h_q", "h_scale"],
-                 refs=["kernels/gfx950/templates/moe/decode/silu_quant.inc:16-236"]),
+                 reads=["x_q", "x_scale", "w13", "w13_scale", *common, "tile_map"], writes=["h_q", "h_scale"],
+                 refs=["kernels/gfx950/templates/moe/decode/gate_up_mfma.inc:12-161",
+                       "kernels/gfx950/templates/moe/decode/silu_quant.inc:16-236"]),
             dict(name="moe.down", symbol=f"netra_moe_down_stream_i{I}_gfx950",
                  grid=(STREAM_GRID_DOWN, 1, 1), block=(256, 1, 1), lds=0, dyn=0,
                  args=["h_q", "h_scale", "w2", "w2_scale", "sorted_ids", "sorted_expert", "tile_map",

@@ -122,15 +122,6 @@ def unpack_tiles_host(q: np.ndarray, gate_up: bool = False) -> np.ndarray:
     return np.ascontiguousarray(t).reshape(g, n, k)
 
 
-def unpack_h_tiles_host(h: np.ndarray, cols: int) -> np.ndarray:
-    """Inverse of the decode GEMMs' tiled h layout: flat bf16 bits -> [rows, cols].
-    Stored order is [row tile, K block, piece q, lane group g, row r, 8 values]
-    for row = tile * 16 + r and column = block * 128 + g * 32 + q * 8 + value."""
-    rows = h.size // cols
-    t = h.reshape(rows // 16, cols // 128, 4, 4, 16, 8).transpose(0, 4, 1, 3, 2, 5)
-    return np.ascontiguousarray(t).reshape(rows, cols)
-
-
 def zipf_bias(E: int, seed: int, s: float = 1.1) -> np.ndarray:
     """bias[e] = log p(rank(e)), p(r) proportional to r^-s over r = 1..E."""
     ranks = np.arange(1, E + 1, dtype=np.float64)

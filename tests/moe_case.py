@@ -14,7 +14,7 @@ from netra_moe import weights as W
 
 ROUTING = ("logits", "topk_ids", "topk_weights", "x_q", "x_scale", "sorted_ids",
            "sorted_expert", "tile_map", "pair_map", "num_valid", "expert_counts", "partial")
-PATH_INTERMEDIATES = {"stream": ("h", "h_q", "h_scale"), "tile": ("h_q", "h_scale")}
+PATH_INTERMEDIATES = {"stream": ("h_q", "h_scale"), "tile": ("h_q", "h_scale")}
 FRONT_INTERMEDIATES = {"exact": ("mask",), "screen": ()}
 
 

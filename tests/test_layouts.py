@@ -45,17 +45,3 @@ def test_pack_tiles_gate_up_interleaves_the_row_tiles():
                 assert p[off] == q[g, n, k]
     np.testing.assert_array_equal(W.unpack_tiles_host(p.reshape(G, N, K), gate_up=True), q)
     np.testing.assert_array_equal(W.unpack_tiles_host(W.pack_tiles_host(q)), q)
-
-
-def test_unpack_h_tiles_inverts_the_device_index():
-    rows, cols = 32, 256
-    flat = np.arange(rows * cols, dtype=np.int64)
-    out = W.unpack_h_tiles_host(flat, cols)
-    for r in range(0, rows, 3):
-        for c in range(0, cols, 5):
-            kb, cc = c >> 7, c & 127
-            e = cc & 31
-            lane = (cc >> 5) * 16 + (r & 15)
-            idx = ((((r >> 4) * (cols // 128) + kb) * 4 + (e >> 3)) * 64 + lane) * 8 + (e & 7)
-            assert out[r, c] == idx
-    assert np.array_equal(np.sort(out.reshape(-1)), flat)

@@ -1,6 +1,7 @@
 // Routing front end for large token counts (prefill, T > 256), four kernels:
-//   route_screen  bf16-MFMA router GEMM over all tokens and router rows: the
-//                 approximate logit a, and the router rows' norms
+//   route_screen  bf16-MFMA router GEMM over all tokens and router rows, K
+//                 split for small T: partial sums of the approximate logit a,
+//                 and partial squared norms of the router rows
 //   route_select  one wave per token: certified candidate set from a and
 //                 the bound m = 2^-10 ||x|| ||w|| on |L - a| (Cauchy-Schwarz),
 //                 exact contract logits of the candidates and the shared-gate
@@ -23,7 +24,7 @@
 namespace nkroute {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-constexpr uint32_t kMaxSlots = 64;  // K + S <= 64
+constexpr uint32_t kMaxSlots = 64;  // K + S <= 64 (and the K selected slots fit in a candidate list)
 // Screen margin: |L - a| <= 2^-10 * ||x|| ||w||. Both the contract's fp32
 // chains (< 140 roundings of relative size 2^-24) and the MFMA's fp32
 // accumulation of exact bf16 products (< 2^11 roundings of at most 2^-23 even
@@ -75,22 +76,23 @@ __device__ __forceinline__ void quant8(uint4 v, uint8_t* __restrict__ q_dst, flo
 // Exact contract logit of one (token, router row) pair by a 16-lane group:
 // lane s runs the sequential fmaf chain over elements 128 j + 8 s + i from +0,
 // then the +8/+4/+2/+1 tree (the same order as netra_moe_router_h<H>). The
-// token row comes from LDS (bf16, natural order), the router row from wv.
+// token row comes from LDS (widened to fp32, natural order), the router row
+// from wv.
 template <uint32_t NJ>
-__device__ __forceinline__ float exact_dot(const uint4* __restrict__ xrow, const uint4 (&wv)[NJ], uint32_t s) {
+__device__ __forceinline__ float exact_dot(const float4* __restrict__ xrow, const uint4 (&wv)[NJ], uint32_t s) {
   float a = 0.0f;
 #pragma unroll
   for (uint32_t j = 0; j < NJ; ++j) {
-    const uint4 x = xrow[16u * j + s];
+    const float4 xl = xrow[32u * j + 2u * s], xh = xrow[32u * j + 2u * s + 1u];
     const uint4 w = wv[j];
-    a = fmaf(nk::bf16_lo(x.x), nk::bf16_lo(w.x), a);
-    a = fmaf(nk::bf16_hi(x.x), nk::bf16_hi(w.x), a);
-    a = fmaf(nk::bf16_lo(x.y), nk::bf16_lo(w.y), a);
-    a = fmaf(nk::bf16_hi(x.y), nk::bf16_hi(w.y), a);
-    a = fmaf(nk::bf16_lo(x.z), nk::bf16_lo(w.z), a);
-    a = fmaf(nk::bf16_hi(x.z), nk::bf16_hi(w.z), a);
-    a = fmaf(nk::bf16_lo(x.w), nk::bf16_lo(w.w), a);
-    a = fmaf(nk::bf16_hi(x.w), nk::bf16_hi(w.w), a);
+    a = fmaf(xl.x, nk::bf16_lo(w.x), a);
+    a = fmaf(xl.y, nk::bf16_hi(w.x), a);
+    a = fmaf(xl.z, nk::bf16_lo(w.y), a);
+    a = fmaf(xl.w, nk::bf16_hi(w.y), a);
+    a = fmaf(xh.x, nk::bf16_lo(w.z), a);
+    a = fmaf(xh.y, nk::bf16_hi(w.z), a);
+    a = fmaf(xh.z, nk::bf16_lo(w.w), a);
+    a = fmaf(xh.w, nk::bf16_hi(w.w), a);
   }
   a = a + __shfl_down(a, 8u, 16);
   a = a + __shfl_down(a, 4u, 16);
@@ -100,16 +102,18 @@ __device__ __forceinline__ float exact_dot(const uint4* __restrict__ xrow, const
 }
 
 // ---------------------------------------------------------------------------
-// route_screen: workgroup (tm, tn), 256 threads: tokens 64 tm .. +63 x router
-// rows 64 tn .. +63. Per 128-K block the x and w tiles are staged in LDS
-// (loads for the next block in flight during this one's multiplies); wave w
-// multiplies its 16 tokens by the four 16-row tiles with
-// v_mfma_f32_16x16x32_bf16. Output screen[t][e] = a for t < T, e < rows, row
-// stride RP (rows rounded up to 64). The workgroups of the first token tile
-// also write the router rows' norms wnorm[e] = ||w_e|| (1 + 2^-9).
-template <uint32_t NJ>  // H / 128
+// route_screen: workgroup (tm, tn, z), 256 threads: tokens 64 tm .. +63 x
+// router rows 64 tn .. +63 over K blocks [z KBS, (z + 1) KBS) (split K, so
+// that a few hundred workgroups cover small token counts). Per 128-K block the
+// x and w tiles are staged in LDS (loads for the next block in flight during
+// this one's multiplies); wave w multiplies its 16 tokens by the four 16-row
+// tiles with v_mfma_f32_16x16x32_bf16. Output screen[z][t][e] = the split's
+// partial sum for t < T, e < rows, row stride RP (rows rounded up to 64); the
+// select kernel adds the splits in z order. The workgroups of the first token
+// tile also write the router rows' partial squared norms wsq[z][e].
+template <uint32_t NJ, uint32_t KBS>  // H / 128, K blocks per split
 __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                             float* __restrict__ screen, float* __restrict__ wnorm,
+                                             float* __restrict__ screen, float* __restrict__ wsq,
                                              uint32_t T, uint32_t rows, uint32_t RP) {
   constexpr uint32_t H = 128u * NJ;
   constexpr uint32_t kStride = 136;  // bf16 per LDS row (128 + 8: rotates banks across rows)
@@ -117,7 +121,8 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
   __shared__ __align__(16) uint16_t s_w[2][64 * kStride];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const bool norms = blockIdx.x == 0;  // uniform
-  const uint32_t t0 = blockIdx.x * 64u, r0 = blockIdx.y * 64u;
+  const uint32_t t0 = blockIdx.x * 64u, r0 = blockIdx.y * 64u, z = blockIdx.z, kb0 = z * KBS;
+  static_assert(KBS <= NJ && NJ % KBS == 0, "splits cover K");
   // staging: thread moves row (16 p + tid / 16) bytes (tid % 16) * 16 of both tiles, p = 0..3
   const uint32_t srow = tid >> 4, sc = (tid & 15u) * 8u;  // sc in bf16
   // buffer loads: one 32-bit byte offset per row and a scalar offset per block
@@ -138,20 +143,20 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
   auto load = [&](uint32_t kb, uint32_t slot) __attribute__((always_inline)) {
 #pragma unroll
     for (uint32_t p = 0; p < 4; ++p) {
-      const nk::u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(xr, (int)xoff[p], (int)(256u * kb), 0);
-      const nk::u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(wr, (int)woff[p], (int)(256u * kb), 0);
+      const nk::u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(xr, (int)xoff[p], (int)(256u * (kb0 + kb)), 0);
+      const nk::u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(wr, (int)woff[p], (int)(256u * (kb0 + kb)), 0);
       xv[slot][p] = make_uint4(a.x, a.y, a.z, a.w);
       wv[slot][p] = make_uint4(b.x, b.y, b.z, b.w);
     }
   };
   load(0, 0);
-  if (NJ > 1) load(1, 1);
+  if (KBS > 1) load(1, 1);
   nk::v4f acc[4];
 #pragma unroll
   for (uint32_t n = 0; n < 4; ++n) acc[n] = nk::v4f{0.0f, 0.0f, 0.0f, 0.0f};
   const uint32_t g = lane >> 4, rl = lane & 15u;
 #pragma unroll
-  for (uint32_t kb = 0; kb < NJ; ++kb) {
+  for (uint32_t kb = 0; kb < KBS; ++kb) {
     const uint32_t buf = kb & 1u, slot = kb % kRing;
 #pragma unroll
     for (uint32_t p = 0; p < 4; ++p) {
@@ -159,7 +164,7 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
       *reinterpret_cast<uint4*>(&s_w[buf][(16u * p + srow) * kStride + sc]) = wv[slot][p];
       if (norms) nw[p] += sumsq8(wv[slot][p]);
     }
-    if (kb + 2u < NJ) load(kb + 2u, (kb + 2u) % kRing);
+    if (kb + 2u < KBS) load(kb + 2u, (kb + 2u) % kRing);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
     for (uint32_t q = 0; q < 4; ++q) {
@@ -172,7 +177,7 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
     }
     __builtin_amdgcn_sched_barrier(0);  // one 128-K block per schedule region
   }
-  if (norms) {  // router-row norms: the 16 threads of a row hold its 16 column slices
+  if (norms) {  // router rows' squared norms: the 16 threads of a row hold its 16 column slices
 #pragma unroll
     for (uint32_t p = 0; p < 4; ++p) {
       float b = nw[p];
@@ -181,7 +186,7 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
       b += __shfl_xor(b, 4u);
       b += __shfl_xor(b, 8u);
       const uint32_t r = r0 + 16u * p + srow;
-      if ((tid & 15u) == 0 && r < rows) wnorm[r] = sqrtf(b) * kNormSlack;
+      if ((tid & 15u) == 0 && r < rows) wsq[(size_t)z * RP + r] = b;
     }
   }
 #pragma unroll
@@ -190,7 +195,7 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) {
       const uint32_t t = t0 + 16u * wave + 4u * g + i;
-      if (t < T && r < rows) screen[(size_t)t * RP + r] = acc[n][i];
+      if (t < T && r < rows) screen[((size_t)z * T + t) * RP + r] = acc[n][i];
     }
   }
 }
@@ -216,26 +221,33 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
 template <uint32_t NJ, uint32_t EMAX, uint32_t W>
 __device__ __forceinline__ void route_select(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
-    const float* __restrict__ screen, const float* __restrict__ wnorm, uint16_t* __restrict__ logits,
+    const float* __restrict__ screen, const float* __restrict__ wsq, uint16_t* __restrict__ logits,
     int32_t* __restrict__ ids,
     float* __restrict__ weights, uint8_t* __restrict__ xq, float* __restrict__ xs,
     int32_t* __restrict__ hist, int32_t* __restrict__ lrank, uint32_t T, uint32_t E, uint32_t K,
-    uint32_t S, uint32_t RP) {
+    uint32_t S, uint32_t RP, uint32_t Z) {
   constexpr uint32_t H = 128u * NJ;
   constexpr uint32_t P = EMAX / 64u;  // experts per lane
   static_assert(EMAX % 64u == 0 && P <= 8u, "shape");
-  __shared__ uint4 s_x[W][16u * NJ];         // the tokens' rows (bf16)
-  __shared__ uint16_t s_cand[W][EMAX];
+  __shared__ float4 s_x[W][32u * NJ];        // the tokens' rows, widened to fp32
+  __shared__ __align__(16) uint16_t s_cand[W][EMAX];  // also the selected slots (K * 8 <= 2 * EMAX bytes)
   __shared__ uint16_t s_exact[W][EMAX + 1];  // exact logit bits, candidate order; shared row last
   __shared__ int32_t s_ids[W][kMaxSlots];
-  __shared__ uint2 s_sel[W][kMaxSlots];       // (expert, code) by slot
   __shared__ uint32_t s_hist[EMAX + 1];
+  __shared__ float s_wn[EMAX];  // router-row norms, ||w_e|| (1 + 2^-9), from the screen's Z partial sums
   const uint32_t rows = E + S, Ktot = K + S;
   if (E > EMAX || K == 0 || K > E || Ktot > kMaxSlots || S > 1u) return;  // uniform
   constexpr uint32_t kThreads = 64u * W;
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
-  for (uint32_t e = tid; e <= EMAX; e += kThreads) s_hist[e] = 0u;
+  for (uint32_t e = tid; e <= EMAX; e += kThreads) {
+    s_hist[e] = 0u;
+    if (e < E) {
+      float q = 0.0f;
+      for (uint32_t z = 0; z < Z; ++z) q += wsq[(size_t)z * RP + e];
+      s_wn[e] = sqrtf(q) * kNormSlack;
+    }
+  }
   __syncthreads();
   const uint32_t s = lane & 15u, g = lane >> 4;
 
@@ -249,7 +261,8 @@ __device__ __forceinline__ void route_select(
     for (uint32_t p = 0; p < H / 512u; ++p) {
       const uint32_t i0 = 512u * p + 8u * lane;
       const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)t * H + i0);
-      s_x[tt][64u * p + lane] = v;
+      s_x[tt][i0 / 4u] = make_float4(nk::bf16_lo(v.x), nk::bf16_hi(v.x), nk::bf16_lo(v.y), nk::bf16_hi(v.y));
+      s_x[tt][i0 / 4u + 1u] = make_float4(nk::bf16_lo(v.z), nk::bf16_hi(v.z), nk::bf16_lo(v.w), nk::bf16_hi(v.w));
       quant8(v, xq + (size_t)t * H + i0, xs + (size_t)t * NJ + (i0 >> 7), s == 0);
       xx += sumsq8(v);
     }
@@ -258,7 +271,7 @@ __device__ __forceinline__ void route_select(
     const float mx = kScreenMargin * sqrtf(xx) * kNormSlack;
 
     // 1. certified candidates
-    const float* srow = screen + (size_t)t * RP;
+    const float* srow = screen + (size_t)t * RP;  // split z at srow + z * T * RP
     uint32_t clo[P], chi[P];
     float aval[P];
 #pragma unroll
@@ -267,8 +280,9 @@ __device__ __forceinline__ void route_select(
       clo[j] = chi[j] = 0u;
       aval[j] = 0.0f;
       if (e < E) {
-        const float a = srow[e];
-        const float m = mx * wnorm[e];
+        float a = srow[e];
+        for (uint32_t z = 1; z < Z; ++z) a += srow[(size_t)z * T * RP + e];
+        const float m = mx * s_wn[e];
         const float b = bias[e];
         aval[j] = a;
         clo[j] = nk::order_bits(nk::bf16_f32(nk::bf16_rne(a - m)) + b);
@@ -303,6 +317,9 @@ __device__ __forceinline__ void route_select(
     const uint32_t jobs = n + S;
 #pragma unroll 1
     for (uint32_t q = g; q < jobs; q += 4u) {
+      // Re-read the token row from LDS for every job: kept in registers
+      // across jobs it costs 128 VGPRs and halves the resident waves.
+      asm volatile("" ::: "memory");
       const uint32_t e = q < n ? (uint32_t)s_cand[tt][q] : E;
       uint4 wv[NJ];
 #pragma unroll
@@ -328,11 +345,14 @@ __device__ __forceinline__ void route_select(
         const uint32_t e2 = (uint32_t)__builtin_amdgcn_readlane((int)ei, (int)i);
         rank += (c2 > ci || (c2 == ci && e2 < ei)) ? 1u : 0u;
       }
-      if (lane < n && rank < K) s_sel[tt][rank] = make_uint2(ei, ci);
+      // (expert, code) by slot, over the candidate list: this wave read its
+      // entries into ei above, and a wave's LDS accesses complete in order
+      uint2* sel_slots = reinterpret_cast<uint2*>(s_cand[tt]);
+      if (lane < n && rank < K) sel_slots[rank] = make_uint2(ei, ci);
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
       __builtin_amdgcn_wave_barrier();
       if (lane < K) {
-        const uint2 sel = s_sel[tt][lane];
+        const uint2 sel = sel_slots[lane];
         my_id = sel.x;
         my_code = sel.y;
       }
@@ -426,28 +446,35 @@ __device__ __forceinline__ void route_select(
 
 }  // namespace nkroute
 
-#define NK_ROUTE_SCREEN(HV)                                                                       \
-  NK_KERNEL __launch_bounds__(256) void netra_moe_route_screen_h##HV##_gfx950(                    \
+#define NK_ROUTE_SCREEN(HV, KBS)                                                                  \
+  NK_KERNEL __launch_bounds__(256) void netra_moe_route_screen_h##HV##_k##KBS##_gfx950(           \
       const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, float* __restrict__ screen,  \
-      float* __restrict__ wnorm, uint32_t T, uint32_t H, uint32_t rows, uint32_t RP) {            \
+      float* __restrict__ wsq, uint32_t T, uint32_t H, uint32_t rows, uint32_t RP) {              \
     (void)H;                                                                                      \
-    nkroute::route_screen<HV / 128>(x, w, screen, wnorm, T, rows, RP);                            \
+    nkroute::route_screen<HV / 128, KBS>(x, w, screen, wsq, T, rows, RP);                         \
   }
-NK_ROUTE_SCREEN(512)
-NK_ROUTE_SCREEN(1024)
-NK_ROUTE_SCREEN(2048)
+NK_ROUTE_SCREEN(512, 2)
+NK_ROUTE_SCREEN(512, 4)
+NK_ROUTE_SCREEN(1024, 2)
+NK_ROUTE_SCREEN(1024, 4)
+NK_ROUTE_SCREEN(1024, 8)
+NK_ROUTE_SCREEN(2048, 2)
+NK_ROUTE_SCREEN(2048, 4)
+NK_ROUTE_SCREEN(2048, 8)
+NK_ROUTE_SCREEN(2048, 16)
 
 #define NK_ROUTE_SELECT(HV, EMAXV, WV)                                                            \
-  NK_KERNEL __launch_bounds__(64 * WV) void netra_moe_route_select_h##HV##_e##EMAXV##_w##WV##_gfx950( \
+  NK_KERNEL __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(4)))                     \
+  void netra_moe_route_select_h##HV##_e##EMAXV##_w##WV##_gfx950(                                 \
       const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,                             \
       const float* __restrict__ bias, const float* __restrict__ screen,                           \
-      const float* __restrict__ wnorm, uint16_t* __restrict__ logits, int32_t* __restrict__ ids,  \
+      const float* __restrict__ wsq, uint16_t* __restrict__ logits, int32_t* __restrict__ ids,    \
       float* __restrict__ weights, uint8_t* __restrict__ xq, float* __restrict__ xs,              \
       int32_t* __restrict__ hist, int32_t* __restrict__ lrank, uint32_t T, uint32_t H, uint32_t E, \
-      uint32_t K, uint32_t S, uint32_t RP) {                                                      \
+      uint32_t K, uint32_t S, uint32_t RP, uint32_t Z) {                                          \
     (void)H;                                                                                      \
-    nkroute::route_select<HV / 128, EMAXV, WV>(x, w, bias, screen, wnorm, logits, ids, weights,   \
-                                               xq, xs, hist, lrank, T, E, K, S, RP);              \
+    nkroute::route_select<HV / 128, EMAXV, WV>(x, w, bias, screen, wsq, logits, ids, weights,     \
+                                               xq, xs, hist, lrank, T, E, K, S, RP, Z);           \
   }
 #define NK_ROUTE_SELECT_W(HV, EMAXV) NK_ROUTE_SELECT(HV, EMAXV, 4) NK_ROUTE_SELECT(HV, EMAXV, 8)
 NK_ROUTE_SELECT_W(512, 256)
@@ -501,13 +528,14 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_sort_count_gfx950(
 // thread summing a contiguous run of them), then
 //  - scatters its 256 routes: route r = (t, s) of expert e lands at row
 //    block_off[e] * 64 + base[e][t / W] + lrank[r], written as (s << 24) | t;
-//  - for experts e = blockIdx.x, + gridDim.x, ...: sorted_expert of its
-//    blocks, its tile_map and pair_map entries, and its padding rows
-//    (Ktot << 24) | T after its routes;
+//  - one expert per wave (e = 4 blockIdx.x + wave, + 4 gridDim.x, ...):
+//    sorted_expert of its blocks, its tile_map and pair_map entries, and its
+//    padding rows (Ktot << 24) | T after its routes;
 //  - a grid-stride share of the unused blocks: sorted_expert -1, every row
 //    padding;
 //  - workgroup 0: num_valid = {padded rows, routes, tiles, pairs}.
-// Grid ceil(T * Ktot / 256) x 256 threads; dynamic LDS 4 * (4 * Etot + 3) bytes.
+// Grid max(ceil(T * Ktot / 256), ceil(Etot / 4)) x 256 threads; dynamic LDS
+// 4 * (4 * Etot + 3) bytes.
 NK_KERNEL __launch_bounds__(256) void netra_moe_sort_place_gfx950(
     const int32_t* __restrict__ ids, const int32_t* __restrict__ base, const int32_t* __restrict__ lrank,
     const int32_t* __restrict__ counts, int32_t* __restrict__ sorted_ids,
@@ -582,14 +610,14 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_sort_place_gfx950(
                          (uint32_t)my_rank;
     if (pos < cap_blocks * 64u) sorted_ids[pos] = (int32_t)((s << 24) | t);
   }
-  for (uint32_t e = blockIdx.x; e < Etot; e += gridDim.x) {
+  for (uint32_t e = blockIdx.x * 4u + wave; e < Etot; e += gridDim.x * 4u) {  // one expert per wave
     const uint32_t b0 = block_off[e], b1 = block_off[e + 1u];
-    for (uint32_t b = b0 + tid; b < b1; b += 256u) sorted_expert[b] = (int32_t)e;
+    for (uint32_t b = b0 + lane; b < b1; b += 64u) sorted_expert[b] = (int32_t)e;
     const uint32_t i0 = tile_off[e], i1 = tile_off[e + 1u];
-    for (uint32_t i = i0 + tid; i < i1; i += 256u) tile_map[i] = (int32_t)(b0 * 4u + (i - i0));
+    for (uint32_t i = i0 + lane; i < i1; i += 64u) tile_map[i] = (int32_t)(b0 * 4u + (i - i0));
     const uint32_t p0 = pair_off[e], p1 = pair_off[e + 1u];
-    for (uint32_t i = p0 + tid; i < p1; i += 256u) pair_map[i] = (int32_t)(b0 + 2u * (i - p0));
-    const uint32_t row = b0 * 64u + cnt[e] + tid;  // at most 63 rows after the expert's routes
+    for (uint32_t i = p0 + lane; i < p1; i += 64u) pair_map[i] = (int32_t)(b0 + 2u * (i - p0));
+    const uint32_t row = b0 * 64u + cnt[e] + lane;  // at most 63 rows after the expert's routes
     if (row < b1 * 64u) sorted_ids[row] = pad;
   }
   const uint32_t stride = gridDim.x * 256u;

@@ -106,6 +106,22 @@ def resolve_front(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> st
     return front
 
 
+SCREEN_WG_TARGET = 160               # route_screen: split K until the grid has this many workgroups
+                                     # (measured: T=512 screen 14.3 -> 6.1 us at 4 splits; 8 splits cost the select more)
+
+
+def screen_splits(cfg: MoEConfig) -> int:
+    """K splits of the screen GEMM (netra_moe_route_screen_h<H>_k<H/128/Z>): the
+    smallest power of two giving SCREEN_WG_TARGET workgroups, at least two
+    128-K blocks per split."""
+    tiles = (cfg.T + 63) // 64 * (screen_row_pad(cfg) // 64)
+    nj = cfg.H // 128
+    z = 1
+    while tiles * z < SCREEN_WG_TARGET and nj // (2 * z) >= 2:
+        z *= 2
+    return z
+
+
 def screen_row_pad(cfg: MoEConfig) -> int:
     """Router rows rounded up to the screen GEMM's 64-row tiles (row stride of the screen buffer)."""
     return (cfg.router_rows + 63) // 64 * 64
@@ -153,8 +169,8 @@ def tensor_table(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> dic
     if front == "exact":
         specs.append(TensorSpec("mask", "u64", (cfg.Etot, cfg.mask_words_per_expert), "temporary"))
     else:
-        specs += [TensorSpec("screen", "f32", (T, screen_row_pad(cfg)), "temporary"),
-                  TensorSpec("route_wnorm", "f32", (screen_row_pad(cfg),), "temporary"),
+        specs += [TensorSpec("screen", "f32", (screen_splits(cfg), T, screen_row_pad(cfg)), "temporary"),
+                  TensorSpec("route_wsq", "f32", (screen_splits(cfg), screen_row_pad(cfg)), "temporary"),
                   TensorSpec("route_base", "i32", (cfg.Etot, screen_groups(cfg)), "temporary"),
                   TensorSpec("route_rank", "i32", (T * cfg.Ktot,), "temporary")]
     if path == "stream":
@@ -191,19 +207,20 @@ def _screen_front(cfg: MoEConfig) -> list[dict]:
     G = screen_groups(cfg)
     Wt = screen_tokens(cfg)
     RP = screen_row_pad(cfg)
+    Z = screen_splits(cfg)
     return [
-        dict(name="moe.route_screen", symbol=f"netra_moe_route_screen_h{H}_gfx950",
-             grid=((T + 63) // 64, RP // 64, 1), block=(256, 1, 1), lds=2 * 2 * 64 * 136 * 2, dyn=0,
-             args=["x", "router_w", "screen", "route_wnorm", u(T), u(H), u(cfg.router_rows), u(RP)],
-             reads=["x", "router_w"], writes=["screen", "route_wnorm"],
+        dict(name="moe.route_screen", symbol=f"netra_moe_route_screen_h{H}_k{H // 128 // Z}_gfx950",
+             grid=((T + 63) // 64, RP // 64, Z), block=(256, 1, 1), lds=2 * 2 * 64 * 136 * 2, dyn=0,
+             args=["x", "router_w", "screen", "route_wsq", u(T), u(H), u(cfg.router_rows), u(RP)],
+             reads=["x", "router_w"], writes=["screen", "route_wsq"],
              refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150"]),
         dict(name="moe.route_select",
              symbol=f"netra_moe_route_select_h{H}_e{screen_emax(cfg)}_w{Wt}_gfx950",
              grid=(G, 1, 1), block=(64 * Wt, 1, 1),
-             lds=Wt * (H * 2 + 2 * (2 * screen_emax(cfg) + 1) + 64 * 12) + 4 * (screen_emax(cfg) + 1), dyn=0,
-             args=["x", "router_w", "router_bias", "screen", "route_wnorm", "logits", "topk_ids", "topk_weights", "x_q",
-                   "x_scale", "route_base", "route_rank", u(T), u(H), u(cfg.E), u(cfg.K), u(cfg.S), u(RP)],
-             reads=["x", "router_w", "router_bias", "screen", "route_wnorm"],
+             lds=Wt * (H * 4 + 2 * (2 * screen_emax(cfg) + 1) + 64 * 4) + 8 * screen_emax(cfg) + 4, dyn=0,
+             args=["x", "router_w", "router_bias", "screen", "route_wsq", "logits", "topk_ids", "topk_weights", "x_q",
+                   "x_scale", "route_base", "route_rank", u(T), u(H), u(cfg.E), u(cfg.K), u(cfg.S), u(RP), u(Z)],
+             reads=["x", "router_w", "router_bias", "screen", "route_wsq"],
              writes=["logits", "topk_ids", "topk_weights", "x_q", "x_scale", "route_base", "route_rank"],
              refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150",
                    "runtime/gfx950/routing/decode/qwen36_shared_gate_append_bridge.hip:76-112"]),
@@ -213,7 +230,7 @@ def _screen_front(cfg: MoEConfig) -> list[dict]:
              reads=["route_base"], writes=["route_base", "expert_counts"],
              refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]),
         dict(name="moe.sort_place", symbol="netra_moe_sort_place_gfx950",
-             grid=((T * cfg.Ktot + 255) // 256, 1, 1), block=(256, 1, 1), lds=4 * 12,
+             grid=(max((T * cfg.Ktot + 255) // 256, (cfg.Etot + 3) // 4), 1, 1), block=(256, 1, 1), lds=4 * 12,
              dyn=4 * (4 * cfg.Etot + 3),
              args=["topk_ids", "route_base", "route_rank", "expert_counts", "sorted_ids", "sorted_expert",
                    "tile_map", "pair_map", "num_valid",

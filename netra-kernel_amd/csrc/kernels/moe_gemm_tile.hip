@@ -367,6 +367,155 @@ __device__ __forceinline__ void down_tile(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Grouped down GEMM over row blocks (reference: kernels/gfx950/templates/moe/
+// prefill/fused_splitk2/down_partial.inc and route_reduce_splitk2_f16.inc:6-117;
+// oracle tools/benchmark/export_qwen36_moe_stage2_capture.py:90-110).
+//
+// Item (b, c): expert block b against NBC consecutive 128-column groups
+// nb = c NBC .. (c + 1) NBC - 1 of H, 8 waves. The block's FP8 rows (64 x I)
+// and their 1x128 scales are staged in LDS once per item; wave w owns columns
+// 128 nb + 16 w .. +15 of every group (one 16-row W2 tile, K contiguous) and
+// refills each K block's weight registers with the next group's tile right
+// after using them (a one-group register ring, so a group of loads is always
+// in flight). Per 128-K block acc += (w_s(nb, kb) * h_s(row, kb)) * mfma. Each
+// group's result, rounded to bf16, goes through an LDS transpose (two
+// buffers, one barrier per group) so each route row leaves as 256 contiguous
+// bytes; rows past the block's valid count take an offset past the buffer
+// and the hardware drops their stores.
+constexpr uint32_t kDownWaves = 8;
+
+template <uint32_t KB>  // I / 128
+__device__ __forceinline__ void down_rows(
+    const uint8_t* __restrict__ hq, const float* __restrict__ hs, const uint8_t* __restrict__ w2,
+    const float* __restrict__ w2s, const int32_t* __restrict__ sorted_ids,
+    const int32_t* __restrict__ sorted_expert, const int32_t* __restrict__ num_valid,
+    uint16_t* __restrict__ partial, uint32_t T, uint32_t H, uint32_t Ktot, uint32_t Etot, uint32_t NBC) {
+  constexpr uint32_t I = 128u * KB;
+  constexpr uint32_t kThreads = 64u * kDownWaves;
+  constexpr uint32_t kStride = I + 16u;  // LDS bytes per A row
+  constexpr uint32_t kOut = 256u + 16u;  // LDS bytes per output row (128 bf16 + pad)
+  static_assert((KB & (KB - 1u)) == 0 && KB <= 64u, "one scale lane per K block");
+  __shared__ __align__(16) uint8_t s_a[kRows * kStride];
+  __shared__ __align__(16) uint8_t s_out[2][kRows * kOut];
+  __shared__ __align__(16) float s_hs[KB * kRows];  // h_s(row, kb) at [kb][row]
+  __shared__ int32_t s_route[kRows];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
+  const uint32_t NB = H / 128u, NCH = NB / NBC;
+  if (NBC == 0u || NCH * NBC != NB) return;  // the engine passes a divisor of H / 128
+  uint32_t item;
+  if (!xcd_item(blockIdx.x, ((uint32_t)num_valid[0] / kRows) * NCH, item)) return;
+  const uint32_t b = item / NCH, nb0 = (item - b * NCH) * NBC;
+  const int32_t e = sorted_expert[b];
+  if (e < 0 || (uint32_t)e >= Etot) return;
+  if (tid < kRows) {
+    const int32_t id = sorted_ids[b * kRows + tid];
+    const uint32_t t = (uint32_t)id & 0xffffffu, slot = (uint32_t)id >> 24;
+    s_route[tid] = (t < T && slot < Ktot) ? (int32_t)(t * Ktot + slot) : -1;
+  }
+  // The expert's W2 in tile16x128 (row tile rt's K blocks contiguous); wave
+  // w's tile of group nb is row tile 8 nb + w. Its weight scales come one per
+  // lane (lane kb holds w_s(nb, kb)) by a vector load: a scalar load would
+  // share the LDS counter and make the next LDS wait a full drain.
+  const __amdgpu_buffer_rsrc_t wt = nk::buffer_rsrc(w2 + (size_t)e * H * I, H * I);
+  const float* wse = w2s + (size_t)e * NB * KB;
+  v8i bq[KB];
+#pragma unroll
+  for (uint32_t kb = 0; kb < KB; ++kb) bq[kb] = nk::load_tile_operand(wt, ((nb0 * 8u + wave) * KB + kb) * 2048u, lane);
+  float wsv = wse[nb0 * KB + (lane & (KB - 1u))];
+  // the block's A rows (64 x I bytes, contiguous) and scales
+  constexpr uint32_t kA16 = kRows * I / 16u / kThreads;  // uint4 per thread
+  static_assert(kA16 >= 1u, "A staging");
+  uint4 areg[kA16];
+  const uint8_t* ablk = hq + (size_t)b * kRows * I;
+#pragma unroll
+  for (uint32_t p = 0; p < kA16; ++p) areg[p] = reinterpret_cast<const uint4*>(ablk)[p * kThreads + tid];
+  for (uint32_t i = tid; i < kRows * KB; i += kThreads) {
+    const uint32_t row = i / KB, kb = i - row * KB;
+    s_hs[kb * kRows + row] = hs[(size_t)b * kRows * KB + i];
+  }
+#pragma unroll
+  for (uint32_t p = 0; p < kA16; ++p) {
+    const uint32_t idx = p * kThreads + tid;  // uint4 index in the block
+    const uint32_t row = idx / (I / 16u), c16 = idx - row * (I / 16u);
+    *reinterpret_cast<uint4*>(&s_a[row * kStride + c16 * 16u]) = areg[p];
+  }
+  lds_barrier();
+  const uint32_t nvalid = (uint32_t)__popcll(__ballot(s_route[lane] >= 0));
+  const uint32_t ntiles = (nvalid + 15u) >> 4;
+  const uint32_t g = lane >> 4;
+  // output stores (64 rows x 256 bytes, 2 uint4 per thread): rows past nvalid
+  // (or padding) take offset 2^31, past the buffer's range (the engine keeps
+  // the partial buffer below 2^31 bytes), so their stores are dropped
+  const __amdgpu_buffer_rsrc_t pr = nk::buffer_rsrc(partial, T * Ktot * H * 2u);
+  uint32_t soff[2];
+#pragma unroll
+  for (uint32_t p = 0; p < 2u; ++p) {
+    const uint32_t idx = p * kThreads + tid, row = idx >> 4, c16 = idx & 15u;
+    const int32_t route = s_route[row];
+    soff[p] = (row < nvalid && route >= 0) ? ((uint32_t)route * H + c16 * 8u) * 2u : 0x80000000u;
+  }
+
+  auto run = [&](auto ntc) __attribute__((always_inline)) {
+    constexpr uint32_t NT = decltype(ntc)::value;
+#pragma unroll 1
+    for (uint32_t q = 0; q < NBC; ++q) {
+      const uint32_t nb = nb0 + q, nbn = nb0 + (q + 1u < NBC ? q + 1u : q);  // the last refill repeats nb
+      const float wsn = wse[nbn * KB + (lane & (KB - 1u))];
+      v4f acc[NT];
+#pragma unroll
+      for (uint32_t rt = 0; rt < NT; ++rt) acc[rt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (uint32_t kb = 0; kb < KB; ++kb) {
+        const float ws = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(wsv), (int)kb));
+        v4f d[NT];
+#pragma unroll
+        for (uint32_t rt = 0; rt < NT; ++rt)
+          d[rt] = nk::mfma_e4m3_16x16x128(lds_fp8x32(&s_a[(rt * 16u + (lane & 15u)) * kStride + kb * 128u + g * 32u]),
+                                          bq[kb]);
+        bq[kb] = nk::load_tile_operand(wt, ((nbn * 8u + wave) * KB + kb) * 2048u, lane);  // next group's tile
+#pragma unroll
+        for (uint32_t rt = 0; rt < NT; ++rt) {
+          const float4 h4 = *reinterpret_cast<const float4*>(&s_hs[kb * kRows + rt * 16u + g * 4u]);
+          acc[rt][0] = fmaf(ws * h4.x, d[rt][0], acc[rt][0]);
+          acc[rt][1] = fmaf(ws * h4.y, d[rt][1], acc[rt][1]);
+          acc[rt][2] = fmaf(ws * h4.z, d[rt][2], acc[rt][2]);
+          acc[rt][3] = fmaf(ws * h4.w, d[rt][3], acc[rt][3]);
+        }
+        // This block's accumulation completes here (the accumulators are
+        // operands of the asm) and the next block's LDS reads stay below it
+        // (memory clobber): otherwise the compiler issues every block's MFMAs
+        // first and holds all their results, which costs ~128 VGPRs.
+#pragma unroll
+        for (uint32_t rt = 0; rt < NT; ++rt) asm volatile("" : "+v"(acc[rt]) : : "memory");
+      }
+      wsv = wsn;
+      uint8_t* so = s_out[q & 1u];
+#pragma unroll
+      for (uint32_t rt = 0; rt < NT; ++rt)
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j)
+          *reinterpret_cast<uint16_t*>(&so[(rt * 16u + g * 4u + j) * kOut + (wave * 16u + (lane & 15u)) * 2u]) =
+              nk::bf16_rne(acc[rt][j]);
+      lds_barrier();  // the group's tile is complete; the other buffer was read before the last barrier
+#pragma unroll
+      for (uint32_t p = 0; p < 2u; ++p) {
+        const uint32_t idx = p * kThreads + tid, row = idx >> 4, c16 = idx & 15u;
+        const uint4 v = *reinterpret_cast<const uint4*>(&so[row * kOut + c16 * 16u]);
+        __builtin_amdgcn_raw_buffer_store_b128(nk::u32x4{v.x, v.y, v.z, v.w}, pr, (int)soff[p],
+                                               (int)(nb * 256u), 0);
+      }
+    }
+  };
+  switch (ntiles) {
+    case 1: run(std::integral_constant<uint32_t, 1>{}); break;
+    case 2: run(std::integral_constant<uint32_t, 2>{}); break;
+    case 3: run(std::integral_constant<uint32_t, 3>{}); break;
+    default: run(std::integral_constant<uint32_t, 4>{}); break;
+  }
+}
+
 }  // namespace nktile
 
 // Gate/up tile kernels: 4 waves x 32 columns, one weight block in flight
@@ -412,3 +561,18 @@ NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h2048_w8_a1_o4_gfx950, 2048, 8, 1, NK_O
 NK_DOWN_TILE(256)
 NK_DOWN_TILE(512)
 NK_DOWN_TILE(1024)
+
+#define NK_DOWN_ROWS(IV)                                                                           \
+  NK_KERNEL __launch_bounds__(512)                                                                \
+  void netra_moe_down_rows_i##IV##_gfx950(                                                        \
+      const uint8_t* __restrict__ hq, const float* __restrict__ hs, const uint8_t* __restrict__ w2, \
+      const float* __restrict__ w2s, const int32_t* __restrict__ sorted_ids,                       \
+      const int32_t* __restrict__ sorted_expert, const int32_t* __restrict__ num_valid,            \
+      uint16_t* __restrict__ partial, uint32_t T, uint32_t H, uint32_t I, uint32_t Ktot,           \
+      uint32_t Etot, uint32_t NBC) {                                                               \
+    (void)I;                                                                                       \
+    nktile::down_rows<IV / 128>(hq, hs, w2, w2s, sorted_ids, sorted_expert, num_valid, partial, T, \
+                                H, Ktot, Etot, NBC);                                               \
+  }
+NK_DOWN_ROWS(256)
+NK_DOWN_ROWS(512)

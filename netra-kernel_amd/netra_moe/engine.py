@@ -54,6 +54,8 @@ STREAM_H = (512, 1024, 2048, 4096)   # netra_moe_gate_up_stream_h<H>_gfx950
 STREAM_I = (256, 512, 1024, 2048)    # netra_moe_down_stream_i<I>_gfx950
 TILE_H = (512, 1024, 2048, 4096)     # netra_moe_gate_up_tile_h<H>_gfx950
 TILE_I = (256, 512, 1024)            # netra_moe_down_tile_i<I>_gfx950
+ROWS_I = (256, 512)                  # netra_moe_down_rows_i<I>_gfx950 (block rows x runs of column groups)
+DOWN_ROWS_ITEMS = 1024               # down_rows: fewer column groups per item until about this many items
 TILE_GU_WAVES = 4                    # waves of netra_moe_gate_up_tile_h<H>_gfx950 (its launch bound)
 LDS_GU_H = (512, 1024, 2048)         # netra_moe_gate_up_lds_h<H>_gfx950: 128-row pairs, LDS operand ring
 # Stream kernel grids (measured at T=64 on one MI355X): gate/up fills the chip
@@ -241,6 +243,39 @@ def _screen_front(cfg: MoEConfig) -> list[dict]:
                    "manifests/gfx950/models/qwen36-35b-c64-fp8.json:43-49"]),
     ]
 
+def down_rows_groups(cfg: MoEConfig) -> int:
+    """128-column groups per netra_moe_down_rows item: all H / 128 when the
+    expected block count fills the chip, else fewer (a power of two) so that
+    about DOWN_ROWS_ITEMS items exist."""
+    nb = cfg.H // 128
+    blocks = (cfg.routes + 63) // 64 + min(cfg.Etot, cfg.routes) // 2  # expected non-empty blocks
+    nbc = nb
+    while nbc > 1 and nbc % 2 == 0 and blocks * (nb // nbc) < DOWN_ROWS_ITEMS:
+        nbc //= 2
+    return nbc
+
+
+def _tile_down(cfg: MoEConfig) -> dict:
+    T, H, I = cfg.T, cfg.H, cfg.I
+    u = lambda v: ("u32", int(v))  # noqa: E731
+    common = ["sorted_ids", "sorted_expert", "num_valid"]
+    refs = ["kernels/gfx950/templates/moe/prefill/fused_splitk2/down_partial.inc",
+            "kernels/gfx950/templates/moe/prefill/route_reduce_splitk2_f16.inc:6-117"]
+    if I in ROWS_I and cfg.routes * H * 2 < 1 << 31:
+        nbc = down_rows_groups(cfg)
+        return dict(name="moe.down", symbol=f"netra_moe_down_rows_i{I}_gfx950",
+                    grid=(xcd_grid(cfg.cap_blocks * (H // 128 // nbc)), 1, 1), block=(512, 1, 1),
+                    lds=64 * (I + 16) + 2 * 64 * 272 + 64 * (I // 128) * 4 + 64 * 4, dyn=0,
+                    args=["h_q", "h_scale", "w2", "w2_scale", *common, "partial",
+                          u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot), u(nbc)],
+                    reads=["h_q", "h_scale", "w2", "w2_scale", *common], writes=["partial"], refs=refs)
+    return dict(name="moe.down", symbol=f"netra_moe_down_tile_i{I}_gfx950",
+                grid=(xcd_grid(cfg.cap_blocks * (H // 128)), 1, 1), block=(256, 1, 1),
+                lds=max(64 * (I + 16), 64 * 272) + 64 * (I // 128) * 4 + 64 * 4, dyn=0,
+                args=["h_q", "h_scale", "w2", "w2_scale", *common, "partial",
+                      u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
+                reads=["h_q", "h_scale", "w2", "w2_scale", *common], writes=["partial"], refs=refs)
+
 
 def operations(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> list[dict]:
     """The six launches of one layer call, in stream order."""
@@ -322,14 +357,7 @@ def operations(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> list[
                       "kernels/gfx950/templates/moe/prefill/fused_splitk2/silu_quant.inc"])
         ops += [
             gate_up,
-            dict(name="moe.down", symbol=f"netra_moe_down_tile_i{I}_gfx950",
-                 grid=(xcd_grid(cfg.cap_blocks * (H // 128)), 1, 1), block=(256, 1, 1),
-                 lds=max(64 * (I + 16), 64 * 272) + 64 * (I // 128) * 4 + 64 * 4, dyn=0,
-                 args=["h_q", "h_scale", "w2", "w2_scale", *common, "partial",
-                       u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
-                 reads=["h_q", "h_scale", "w2", "w2_scale", *common], writes=["partial"],
-                 refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/down_partial.inc",
-                       "kernels/gfx950/templates/moe/prefill/route_reduce_splitk2_f16.inc:6-117"]),
+            _tile_down(cfg),
         ]
     combine_sym, combine_cols = ("netra_moe_combine_gfx950", 1024) if path == "stream" else \
         ("netra_moe_combine_bf16_gfx950", 2048)

@@ -27,28 +27,31 @@
 //       grid 1, block 1024, dynamic LDS 4*B + (8*Etot*W if that stays <= 160 KiB),
 //       B = Etot*W + 4*Etot + 51 + CAP rounded up to even
 //   prefill ("screen") front end, H in {512,1024,2048}, EMAX in {256,512}:
-//   netra_moe_route_screen_h<H>_gfx950(x, w, screen f32[T,RP], wnorm f32[RP];
-//       T, H, rows, RP)   grid (ceil(T/64), RP/64), block 256, RP = rows
-//       rounded up to 64; workgroups with blockIdx.x == 0 write wnorm
-//   netra_moe_route_select_h<H>_e<EMAX>_gfx950(x, w, bias, screen, wnorm, logits, ids,
-//       weights, xq, xs, route_base i32[G,Etot], route_rank i32[T*Ktot];
-//       T, H, E, K, S, RP)   grid G = ceil(T/16), block 512
-//   netra_moe_sort_scan_gfx950(route_base, sorted_ids, sorted_expert, tile_map,
-//       pair_map, num_valid, counts; T, Ktot, Etot, G, CAP)   grid 1, block 1024,
-//       dynamic LDS 4*(1024 + 4*Etot + 51 + CAP)
-//   netra_moe_sort_scatter_gfx950(ids, route_base, route_rank, sorted_ids;
-//       T, Ktot, Etot, CAP)   grid ceil(T*Ktot/256), block 256
+//   netra_moe_route_screen_h<H>_k<KBS>_gfx950(x, w, screen f32[Z,T,RP],
+//       wsq f32[Z,RP]; T, H, rows, RP)   grid (ceil(T/64), RP/64, Z), block 256,
+//       RP = rows rounded up to 64, Z = H/128/KBS K splits (KBS in {2,4,8,16},
+//       at most H/128); workgroups with blockIdx.x == 0 write the partial
+//       squared router-row norms wsq
+//   netra_moe_route_select_h<H>_e<EMAX>_w<W>_gfx950(x, w, bias, screen, wsq, logits,
+//       ids, weights, xq, xs, route_base i32[Etot,G], route_rank i32[T*Ktot];
+//       T, H, E, K, S, RP, Z)   grid G = ceil(T/W), block 64*W, W in {4,8}
+//       (one token per wave)
+//   netra_moe_sort_count_gfx950(route_base, counts; G, Etot)   grid Etot, block 256
+//   netra_moe_sort_place_gfx950(ids, route_base, route_rank, counts, sorted_ids,
+//       sorted_expert, tile_map, pair_map, num_valid; T, Ktot, Etot, G, W, CAP)
+//       grid max(ceil(T*Ktot/256), ceil(Etot/4)), block 256, dynamic LDS 4*(4*Etot+3)
 //   decode ("stream") GEMMs, H in {512,1024,2048,4096}, I in {256,512,1024,2048}:
 //   (every w13 below is in the gate/up-interleaved tile16x128 layout of
 //   netra_moe_pack_tiles_gate_up)
-//   netra_moe_gate_up_stream_h<H>_gfx950(xq, xs, w13 e4m3[Etot,2I,H],
+//   netra_moe_gate_up_stream_h<H>_c<CH>_gfx950(xq, xs, w13 e4m3[Etot,2I,H],
 //       w13s f32[Etot,2I/128,H/128], sorted_ids, sorted_expert, tile_map, num_valid,
-//       h bf16[CAP*64,I] (tiled); T, H, I, Ktot, Etot)   grid 512, block 256 (persistent)
-//   netra_moe_requant_h_gfx950(h, hq e4m3[CAP*64,I] (tile16x128),
-//       hs f32[CAP*4,I/128,16], tile_map, num_valid; I)   grid 256, block 256
-//   netra_moe_down_stream_i<I>_gfx950(hq, hs, w2 e4m3[Etot,H,I], w2s f32[Etot,H/128,I/128],
-//       sorted_ids, sorted_expert, tile_map, num_valid, partial f32[T*Ktot,H];
-//       T, H, I, Ktot, Etot)   grid 1024, block 256 (persistent)
+//       hq e4m3[CAP*64,I] (tile16x128), hs f32[CAP*4,I/128,16]; T, H, I, Ktot, Etot)
+//       grid 256, block 512 (persistent; CH K blocks per prefetch step, 2 or 4;
+//       h = bf16(silu(g)*u) is requantised 1x128 in the epilogue)
+//   netra_moe_down_stream_i<I>_c<DC>_gfx950(hq, hs, w2 e4m3[Etot,H,I],
+//       w2s f32[Etot,H/128,I/128], sorted_ids, sorted_expert, tile_map, num_valid,
+//       partial f32[T*Ktot,H]; T, H, I, Ktot, Etot)   grid 2048, block 256
+//       (DC K blocks per step, 1 or 2)
 //   prefill ("tile") GEMMs, H in {512,1024,2048,4096}, I in {256,512,1024}:
 //   netra_moe_gate_up_tile_h<H>_gfx950(xq, xs, w13, w13s, sorted_ids, sorted_expert,
 //       num_valid, hq e4m3[CAP*64,I], hs f32[CAP*64,I/128]; T, H, I, Ktot, Etot)
@@ -57,8 +60,13 @@
 //       num_valid, pair_map, hq, hs; T, H, I, Ktot, Etot)   H in {512,1024,2048},
 //       grid 8*ceil(CAP*I/128/8), block 512, static LDS <= 155 KiB, T*H < 2^31;
 //       one item per (block pair, 128 h columns), assigned XCD-major
+//   netra_moe_down_rows_i<I>_gfx950(hq, hs, w2, w2s, sorted_ids, sorted_expert, num_valid,
+//       partial bf16[T*Ktot,H]; T, H, I, Ktot, Etot, NBC)   I in {256,512},
+//       grid 8*ceil(CAP*(H/128/NBC)/8), block 512, T*Ktot*H*2 < 2^31; one item per
+//       (64-row block, NBC consecutive 128-column groups), NBC divides H/128
 //   netra_moe_down_tile_i<I>_gfx950(hq, hs, w2, w2s, sorted_ids, sorted_expert, num_valid,
-//       partial bf16[T*Ktot,H]; T, H, I, Ktot, Etot)   grid 8*ceil(CAP*H/128/8), block 256
+//       partial bf16[T*Ktot,H]; T, H, I, Ktot, Etot)   grid 8*ceil(CAP*H/128/8), block 256;
+//       used for I = 1024
 //   netra_moe_combine_gfx950(partial f32, weights, out bf16[T,H]; T, H, Ktot)
 //       grid (ceil(H/1024), T), block 256
 //   netra_moe_combine_bf16_gfx950(partial bf16, weights, out; T, H, Ktot)

@@ -79,7 +79,7 @@ __device__ __forceinline__ void load_tile(TileRows& tr, const int32_t* __restric
 // (8 waves) takes groups w, w + gridDim.x, ... For a group it stages the
 // tile's FP8 activation rows (16 x H, in the MFMA operand layout) and their
 // scales in LDS once, and each wave then streams only the W13 tiles of its P
-// columns, in steps of kGuChunk K blocks, one step ahead. (Loading the 16
+// columns, in steps of CH K blocks, one step ahead. (Loading the 16
 // gathered activation rows from L2 at every step as well doubled the
 // cache-line requests per step and held the weight stream at ~5.1 TB/s.)
 // Each item's 16 x 16 bf16 h block goes to LDS; when the group is done, waves
@@ -87,16 +87,16 @@ __device__ __forceinline__ void load_tile(TileRows& tr, const int32_t* __restric
 // (scale = max(amax, 1e-10) * 0x3b124925, q = e4m3(h * (1 / scale))) and
 // write it in the tile16x128 operand layout with its 16 row scales, which is
 // what the down GEMM loads.
-constexpr uint32_t kGuChunk = 2;
 constexpr uint32_t kGuWaves = 8;
 constexpr uint32_t kGuMaxP = 4;
 
+template <uint32_t CH>
 struct GateUpStep {
-  nk::v8i g[kGuChunk], u[kGuChunk];
+  nk::v8i g[CH], u[CH];
   float ws;  // lane i < KB: gate block scale of K block i; KB <= i < 2 KB: up block scale of K block i - KB
 };
 
-template <uint32_t KB>
+template <uint32_t KB, uint32_t CH>  // H / 128, K blocks per step
 __device__ __forceinline__ void gate_up_stream(
     const uint8_t* __restrict__ xq, const float* __restrict__ xs,
     const uint8_t* __restrict__ w13, const float* __restrict__ w13s,
@@ -106,10 +106,10 @@ __device__ __forceinline__ void gate_up_stream(
     uint32_t Etot) {
   using namespace nkstream;
   constexpr uint32_t H = 128 * KB;
-  constexpr uint32_t NCH = KB / kGuChunk;
+  constexpr uint32_t NCH = KB / CH;
   constexpr uint32_t kThreads = 64u * kGuWaves;
   constexpr uint32_t kHbStride = 128u * kGuMaxP + 8u;  // bf16 per LDS h row (+16 bytes rotates banks)
-  static_assert(KB % (2 * kGuChunk) == 0, "H must be a multiple of 512 (an even step count)");
+  static_assert(KB % (2 * CH) == 0, "an even step count per item");
   static_assert(H % kThreads == 0, "staging moves H / 512 pieces per thread");
   __shared__ __align__(16) uint8_t s_a[KB * 2048u];  // the tile's activations, operand layout per K block
   __shared__ float s_xs[16 * KB];                    // their scales, [row][kb]
@@ -137,11 +137,11 @@ __device__ __forceinline__ void gate_up_stream(
     // Weight scales come in with a vector load (in order with the weights on
     // the vector-memory counter): scalar loads would share the LDS counter,
     // and their out-of-order returns make every LDS wait a full drain.
-    auto issue = [&](GateUpStep& st, uint32_t s) __attribute__((always_inline)) {
+    auto issue = [&](GateUpStep<CH>& st, uint32_t s) __attribute__((always_inline)) {
       const uint32_t c = c0 + s / NCH, ch = s % NCH;
 #pragma unroll
-      for (uint32_t i = 0; i < kGuChunk; ++i) {
-        const uint32_t kb = ch * kGuChunk + i;
+      for (uint32_t i = 0; i < CH; ++i) {
+        const uint32_t kb = ch * CH + i;
         st.g[i] = nk::load_tile_operand(nk::tile_base(we, 2u * c, kb, KB), lane);        // gate tile c
         st.u[i] = nk::load_tile_operand(nk::tile_base(we, 2u * c + 1u, kb, KB), lane);   // up tile c
       }
@@ -171,7 +171,7 @@ __device__ __forceinline__ void gate_up_stream(
       const int32_t t = __shfl(m.row, (i / KB) & 15u);
       xv[q] = i < 16u * KB ? xs[(size_t)(t < 0 ? 0 : t) * KB + i % KB] : 0.0f;
     }
-    GateUpStep b0, b1;
+    GateUpStep<CH> b0, b1;
     issue(b0, 0u);
 #pragma unroll
     for (uint32_t q = 0; q < kPieces; ++q) {
@@ -184,11 +184,11 @@ __device__ __forceinline__ void gate_up_stream(
       if (tid + q * kThreads < 16u * KB) s_xs[tid + q * kThreads] = xv[q];
     lds_barrier();
 
-    auto compute = [&](const GateUpStep& st, uint32_t s) __attribute__((always_inline)) {
+    auto compute = [&](const GateUpStep<CH>& st, uint32_t s) __attribute__((always_inline)) {
       const uint32_t ch = s % NCH;
 #pragma unroll
-      for (uint32_t i = 0; i < kGuChunk; ++i) {
-        const uint32_t kb = ch * kGuChunk + i;
+      for (uint32_t i = 0; i < CH; ++i) {
+        const uint32_t kb = ch * CH + i;
         const nk::v8i a = nk::load_tile_operand(s_a + kb * 2048u, lane);
         const nk::v4f dg = nk::mfma_e4m3_16x16x128(a, st.g[i]);
         const nk::v4f du = nk::mfma_e4m3_16x16x128(a, st.u[i]);
@@ -267,7 +267,7 @@ __device__ __forceinline__ void gate_up_stream(
   }
 }
 
-#define NK_GATE_UP_STREAM_V(NAME, HV, WPE)                                                       \
+#define NK_GATE_UP_STREAM_V(NAME, HV, CH, WPE)                                                   \
   NK_KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WPE)))                     \
   void NAME(                                                                                     \
       const uint8_t* __restrict__ xq, const float* __restrict__ xs,                              \
@@ -277,22 +277,26 @@ __device__ __forceinline__ void gate_up_stream(
       uint8_t* __restrict__ hq, float* __restrict__ hs, uint32_t T, uint32_t H, uint32_t I,      \
       uint32_t Ktot, uint32_t Etot) {                                                            \
     (void)H;                                                                                     \
-    gate_up_stream<HV / 128>(xq, xs, w13, w13s, sorted_ids, sorted_expert, tile_map, num_valid, \
+    gate_up_stream<HV / 128, CH>(xq, xs, w13, w13s, sorted_ids, sorted_expert, tile_map, num_valid, \
                              hq, hs, T, I, Ktot, Etot);                                          \
   }
-#define NK_GATE_UP_STREAM(HV) \
-  NK_GATE_UP_STREAM_V(netra_moe_gate_up_stream_h##HV##_gfx950, HV, NK_GATE_UP_WAVES_PER_EU)
-NK_GATE_UP_STREAM(512)
-NK_GATE_UP_STREAM(1024)
-NK_GATE_UP_STREAM(2048)
-NK_GATE_UP_STREAM(4096)
+// Symbol netra_moe_gate_up_stream_h<H>_c<CH>_gfx950: CH K blocks per step.
+#define NK_GATE_UP_STREAM(HV, CH) \
+  NK_GATE_UP_STREAM_V(netra_moe_gate_up_stream_h##HV##_c##CH##_gfx950, HV, CH, NK_GATE_UP_WAVES_PER_EU)
+NK_GATE_UP_STREAM(512, 2)
+NK_GATE_UP_STREAM(1024, 2)
+NK_GATE_UP_STREAM(1024, 4)
+NK_GATE_UP_STREAM(2048, 2)
+NK_GATE_UP_STREAM(2048, 4)
+NK_GATE_UP_STREAM(4096, 2)
+NK_GATE_UP_STREAM(4096, 4)
 
 // ---------------------------------------------------------------------------
 // (reference: kernels/gfx950/templates/moe/decode/down_reduce_mfma_2wave.inc:
 // 14-291; oracle tools/benchmark/export_qwen36_moe_stage2_capture.py:90-110)
 //
 // Item (tile, c): output columns [32 c, 32 c + 32) (two 16-row W2 tiles) of
-// one 16-row tile; one 128-wide K block per step; per block
+// one 16-row tile; DC 128-wide K blocks per step; per block
 // acc += w_s * (a_s * mfma). After the last step each valid row's fp32 result
 // goes to partial[route].
 //
@@ -305,12 +309,13 @@ NK_GATE_UP_STREAM(4096)
 constexpr uint32_t kDnWaves = 4;
 constexpr uint32_t kDnMaxP = 16;
 
+template <uint32_t DC>
 struct DownStep {
-  nk::v8i w[2];
-  float ws;  // lane 0: w_s of the first 16-row tile's block, lane 1: of the second (vector load)
+  nk::v8i w[DC][2];
+  float ws;  // lane 2 i + t: w_s of 16-row tile t's block at the step's K block i (vector load)
 };
 
-template <uint32_t KB>
+template <uint32_t KB, uint32_t DC>  // I / 128, K blocks per step
 __device__ __forceinline__ void down_stream(
     const uint8_t* __restrict__ hq, const float* __restrict__ hs, const uint8_t* __restrict__ w2,
     const float* __restrict__ w2s, const int32_t* __restrict__ sorted_ids,
@@ -319,10 +324,10 @@ __device__ __forceinline__ void down_stream(
     uint32_t Ktot, uint32_t Etot) {
   using namespace nkstream;
   constexpr uint32_t I = 128 * KB;
-  constexpr uint32_t NCH = KB;
+  constexpr uint32_t NCH = KB / DC;
   constexpr uint32_t kThreads = 64u * kDnWaves;
   constexpr uint32_t kPieces = KB * 128u / kThreads;  // 16-byte pieces of the A operand per thread
-  static_assert(NCH % 2 == 0, "I must be a multiple of 256");
+  static_assert(KB % (2 * DC) == 0, "an even step count per item");
   static_assert(KB * 128u % kThreads == 0, "A operand copy");
   __shared__ __align__(16) uint8_t s_a[KB * 2048u];  // the tile's A operand, KB operand tiles
   __shared__ __align__(16) float s_as[KB * 16u];     // its row scales, [kb][row]
@@ -347,12 +352,15 @@ __device__ __forceinline__ void down_stream(
     const float* wse = w2s + (size_t)m.expert * (H / 128u) * KB;
     // weight scales by a vector load (scalar loads would share the LDS
     // counter, and their out-of-order returns make every LDS wait a full drain)
-    auto issue = [&](DownStep& st, uint32_t s) __attribute__((always_inline)) {
-      const uint32_t c = c0 + s / NCH, kb = s % NCH;
+    auto issue = [&](DownStep<DC>& st, uint32_t s) __attribute__((always_inline)) {
+      const uint32_t c = c0 + s / NCH, kb0 = (s % NCH) * DC;
 #pragma unroll
-      for (uint32_t t2 = 0; t2 < 2; ++t2)
-        st.w[t2] = nk::load_tile_operand(nk::tile_base(we, c * 2u + t2, kb, KB), lane);
-      st.ws = wse[((c * 2u + (lane & 1u)) >> 3) * KB + kb];
+      for (uint32_t i = 0; i < DC; ++i)
+#pragma unroll
+        for (uint32_t t2 = 0; t2 < 2; ++t2)
+          st.w[i][t2] = nk::load_tile_operand(nk::tile_base(we, c * 2u + t2, kb0 + i, KB), lane);
+      const uint32_t li = (lane >> 1) < DC ? lane >> 1 : 0u;
+      st.ws = wse[((c * 2u + (lane & 1u)) >> 3) * KB + kb0 + li];
     };
     // the tile's operand and scales, loaded before the first weight step is
     // issued so that waiting for them does not drain the weight stream
@@ -363,28 +371,32 @@ __device__ __forceinline__ void down_stream(
     for (uint32_t q = 0; q < kPieces; ++q) av[q] = asrc[tid + q * kThreads];
     float4 sv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (tid < KB * 4u) sv = reinterpret_cast<const float4*>(hs + tile16 * KB * 16u)[tid];
-    DownStep b0, b1;
+    DownStep<DC> b0, b1;
     issue(b0, 0u);
 #pragma unroll
     for (uint32_t q = 0; q < kPieces; ++q) reinterpret_cast<uint4*>(s_a)[tid + q * kThreads] = av[q];
     if (tid < KB * 4u) reinterpret_cast<float4*>(s_as)[tid] = sv;
     lds_barrier();
 
-    auto compute = [&](const DownStep& st, uint32_t s) __attribute__((always_inline)) {
-      const uint32_t kb = s % NCH;
-      const nk::v8i a = nk::load_tile_operand(s_a + kb * 2048u, lane);
-      const float4 as4 = *reinterpret_cast<const float4*>(&s_as[kb * 16u + (lane >> 4) * 4u]);
-      const float as[4] = {as4.x, as4.y, as4.z, as4.w};
-      const nk::v4f d0 = nk::mfma_e4m3_16x16x128(a, st.w[0]);
-      const nk::v4f d1 = nk::mfma_e4m3_16x16x128(a, st.w[1]);
-      const float s0 = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(st.ws), 0));
-      const float s1 = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(st.ws), 1));
+    auto compute = [&](const DownStep<DC>& st, uint32_t s) __attribute__((always_inline)) {
+      const uint32_t ch = s % NCH;
 #pragma unroll
-      for (uint32_t j = 0; j < 4; ++j) {
-        acc0[j] = acc0[j] + s0 * (as[j] * d0[j]);
-        acc1[j] = acc1[j] + s1 * (as[j] * d1[j]);
+      for (uint32_t i = 0; i < DC; ++i) {
+        const uint32_t kb = ch * DC + i;
+        const nk::v8i a = nk::load_tile_operand(s_a + kb * 2048u, lane);
+        const float4 as4 = *reinterpret_cast<const float4*>(&s_as[kb * 16u + (lane >> 4) * 4u]);
+        const float as[4] = {as4.x, as4.y, as4.z, as4.w};
+        const nk::v4f d0 = nk::mfma_e4m3_16x16x128(a, st.w[i][0]);
+        const nk::v4f d1 = nk::mfma_e4m3_16x16x128(a, st.w[i][1]);
+        const float s0 = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(st.ws), (int)(2u * i)));
+        const float s1 = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(st.ws), (int)(2u * i + 1u)));
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+          acc0[j] = acc0[j] + s0 * (as[j] * d0[j]);
+          acc1[j] = acc1[j] + s1 * (as[j] * d1[j]);
+        }
       }
-      if (kb == NCH - 1u) {
+      if (ch == NCH - 1u) {
         const uint32_t c = c0 + s / NCH;
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
@@ -415,7 +427,7 @@ __device__ __forceinline__ void down_stream(
   }
 }
 
-#define NK_DOWN_STREAM_V(NAME, IV, WPE)                                                         \
+#define NK_DOWN_STREAM_V(NAME, IV, DC, WPE)                                                     \
   NK_KERNEL __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE)))                     \
   void NAME(                                                                                    \
       const uint8_t* __restrict__ hq, const float* __restrict__ hs, const uint8_t* __restrict__ w2, \
@@ -424,11 +436,16 @@ __device__ __forceinline__ void down_stream(
       const int32_t* __restrict__ num_valid, float* __restrict__ partial, uint32_t T,           \
       uint32_t H, uint32_t I, uint32_t Ktot, uint32_t Etot) {                                   \
     (void)I;                                                                                    \
-    down_stream<IV / 128>(hq, hs, w2, w2s, sorted_ids, sorted_expert, tile_map, num_valid,      \
+    down_stream<IV / 128, DC>(hq, hs, w2, w2s, sorted_ids, sorted_expert, tile_map, num_valid,  \
                           partial, T, H, Ktot, Etot);                                           \
   }
-#define NK_DOWN_STREAM(IV) NK_DOWN_STREAM_V(netra_moe_down_stream_i##IV##_gfx950, IV, NK_DOWN_WAVES_PER_EU)
-NK_DOWN_STREAM(256)
-NK_DOWN_STREAM(512)
-NK_DOWN_STREAM(1024)
-NK_DOWN_STREAM(2048)
+// Symbol netra_moe_down_stream_i<I>_c<DC>_gfx950: DC K blocks per step.
+#define NK_DOWN_STREAM(IV, DC) \
+  NK_DOWN_STREAM_V(netra_moe_down_stream_i##IV##_c##DC##_gfx950, IV, DC, NK_DOWN_WAVES_PER_EU)
+NK_DOWN_STREAM(256, 1)
+NK_DOWN_STREAM(512, 1)
+NK_DOWN_STREAM(512, 2)
+NK_DOWN_STREAM(1024, 1)
+NK_DOWN_STREAM(1024, 2)
+NK_DOWN_STREAM(2048, 1)
+NK_DOWN_STREAM(2048, 2)

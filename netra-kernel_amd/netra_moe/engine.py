@@ -50,8 +50,8 @@ class TensorSpec:
 
 
 GEMM_PATHS = ("stream", "tile")
-STREAM_H = (512, 1024, 2048, 4096)   # netra_moe_gate_up_stream_h<H>_gfx950
-STREAM_I = (256, 512, 1024, 2048)    # netra_moe_down_stream_i<I>_gfx950
+STREAM_H = (512, 1024, 2048, 4096)   # netra_moe_gate_up_stream_h<H>_c<CH>_gfx950
+STREAM_I = (256, 512, 1024, 2048)    # netra_moe_down_stream_i<I>_c<DC>_gfx950
 TILE_H = (512, 1024, 2048, 4096)     # netra_moe_gate_up_tile_h<H>_gfx950
 TILE_I = (256, 512, 1024)            # netra_moe_down_tile_i<I>_gfx950
 ROWS_I = (256, 512)                  # netra_moe_down_rows_i<I>_gfx950 (block rows x runs of column groups)
@@ -66,6 +66,18 @@ LDS_GU_H = (512, 1024, 2048)         # netra_moe_gate_up_lds_h<H>_gfx950: 128-ro
 STREAM_GRID_GATE_UP = 256
 STREAM_GU_THREADS = 512
 STREAM_GRID_DOWN = 2048
+# K blocks per prefetch step of the stream kernels (symbol suffix _c<n>): the
+# bytes each wave keeps in flight, which bounds the weight stream.
+STREAM_GU_CHUNK = 2
+STREAM_DN_CHUNK = 1
+
+
+def stream_chunks(cfg: MoEConfig) -> tuple[int, int]:
+    """(gate/up, down) K blocks per step, limited so every item has an even step count."""
+    kb_h, kb_i = cfg.H // 128, cfg.I // 128
+    cu = STREAM_GU_CHUNK if kb_h % (2 * STREAM_GU_CHUNK) == 0 else 2
+    cd = STREAM_DN_CHUNK if kb_i % (2 * STREAM_DN_CHUNK) == 0 else 1
+    return cu, cd
 
 
 def resolve_path(cfg: MoEConfig, path: str = "auto") -> str:
@@ -316,7 +328,7 @@ def operations(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> list[
     common = ["sorted_ids", "sorted_expert", "num_valid"]
     if path == "stream":
         ops += [
-            dict(name="moe.gate_up", symbol=f"netra_moe_gate_up_stream_h{H}_gfx950",
+            dict(name="moe.gate_up", symbol=f"netra_moe_gate_up_stream_h{H}_c{stream_chunks(cfg)[0]}_gfx950",
                  grid=(STREAM_GRID_GATE_UP, 1, 1), block=(STREAM_GU_THREADS, 1, 1), lds=0, dyn=0,
                  args=["x_q", "x_scale", "w13", "w13_scale", "sorted_ids", "sorted_expert",
                        "tile_map", "num_valid", "h_q", "h_scale",
@@ -324,7 +336,7 @@ def operations(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> list[
                  reads=["x_q", "x_scale", "w13", "w13_scale", *common, "tile_map"], writes=["h_q", "h_scale"],
                  refs=["kernels/gfx950/templates/moe/decode/gate_up_mfma.inc:12-161",
                        "kernels/gfx950/templates/moe/decode/silu_quant.inc:16-236"]),
-            dict(name="moe.down", symbol=f"netra_moe_down_stream_i{I}_gfx950",
+            dict(name="moe.down", symbol=f"netra_moe_down_stream_i{I}_c{stream_chunks(cfg)[1]}_gfx950",
                  grid=(STREAM_GRID_DOWN, 1, 1), block=(256, 1, 1), lds=0, dyn=0,
                  args=["h_q", "h_scale", "w2", "w2_scale", "sorted_ids", "sorted_expert", "tile_map",
                        "num_valid", "partial",

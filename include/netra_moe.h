@@ -116,6 +116,18 @@ int netra_moe_pack_tiles(const uint8_t* src, uint8_t* dst, uint32_t groups, uint
 int netra_moe_pack_tiles_gate_up(const uint8_t* src, uint8_t* dst, uint32_t groups, uint32_t n,
                                  uint32_t k, hipStream_t stream);
 
+// The same two layout changes from weights already in the AITER 16x16 shuffle
+// the reference's kernels consume (layout "aiter_shuffle_16x16_fp8_block128",
+// compiler/netra_compiler/layouts.py:90-106; bytes of [groups, n, k] stored as
+// [n/16][k/32][2][16][16], the inverse of
+// tools/benchmark/export_qwen36_dense_m1_capture.py:55-63), so a checkpoint
+// prepared for the reference loads without a round trip through row-major.
+// src is the shuffled tensor; same shape rules and error convention as above.
+int netra_moe_pack_tiles_from_aiter(const uint8_t* src, uint8_t* dst, uint32_t groups, uint32_t n,
+                                    uint32_t k, hipStream_t stream);
+int netra_moe_pack_tiles_gate_up_from_aiter(const uint8_t* src, uint8_t* dst, uint32_t groups,
+                                            uint32_t n, uint32_t k, hipStream_t stream);
+
 // Conversion self-check: writes the contract's integer E4M3 encoding (sw) and
 // the hardware conversion used by the hot kernels (hw) of n fp32 inputs.
 // No counterpart in the reference; tests use it to prove the two agree.

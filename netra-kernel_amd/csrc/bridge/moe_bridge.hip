@@ -60,6 +60,32 @@ extern "C" int netra_moe_pack_tiles_gate_up(const uint8_t* src, uint8_t* dst, ui
   return 0;
 }
 
+static int pack_from_aiter(const char* name, const uint8_t* src, uint8_t* dst, uint32_t groups,
+                           uint32_t n, uint32_t k, uint32_t gate_up, hipStream_t stream) {
+  if (!src || !dst || src == dst || groups == 0 || n == 0 || k == 0 || n % (gate_up ? 32u : 16u) ||
+      k % 128u)
+    return fail(-1, std::string(name) + ": null/aliased pointers or n % " + (gate_up ? "32" : "16") +
+                        ", k % 128 != 0");
+  const uint64_t tiles = static_cast<uint64_t>(groups) * (n / 16u) * (k / 128u);
+  if (tiles > 0xfffffffcull) return fail(-1, std::string(name) + ": too many tiles");
+  hipLaunchKernelGGL(netra_moe_pack_tiles_aiter_gfx950, dim3(static_cast<uint32_t>((tiles + 3u) / 4u)),
+                     dim3(256), 0, stream, src, dst, groups, n, k, gate_up);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(static_cast<int>(err), hipGetErrorString(err));
+  g_last_error.clear();
+  return 0;
+}
+
+extern "C" int netra_moe_pack_tiles_from_aiter(const uint8_t* src, uint8_t* dst, uint32_t groups,
+                                               uint32_t n, uint32_t k, hipStream_t stream) {
+  return pack_from_aiter("netra_moe_pack_tiles_from_aiter", src, dst, groups, n, k, 0u, stream);
+}
+
+extern "C" int netra_moe_pack_tiles_gate_up_from_aiter(const uint8_t* src, uint8_t* dst, uint32_t groups,
+                                                       uint32_t n, uint32_t k, hipStream_t stream) {
+  return pack_from_aiter("netra_moe_pack_tiles_gate_up_from_aiter", src, dst, groups, n, k, 1u, stream);
+}
+
 extern "C" int netra_moe_e4m3_check(const float* in, uint8_t* sw, uint8_t* hw, uint32_t n,
                                     hipStream_t stream) {
   if (!in || !sw || !hw || n == 0) return fail(-1, "netra_moe_e4m3_check: null pointer or n == 0");

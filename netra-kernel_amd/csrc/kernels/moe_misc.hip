@@ -176,6 +176,39 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_pack_tiles_gfx950(
 }
 
 // ---------------------------------------------------------------------------
+// Weight layout change from the AITER 16x16 shuffle the reference's kernels
+// consume (checkpoint layout "aiter_shuffle_16x16_fp8_block128",
+// compiler/netra_compiler/layouts.py:90-106; its inverse is
+// tools/benchmark/export_qwen36_dense_m1_capture.py:55-63): bytes of a
+// [groups, n, k] e4m3 matrix stored as [n/16][k/32][2][16][16], i.e. row tile,
+// 32-column group, 16-column half, row, byte. A 16 x 128 block of either
+// layout is 2 KiB at the same place (row tiles outermost, k contiguous per row
+// tile) made of eight 256-byte chunks (16 rows x 16 bytes); AITER orders the
+// chunks (group, half), tile16x128 orders them (half, group). One wave per
+// block moves 128 16-byte pieces; with gate_up != 0 the row tiles are stored
+// gate/up-interleaved as by netra_moe_pack_tiles_gfx950.
+NK_KERNEL __launch_bounds__(256) void netra_moe_pack_tiles_aiter_gfx950(
+    const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t groups, uint32_t n,
+    uint32_t k, uint32_t gate_up) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t tile = blockIdx.x * 4u + (threadIdx.x >> 6);
+  const uint32_t nt = n / 16u, kb = k / 128u;
+  if (tile >= groups * nt * kb) return;
+  const uint32_t g = tile / (nt * kb), rt = (tile / kb) % nt, cb = tile % kb;
+  const uint32_t prt = gate_up ? nk::gu_tile(rt, n) : rt;
+  const uint8_t* s = src + (((size_t)g * nt + rt) * kb + cb) * 2048u;
+  uint8_t* d = dst + (((size_t)g * nt + prt) * kb + cb) * 2048u;
+#pragma unroll
+  for (uint32_t q = 0; q < 2u; ++q) {
+    const uint32_t piece = q * 64u + lane;        // destination order: chunk (half, group), row
+    const uint32_t chunk = piece >> 4, row = piece & 15u;
+    const uint32_t half = chunk >> 2, grp = chunk & 3u;
+    const uint4 v = *reinterpret_cast<const uint4*>(s + (grp * 2u + half) * 256u + row * 16u);
+    *reinterpret_cast<uint4*>(d + chunk * 256u + row * 16u) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Plain 16-byte-per-lane copy of known size. Counter calibration: its
 // FETCH_SIZE / WRITE_SIZE readings over a copy of B bytes convert the same
 // counters' readings on the MoE kernels into HBM bytes, and its duration gives

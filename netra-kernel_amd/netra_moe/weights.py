@@ -35,6 +35,9 @@ def bridge_library() -> ctypes.CDLL:
         lib.netra_moe_pack_tiles.restype = ctypes.c_int
         lib.netra_moe_pack_tiles_gate_up.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_uint32] * 3 + [ctypes.c_void_p]
         lib.netra_moe_pack_tiles_gate_up.restype = ctypes.c_int
+        for fn in (lib.netra_moe_pack_tiles_from_aiter, lib.netra_moe_pack_tiles_gate_up_from_aiter):
+            fn.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_uint32] * 3 + [ctypes.c_void_p]
+            fn.restype = ctypes.c_int
         lib.netra_moe_e4m3_check.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_uint32, ctypes.c_void_p]
         lib.netra_moe_e4m3_check.restype = ctypes.c_int
         lib.netra_moe_copy.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_uint64, ctypes.c_void_p]
@@ -77,6 +80,35 @@ def pack_tiles(q: torch.Tensor, gate_up: bool = False) -> torch.Tensor:
     if rc != 0:
         raise RuntimeError(f"weight packing failed ({rc}): {lib.netra_moe_last_error().decode()}")
     return out
+
+
+def pack_tiles_from_aiter(q: torch.Tensor, gate_up: bool = False) -> torch.Tensor:
+    """AITER 16x16-shuffled e4m3 bytes [G, N, K] on the GPU (the layout the
+    reference's kernels consume) -> the kernels' tile16x128 layout, as
+    pack_tiles() would produce from the row-major bytes."""
+    if q.dim() != 3 or q.dtype != torch.uint8 or not q.is_cuda or not q.is_contiguous():
+        raise ValueError("pack_tiles_from_aiter needs a contiguous uint8 [G, N, K] GPU tensor")
+    g, n, k = q.shape
+    if n % (32 if gate_up else 16) or k % 128:
+        raise ValueError("N must be a multiple of 16 (32 for W13) and K of 128")
+    out = torch.empty_like(q)
+    lib = bridge_library()
+    fn = lib.netra_moe_pack_tiles_gate_up_from_aiter if gate_up else lib.netra_moe_pack_tiles_from_aiter
+    rc = fn(q.data_ptr(), out.data_ptr(), g, n, k, torch.cuda.current_stream(q.device).cuda_stream)
+    if rc != 0:
+        raise RuntimeError(f"weight packing failed ({rc}): {lib.netra_moe_last_error().decode()}")
+    return out
+
+
+def aiter_shuffle_host(q: np.ndarray) -> np.ndarray:
+    """AITER 16x16 shuffle of row-major bytes [..., N, K]: element (n, k) goes to
+    [n/16][k/32][(k%32)/16][n%16][k%16] (the inverse of
+    tools/benchmark/export_qwen36_dense_m1_capture.py:55-63)."""
+    *lead, n, k = q.shape
+    t = q.reshape(*lead, n // 16, 16, k // 32, 2, 16)
+    nd = len(lead)
+    t = t.transpose(*range(nd), nd, nd + 2, nd + 3, nd + 1, nd + 4)
+    return np.ascontiguousarray(t).reshape(*lead, n, k)
 
 
 def device_copy(src: torch.Tensor, dst: torch.Tensor) -> None:

@@ -72,3 +72,15 @@ def test_pack_tiles_kernel_matches_host_layout():
     torch.cuda.synchronize()
     np.testing.assert_array_equal(out.cpu().numpy(), W.pack_tiles_host(q))
     np.testing.assert_array_equal(out_gu.cpu().numpy(), W.pack_tiles_host(q, gate_up=True))
+
+
+@pytest.mark.parametrize("n,k,gate_up", [(64, 256, False), (1024, 512, True), (2048, 512, False), (96, 384, True)])
+def test_pack_from_aiter_equals_pack_from_row_major(n, k, gate_up):
+    """Weights in the reference's AITER 16x16 shuffle convert to exactly the
+    bytes the row-major packer writes."""
+    rng = np.random.default_rng(n + k)
+    q = rng.integers(0, 256, size=(3, n, k), dtype=np.uint8)
+    src = torch.from_numpy(W.aiter_shuffle_host(q)).to(DEV)
+    got = W.pack_tiles_from_aiter(src, gate_up=gate_up)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy(), W.pack_tiles_host(q, gate_up=gate_up))

@@ -1,11 +1,14 @@
 """Host restatements of the kernels' data layouts (CPU).
 
-The packed weight layout and the tiled h layout are pure permutations; these
-tests pin the host restatements against element-by-element definitions
-(independent index arithmetic) so the GPU tests that rely on them compare like
-with like.
+The packed weight layout and the AITER 16x16 shuffle the reference's kernels
+consume are pure permutations; these tests pin the host restatements against
+element-by-element definitions (independent index arithmetic, and the
+reference's own inverse of the shuffle) so the GPU tests that rely on them
+compare like with like.
 """
 import numpy as np
+import pytest
+import torch
 
 from netra_moe import weights as W
 
@@ -45,3 +48,28 @@ def test_pack_tiles_gate_up_interleaves_the_row_tiles():
                 assert p[off] == q[g, n, k]
     np.testing.assert_array_equal(W.unpack_tiles_host(p.reshape(G, N, K), gate_up=True), q)
     np.testing.assert_array_equal(W.unpack_tiles_host(W.pack_tiles_host(q)), q)
+
+
+def _reference_unshuffle(shuffled: np.ndarray) -> np.ndarray:
+    """The reference's inverse of the AITER 16x16 shuffle, as its capture tool
+    states it (tools/benchmark/export_qwen36_dense_m1_capture.py:55-63):
+    view(n/16, k/32, 2, 16, 16).permute(0, 3, 1, 2, 4), per matrix."""
+    n, k = shuffled.shape
+    return torch.from_numpy(shuffled).view(n // 16, k // 32, 2, 16, 16).permute(0, 3, 1, 2, 4) \
+        .contiguous().view(n, k).numpy()
+
+
+@pytest.mark.parametrize("n,k", [(16, 128), (64, 256), (96, 384)])
+def test_aiter_shuffle_is_inverted_by_the_reference_unshuffle(n, k):
+    rng = np.random.default_rng(n * 1000 + k)
+    q = rng.integers(0, 256, size=(2, n, k), dtype=np.uint8)
+    s = W.aiter_shuffle_host(q)
+    for g in range(2):
+        np.testing.assert_array_equal(_reference_unshuffle(s[g]), q[g])
+    # the reference decode kernel's addressing: row tile * 32 KiB (k = 2048)
+    # generalises to row tile * 16 k; lane (n % 16) * 16; 16-column fragment
+    # ((k % 128) // 16) * 256 within a 128-column block (gate_up_mfma.inc:47-55)
+    flat = s.reshape(2, -1)
+    for (nn, kk) in [(0, 0), (n - 1, k - 1), (n // 2 + 3, 37), (5, k // 2 + 17)]:
+        off = (nn // 16) * 16 * k + (kk // 32) * 512 + ((kk % 32) // 16) * 256 + (nn % 16) * 16 + kk % 16
+        assert flat[1, off] == q[1, nn, kk]

@@ -14,10 +14,11 @@
 // down_reduce_mfma_2wave.inc:14-291) and the route reducer
 // (moe/prefill/route_reduce_splitk2_f16.inc:6-117):
 //
-//   netra_moe_router_h<H>_gfx950, H in {512,1024,2048,4096} (x bf16[T,H],
+//   netra_moe_router_h<H>_t<NT>_gfx950, H in {512,1024,2048,4096} (x bf16[T,H],
 //       w bf16[E+S,H], logits bf16[T,E+S], xq e4m3[T,H], xs f32[T,H/128],
 //       mask u64[(E+S)*W]; T, H, rows=E+S, (E+S)*W)
-//       grid (ceil(rows/16), ceil(T/NT)), block 256, NT = 4 (2 for H = 4096),
+//       grid (ceil(rows/16), ceil(T/NT)), block 256, NT = max(1, 2048/H) for T <= 128 else 4
+//       (NT = 2 for H = 4096),
 //       static LDS 4 * NT * H bytes
 //   netra_moe_topk_gfx950(logits, bias f32[E], ids i32[T,Ktot], weights f32[T,Ktot],
 //       mask; T, E, K, S, W)   grid ceil(T/4), block 256 (one wave per token)

@@ -137,7 +137,7 @@ __device__ __forceinline__ void router(const uint16_t* __restrict__ x, const uin
 
 #define NK_ROUTER(HV, NT)                                                                      \
   NK_KERNEL __launch_bounds__(256)                                                         \
-  void netra_moe_router_h##HV##_gfx950(                                                        \
+  void netra_moe_router_h##HV##_t##NT##_gfx950(                                                \
       const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,                          \
       uint16_t* __restrict__ logits, uint8_t* __restrict__ xq, float* __restrict__ xs,         \
       unsigned long long* __restrict__ mask, uint32_t T, uint32_t H, uint32_t rows,            \
@@ -145,8 +145,14 @@ __device__ __forceinline__ void router(const uint16_t* __restrict__ x, const uin
     (void)H;                                                                                   \
     router<HV / 128, NT>(x, w, logits, xq, xs, mask, T, rows, mask_words);                     \
   }
+// Symbol netra_moe_router_h<H>_t<NT>_gfx950: NT tokens per workgroup (for
+// small T the fewest the staging allows, NT * H a multiple of 2048: each
+// wave's fmaf chains run fewer tokens and more workgroups share the weight
+// rows; 7.9 -> 6.0 us at T = 64, H = 2048).
 NK_ROUTER(512, 4)
+NK_ROUTER(1024, 2)
 NK_ROUTER(1024, 4)
+NK_ROUTER(2048, 1)
 NK_ROUTER(2048, 4)
 NK_ROUTER(4096, 2)
 

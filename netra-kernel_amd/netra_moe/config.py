@@ -24,7 +24,7 @@ class MoEConfig:
     K: int            # routed top-k
     I: int            # expert intermediate size
     S: int = 0        # shared experts (0 or 1)
-    router_bias: str = "none"   # "none" | "zipf1.1": log-Zipf(1.1) expert bias
+    router_bias: str = "none"   # "none" | "zipf1.1": log-Zipf(1.1) expert bias | "hot": +64 on experts 0..K-1
     seed: int = 0
     notes: str = field(default="", compare=False)
 
@@ -41,7 +41,7 @@ class MoEConfig:
             raise ValueError("S must be 0 or 1")
         if self.E > 512:
             raise ValueError("E must be <= 512")
-        if self.router_bias not in ("none", "zipf1.1"):
+        if self.router_bias not in ("none", "zipf1.1", "hot"):
             raise ValueError("unknown router_bias")
 
     # ---- derived sizes ------------------------------------------------------

@@ -207,12 +207,21 @@ def op_names(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> tuple[s
     path = resolve_path(cfg, path)
     front_ops = EXACT_FRONT_OPS if resolve_front(cfg, path, front) == "exact" else SCREEN_FRONT_OPS
     return front_ops + PATH_OPS[path]
-ROUTER_H = (512, 1024, 2048, 4096)   # netra_moe_router_h<H>_gfx950
+ROUTER_H = (512, 1024, 2048, 4096)   # netra_moe_router_h<H>_t<NT>_gfx950
 
 
-def router_tokens(H: int) -> int:
-    """Tokens per router workgroup (template NT of netra_moe_router_h<H>)."""
-    return 2 if H >= 4096 else 4
+ROUTER_SMALL_T = 128                 # up to this T the router runs one token per workgroup
+
+
+def router_tokens(H: int, T: int) -> int:
+    """Tokens per router workgroup (template NT of netra_moe_router_h<H>_t<NT>):
+    for small T the fewest the staging allows (NT * H a multiple of 2048:
+    shorter fmaf chains per wave, more workgroups; measured 7.9 -> 6.0 us at
+    T = 64, H = 2048), else four, so large T does not re-read the router rows
+    from L2 for every token; two at H = 4096."""
+    if H >= 4096:
+        return 2
+    return max(1, 2048 // H) if T <= ROUTER_SMALL_T else 4
 
 
 def _screen_front(cfg: MoEConfig) -> list[dict]:
@@ -299,9 +308,9 @@ def operations(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> list[
         raise ValueError(f"router kernels exist for H in {ROUTER_H}")
     u = lambda v: ("u32", int(v))  # noqa: E731
     ops = [
-        dict(name="moe.router", symbol=f"netra_moe_router_h{H}_gfx950",
-             grid=((cfg.router_rows + 15) // 16, (T + router_tokens(H) - 1) // router_tokens(H), 1),
-             block=(256, 1, 1), lds=4 * router_tokens(H) * H, dyn=0,
+        dict(name="moe.router", symbol=f"netra_moe_router_h{H}_t{router_tokens(H, T)}_gfx950",
+             grid=((cfg.router_rows + 15) // 16, (T + router_tokens(H, T) - 1) // router_tokens(H, T), 1),
+             block=(256, 1, 1), lds=4 * router_tokens(H, T) * H, dyn=0,
              args=["x", "router_w", "logits", "x_q", "x_scale", "mask",
                    u(T), u(H), u(cfg.router_rows), u(cfg.Etot * W)],
              reads=["x", "router_w"], writes=["logits", "x_q", "x_scale", "mask"],

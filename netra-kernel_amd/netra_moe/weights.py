@@ -172,6 +172,9 @@ def synthetic_activations(cfg: MoEConfig, device: torch.device | str = "cpu") ->
     router_w = (torch.randn((cfg.router_rows, cfg.H), generator=g, dtype=torch.float32) * 0.02).to(torch.bfloat16)
     if cfg.router_bias == "zipf1.1":
         bias = torch.from_numpy(zipf_bias(cfg.E, cfg.seed))
+    elif cfg.router_bias == "hot":  # every token picks experts 0..K-1: K experts hold all rows
+        bias = torch.zeros(cfg.E, dtype=torch.float32)
+        bias[:cfg.K] = 64.0
     else:
         bias = torch.zeros(cfg.E, dtype=torch.float32)
     return {"x": x.to(device), "router_w": router_w.to(device), "router_bias": bias.to(device)}

@@ -28,10 +28,14 @@ DEV = torch.device("cuda", 0)
 
 # Shapes beyond the benchmark configs, so every kernel instantiation family is
 # exercised: H = 4096 (exact front end, register-operand tile gate/up) and
-# H = 1024 with I = 1024 (the other GEMM widths).
+# H = 1024 with I = 1024 (the other GEMM widths); and the extreme of routing
+# skew: every token on the same K experts (T = 300 rows each, 60 experts
+# empty), T not a multiple of any tile.
 EXTRA_CONFIGS = {
     "shape_h4096": MoEConfig("shape_h4096", T=48, H=4096, E=32, K=4, I=256, S=1, seed=1101),
     "shape_h1024_i1024": MoEConfig("shape_h1024_i1024", T=40, H=1024, E=24, K=3, I=1024, S=1, seed=1102),
+    "shape_hot_experts": MoEConfig("shape_hot_experts", T=300, H=1024, E=64, K=4, I=256, S=1,
+                                   router_bias="hot", seed=1103),
 }
 CONFIGS = {**BASELINE_CONFIGS, **EXTRA_CONFIGS}
 CASES = [(name, path) for name in CONFIGS for path in ("stream", "tile")]
@@ -103,8 +107,11 @@ def test_gate_up_silu_quant_rows(case):
     fp32 accumulation order differs, so a group max may move by one bf16 step
     (scale ratio within 2^-7) and an element by one E4M3 step (dequantised
     difference within 1/8 relative + 1.5% for the scale); elements near zero,
-    where g or u cancel, may move by up to two subnormal steps (2^-9 * scale
-    each); fewer than 1% of codes may differ."""
+    where g or u cancel, may move by up to four subnormal steps (2^-9 * scale
+    each): an exact h of ~1e-5 against a row maximum near 1 can land two steps
+    either side of zero in fp32 against the fp64 oracle (the hot-expert shape
+    shows it, both GEMM paths agreeing with each other); fewer than 1% of codes
+    may differ."""
     cfg, host, got, ref = case
     nv = int(ref["num_valid"][0])
     rows = min(nv, 1024)
@@ -125,7 +132,7 @@ def test_gate_up_silu_quant_rows(case):
     d_got = table[q_got] * np.repeat(s_got, 128, axis=1)
     scale_rel = float(np.max(np.abs(s_got - s_ref) / s_ref))
     smax = np.repeat(np.maximum(s_ref, s_got), 128, axis=1)
-    bound = 0.14 * np.maximum(np.abs(d_ref), np.abs(d_got)) + smax * 2.0 ** -8 * 1.01
+    bound = 0.14 * np.maximum(np.abs(d_ref), np.abs(d_got)) + smax * 2.0 ** -7 * 1.01
     excess = float(np.max(np.abs(d_got - d_ref) - bound))
     frac = float(np.mean(q_ref != q_got))
     print(f"[parity] {cfg.name} h rows={int(valid.sum())} scale_rel={scale_rel:.2e} "

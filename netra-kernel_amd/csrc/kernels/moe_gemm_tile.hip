@@ -519,11 +519,10 @@ __device__ __forceinline__ void down_rows(
 }  // namespace nktile
 
 // Gate/up tile kernels: 4 waves x 32 columns, one weight block in flight
-// ahead (the variant measured fastest at prefill shapes;
-// the _w / _a instantiations for H = 2048 are the alternatives kept for
-// tuning runs).
-#define NK_GATE_UP_TILE_V(NAME, HV, WAVES, AHEAD, ATTR)                                            \
-  NK_KERNEL __launch_bounds__(64 * WAVES) ATTR void NAME(                                          \
+// ahead. The engine uses them for H = 4096, where the block-pair LDS ring
+// does not fit; the other widths are instantiated for tests and comparison.
+#define NK_GATE_UP_TILE_V(NAME, HV, WAVES, AHEAD)                                                 \
+  NK_KERNEL __launch_bounds__(64 * WAVES) void NAME(                                               \
       const uint8_t* __restrict__ xq, const float* __restrict__ xs, const uint8_t* __restrict__ w13, \
       const float* __restrict__ w13s, const int32_t* __restrict__ sorted_ids,                      \
       const int32_t* __restrict__ sorted_expert, const int32_t* __restrict__ num_valid,            \
@@ -533,18 +532,10 @@ __device__ __forceinline__ void down_rows(
     nktile::gate_up_tile<HV / 128, WAVES, AHEAD>(xq, xs, w13, w13s, sorted_ids, sorted_expert,     \
                                                  num_valid, hq, hs, T, I, Ktot, Etot);             \
   }
-#define NK_NOATTR
-#define NK_OCC4 __attribute__((amdgpu_waves_per_eu(4)))
-NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h512_gfx950, 512, 4, 1, NK_NOATTR)
-NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h1024_gfx950, 1024, 4, 1, NK_NOATTR)
-NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h2048_gfx950, 2048, 4, 1, NK_NOATTR)
-NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h4096_gfx950, 4096, 4, 1, NK_NOATTR)
-NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h2048_w4_a2_gfx950, 2048, 4, 2, NK_NOATTR)
-NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h2048_w8_a1_gfx950, 2048, 8, 1, NK_NOATTR)
-NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h2048_w4_a3_gfx950, 2048, 4, 3, NK_NOATTR)
-NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h2048_w8_a4_gfx950, 2048, 8, 4, NK_NOATTR)
-NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h2048_w8_a2_gfx950, 2048, 8, 2, __attribute__((amdgpu_waves_per_eu(4))))
-NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h2048_w8_a1_o4_gfx950, 2048, 8, 1, NK_OCC4)
+NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h512_gfx950, 512, 4, 1)
+NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h1024_gfx950, 1024, 4, 1)
+NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h2048_gfx950, 2048, 4, 1)
+NK_GATE_UP_TILE_V(netra_moe_gate_up_tile_h4096_gfx950, 4096, 4, 1)
 
 #define NK_DOWN_TILE(IV)                                                                           \
   NK_KERNEL __launch_bounds__(256)                                                                \

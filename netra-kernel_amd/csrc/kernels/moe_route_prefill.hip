@@ -206,7 +206,7 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
 //  0. the token row is staged in LDS, quantised (1x128) and its norm taken;
 //  1. bounds zlo/zhi of z = f32(bf16(L)) + bias from L in [a - m, a + m],
 //     m = 2^-10 ||x|| ||w_e|| (norms rounded up; bf16
-//     rounding and the bias add are monotone); theta = K-th largest zlo;
+//     rounding and the bias add are monotone); theta <= K-th largest zlo;
 //     candidates = {e : zhi_e >= theta} contain the true top-K, since every
 //     other expert lies strictly below K experts;
 //  2. exact logits of the candidates and of the shared-gate row, one per
@@ -240,6 +240,31 @@ __device__ __forceinline__ void route_select(
   constexpr uint32_t kThreads = 64u * W;
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
+  // This wave's token (one per wave): its row, screen sums and biases are
+  // requested before the workgroup's norm set-up below, so the three
+  // dependent round trips of the original order overlap.
+  const uint32_t t_w = blockIdx.x * W + wave;
+  const bool active = t_w < T;
+  uint4 xv[H / 512u];
+  float aval[P], bv[P];
+  if (active) {
+#pragma unroll
+    for (uint32_t p = 0; p < H / 512u; ++p)
+      xv[p] = *reinterpret_cast<const uint4*>(x + (size_t)t_w * H + 512u * p + 8u * lane);
+    const float* srow = screen + (size_t)t_w * RP;  // split z at srow + z * T * RP
+#pragma unroll
+    for (uint32_t j = 0; j < P; ++j) {
+      const uint32_t e = lane + 64u * j;
+      aval[j] = 0.0f;
+      bv[j] = 0.0f;
+      if (e < E) {
+        float a = srow[e];
+        for (uint32_t z = 1; z < Z; ++z) a += srow[(size_t)z * T * RP + e];
+        aval[j] = a;
+        bv[j] = bias[e];
+      }
+    }
+  }
   for (uint32_t e = tid; e <= EMAX; e += kThreads) {
     s_hist[e] = 0u;
     if (e < E) {
@@ -260,7 +285,7 @@ __device__ __forceinline__ void route_select(
 #pragma unroll
     for (uint32_t p = 0; p < H / 512u; ++p) {
       const uint32_t i0 = 512u * p + 8u * lane;
-      const uint4 v = *reinterpret_cast<const uint4*>(x + (size_t)t * H + i0);
+      const uint4 v = xv[p];
       s_x[tt][i0 / 4u] = make_float4(nk::bf16_lo(v.x), nk::bf16_hi(v.x), nk::bf16_lo(v.y), nk::bf16_hi(v.y));
       s_x[tt][i0 / 4u + 1u] = make_float4(nk::bf16_lo(v.z), nk::bf16_hi(v.z), nk::bf16_lo(v.w), nk::bf16_hi(v.w));
       quant8(v, xq + (size_t)t * H + i0, xs + (size_t)t * NJ + (i0 >> 7), s == 0);
@@ -271,29 +296,26 @@ __device__ __forceinline__ void route_select(
     const float mx = kScreenMargin * sqrtf(xx) * kNormSlack;
 
     // 1. certified candidates
-    const float* srow = screen + (size_t)t * RP;  // split z at srow + z * T * RP
     uint32_t clo[P], chi[P];
-    float aval[P];
 #pragma unroll
     for (uint32_t j = 0; j < P; ++j) {
       const uint32_t e = lane + 64u * j;
       clo[j] = chi[j] = 0u;
-      aval[j] = 0.0f;
       if (e < E) {
-        float a = srow[e];
-        for (uint32_t z = 1; z < Z; ++z) a += srow[(size_t)z * T * RP + e];
-        const float m = mx * s_wn[e];
-        const float b = bias[e];
-        aval[j] = a;
+        const float a = aval[j], m = mx * s_wn[e], b = bv[j];
         clo[j] = nk::order_bits(nk::bf16_f32(nk::bf16_rne(a - m)) + b);
         chi[j] = nk::order_bits(nk::bf16_f32(nk::bf16_rne(a + m)) + b);
       }
     }
-    // theta = K-th largest zlo: the largest code with at least K codes >= it,
-    // found bit by bit from the top (absent experts have code 0)
+    // theta <= the K-th largest zlo: the largest code with its low 16 bits
+    // clear that has at least K codes >= it, found bit by bit from the top
+    // (absent experts have code 0). Any theta at or below the K-th largest
+    // zlo certifies (every expert outside {zhi >= theta} lies below K
+    // experts); stopping at 16 bits lowers it by less than one bf16 step of
+    // z and halves the search.
     uint32_t theta = 0u;
 #pragma unroll 1
-    for (int bit = 31; bit >= 0; --bit) {
+    for (int bit = 31; bit >= 16; --bit) {
       const uint32_t cand = theta | (1u << bit);
       uint32_t cnt = 0u;
 #pragma unroll

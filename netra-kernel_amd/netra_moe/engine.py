@@ -60,16 +60,17 @@ TILE_GU_WAVES = 4                    # waves of netra_moe_gate_up_tile_h<H>_gfx9
 LDS_GU_H = (512, 1024, 2048)         # netra_moe_gate_up_lds_h<H>_gfx950: 128-row pairs, LDS operand ring
 # Stream kernel grids (measured at T=64 on one MI355X): gate/up fills the chip
 # once, 256 CUs x 4 SIMDs x 2 resident waves (NK_GATE_UP_WAVES_PER_EU) / 8
-# waves per workgroup; down runs 2048 four-wave workgroups, about twice what
-# is resident at once, so each wave streams fewer steps (47 us against 49 us
-# for 1024 workgroups and 49 us for 512).
+# waves per workgroup; down runs 4096 four-wave workgroups, about four times
+# what is resident at once, with 2 K blocks per step, so each wave streams few
+# steps (46.2 us against 47.3 us for 2048 workgroups of 1-block steps, 49 us
+# for 1024).
 STREAM_GRID_GATE_UP = 256
 STREAM_GU_THREADS = 512
-STREAM_GRID_DOWN = 2048
+STREAM_GRID_DOWN = 4096
 # K blocks per prefetch step of the stream kernels (symbol suffix _c<n>): the
 # bytes each wave keeps in flight, which bounds the weight stream.
 STREAM_GU_CHUNK = 2
-STREAM_DN_CHUNK = 1
+STREAM_DN_CHUNK = 2
 
 
 def stream_chunks(cfg: MoEConfig) -> tuple[int, int]:

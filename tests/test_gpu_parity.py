@@ -36,6 +36,9 @@ EXTRA_CONFIGS = {
     "shape_h1024_i1024": MoEConfig("shape_h1024_i1024", T=40, H=1024, E=24, K=3, I=1024, S=1, seed=1102),
     "shape_hot_experts": MoEConfig("shape_hot_experts", T=300, H=1024, E=64, K=4, I=256, S=1,
                                    router_bias="hot", seed=1103),
+    # more than 256 experts: the 512-expert route_select / top-k / sort variants
+    "shape_e384": MoEConfig("shape_e384", T=96, H=1024, E=384, K=6, I=256, S=1,
+                            router_bias="zipf1.1", seed=1104),
 }
 CONFIGS = {**BASELINE_CONFIGS, **EXTRA_CONFIGS}
 CASES = [(name, path) for name in CONFIGS for path in ("stream", "tile")]

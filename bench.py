@@ -125,7 +125,10 @@ def cpu_baseline(cfg, act_cpu, w_host, threads: int, min_seconds: float):
         if len(runs) >= 1000:
             break
     med = sorted(runs)[len(runs) // 2]
-    return {"value": n / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+    host = os.cpu_count() or 1
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else host
+    return {"value": n / med, "unit": "tokens/s", "cores": threads, "host_cores": host,
+            "host_cores_usable": usable, "kind": "port",
             "sample": f"{n} tokens of {cfg.name} (router+top-k+quant+all {cfg.Ktot} expert slots per token, "
                       f"fp64-accumulated C oracle, OpenMP), median of {len(runs)} runs, {med * 1e3:.1f} ms each"}
 
@@ -309,7 +312,7 @@ def main() -> int:
                 dl.append(lay)
             kern = {}
             for op in dl[0].op_names:
-                kern[op] = time_operation(dl, op, max(20, steps // 2), torch) * 1e3  # us
+                kern[op] = time_operation(dl, op, max(50, steps // 2), torch) * 1e3  # us
             for lay in dl:
                 lay.close()
         for lay in layers:
@@ -335,14 +338,17 @@ def main() -> int:
     for name in [s for s in args.secondary.split(",") if s]:
         c = BASELINE_CONFIGS[name]
         log(f"[bench] secondary {name}")
-        steps = max(10, args.steps // (4 if c.T >= 4096 else 1))
-        res, _, _ = run_config(c, steps, max(3, args.warmup // 2), False)
+        # at least 50 timed steps and 10 warm-up steps, whatever --steps says
+        res, kern_c, _ = run_config(c, max(50, args.steps), max(10, args.warmup), True)
+        res["kernels_us"] = kern_c
         secondary[name] = res
 
     cpu = None
     if not args.no_cpu_baseline:
-        threads = min(16, os.cpu_count() or 1)
-        log(f"[bench] cpu baseline on {threads} threads")
+        # the GPU box grants one GPU's share of its host: 16 threads at most,
+        # whatever nproc shows (the line reports both)
+        threads = min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count() or 1)
+        log(f"[bench] cpu baseline on {threads} threads (host nproc {os.cpu_count()})")
         w_host = {"w13": wsets[0]["w13_row_major"].cpu().numpy(),
                   "w13_scale": wsets[0]["w13_scale"].cpu().numpy(),
                   "w2": wsets[0]["w2_row_major"].cpu().numpy(),

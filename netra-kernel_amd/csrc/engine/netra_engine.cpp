@@ -1,10 +1,19 @@
 // Netra engine C-ABI runtime for gfx950: engine directory -> loaded code
 // objects, bound pointers, fixed launches on the caller's stream.
 //
-// Behaviour mirrors the reference runtime (runtime/gfx950/engine/
-// netra_engine.hip): create 249-395, query 400-405, bind 406-420, finalize
-// 421-434, prepare (graph capture) 435-449, launch 450-466, launch_operation
-// 467-497, launch_operation_bound 498-558, last_error 559, destroy 562-566.
+// The entry points are those of the reference runtime
+// (runtime/gfx950/engine/netra_engine.h:60-108). Which status a given misuse
+// returns, and which check wins when several apply, is interface a caller of
+// the reference depends on; those precedences are kept and listed, entry by
+// entry, above each function below. The bodies, the engine's state model and
+// the error texts are this runtime's own (one text, "bindings are finalized
+// and immutable", is kept word for word because a reference test looks for
+// it: tests/compiler/test_runtime_hotpath.py:68).
+//
+// State: bindings are open until netra_engine_finalize_bindings (engine-wide,
+// one way); a profile captured by netra_engine_prepare_profile is immutable
+// and launches only as its graph. `in_flight` counts launch calls between
+// admission and return, so bind / finalize / destroy can refuse during one.
 // The launch paths allocate nothing, parse nothing, never synchronise and
 // touch no files or environment.
 #include "../../../include/netra_engine.h"
@@ -13,6 +22,7 @@
 
 #include <array>
 #include <atomic>
+#include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -31,6 +41,7 @@ struct OpRecord {
   std::array<uint32_t, 3> block{1, 1, 1};
   uint32_t dynamic_lds_bytes = 0;
   uint32_t argument_count = 0;
+  uint32_t slot_count = 0;  // pointer arguments the caller binds
   // Argument storage: kernelParams entries point into these arrays, so a
   // record is never moved after create (profiles reserve their vectors).
   std::array<void*, netra::kMaxArguments> pointers{};
@@ -45,7 +56,7 @@ struct ProfileRecord {
   std::vector<OpRecord> ops;
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
-  bool graph_ready = false;
+  bool captured = false;
 };
 
 }  // namespace
@@ -64,43 +75,88 @@ struct netra_engine {
 
 namespace {
 
-netra_status_t fail(netra_engine* e, netra_status_t status, const char* message) {
-  if (e) std::snprintf(e->last_error, sizeof(e->last_error), "%s", message);
+// Records a refusal (formatted into the engine's last_error) and returns its status.
+__attribute__((format(printf, 3, 4))) netra_status_t refuse(netra_engine* e, netra_status_t status,
+                                                           const char* format, ...) {
+  if (e) {
+    va_list args;
+    va_start(args, format);
+    std::vsnprintf(e->last_error, sizeof(e->last_error), format, args);
+    va_end(args);
+  }
   return status;
 }
 
-netra_status_t hip_fail(netra_engine* e, const char* what, hipError_t err) {
-  if (e) std::snprintf(e->last_error, sizeof(e->last_error), "%s: %s", what, hipGetErrorString(err));
-  return NETRA_STATUS_HIP;
+netra_status_t hip_refusal(netra_engine* e, const char* call, hipError_t err) {
+  return refuse(e, NETRA_STATUS_HIP, "%s failed: %s", call, hipGetErrorString(err));
 }
 
-void clear_error(netra_engine* e) { e->last_error[0] = '\0'; }
+netra_status_t accept(netra_engine* e) {
+  e->last_error[0] = '\0';
+  return NETRA_STATUS_OK;
+}
 
-bool guard_ok(const netra_profile_info_t& p, const netra_launch_shape_t& s) {
-  return s.m >= p.min_m && s.m <= p.max_m && s.batch >= p.min_batch && s.batch <= p.max_batch &&
-         s.sequence >= p.min_sequence && s.sequence <= p.max_sequence &&
+bool busy(const netra_engine* e) { return e->in_flight.load(std::memory_order_acquire) != 0; }
+bool finalized(const netra_engine* e) { return e->finalized.load(std::memory_order_acquire); }
+
+// First pointer slot of an operation with nothing bound, or -1.
+int first_unbound(const OpRecord& op) {
+  for (uint32_t a = 0; a < op.argument_count; ++a)
+    if (op.bindable[a] && op.pointers[a] == nullptr) return static_cast<int>(a);
+  return -1;
+}
+
+bool within_guards(const netra_profile_info_t& p, const netra_launch_shape_t& s) {
+  return p.min_m <= s.m && s.m <= p.max_m && p.min_batch <= s.batch && s.batch <= p.max_batch &&
+         p.min_sequence <= s.sequence && s.sequence <= p.max_sequence &&
          s.tensor_parallel == p.tensor_parallel;
 }
 
-bool all_bound(const OpRecord& op) {
-  for (uint32_t i = 0; i < op.argument_count; ++i)
-    if (op.bindable[i] && op.pointers[i] == nullptr) return false;
-  return true;
+// Shared first checks of the three launch entry points, after argument
+// validation: the current device is the engine's (UNSUPPORTED_TARGET), then
+// the shape is inside the profile's guards (UNSUPPORTED_PROFILE).
+netra_status_t admit(netra_engine* e, const ProfileRecord& p, const netra_launch_shape_t& shape) {
+  int device = -1;
+  const hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return hip_refusal(e, "hipGetDevice", err);
+  if (device != e->device)
+    return refuse(e, NETRA_STATUS_UNSUPPORTED_TARGET,
+                  "launch refused: current device %d is not the engine's device %d", device, e->device);
+  if (!within_guards(p.info, shape))
+    return refuse(e, NETRA_STATUS_UNSUPPORTED_PROFILE,
+                  "launch refused: shape (m=%u, batch=%u, sequence=%llu, tp=%u) is outside profile %u's "
+                  "guards; the caller takes its framework path",
+                  shape.m, shape.batch, static_cast<unsigned long long>(shape.sequence),
+                  shape.tensor_parallel, p.info.profile_id);
+  return NETRA_STATUS_OK;
 }
 
-hipError_t submit(const OpRecord& op, void** params, hipStream_t stream) {
+// Marks one launch call in flight for its lifetime.
+struct LaunchScope {
+  netra_engine* e;
+  explicit LaunchScope(netra_engine* engine) : e(engine) { e->in_flight.fetch_add(1, std::memory_order_acq_rel); }
+  ~LaunchScope() { e->in_flight.fetch_sub(1, std::memory_order_acq_rel); }
+};
+
+hipError_t dispatch(const OpRecord& op, void** params, hipStream_t stream) {
   return hipModuleLaunchKernel(op.function, op.grid[0], op.grid[1], op.grid[2], op.block[0],
                                op.block[1], op.block[2], op.dynamic_lds_bytes, stream, params,
                                nullptr);
 }
 
-netra_status_t launch_all(netra_engine* e, ProfileRecord& p, hipStream_t stream) {
-  for (OpRecord& op : p.ops) {
+// Every operation of a profile in order, from the bound records.
+netra_status_t dispatch_profile(netra_engine* e, const ProfileRecord& p, hipStream_t stream) {
+  for (size_t i = 0; i < p.ops.size(); ++i) {
+    const OpRecord& op = p.ops[i];
     if (op.fallback)
-      return fail(e, NETRA_STATUS_FALLBACK_REQUIRED, "profile contains a framework fallback operation");
-    if (!all_bound(op)) return fail(e, NETRA_STATUS_BINDING, "kernel pointer argument is unbound");
-    const hipError_t err = submit(op, op.params.data(), stream);
-    if (err != hipSuccess) return hip_fail(e, "hipModuleLaunchKernel", err);
+      return refuse(e, NETRA_STATUS_FALLBACK_REQUIRED,
+                    "profile %u operation %zu is a framework-fallback operation", p.info.profile_id, i);
+    const int hole = first_unbound(op);
+    if (hole >= 0)
+      return refuse(e, NETRA_STATUS_BINDING, "operation %zu argument %d has no pointer bound", i, hole);
+    void** params = const_cast<void**>(op.params.data());
+    const hipError_t err = dispatch(op, params, stream);
+    if (err != hipSuccess) return hip_refusal(e, "hipModuleLaunchKernel", err);
   }
   return NETRA_STATUS_OK;
 }
@@ -113,16 +169,6 @@ void release(netra_engine* e) {
   for (auto& kv : e->modules)
     if (kv.second) (void)hipModuleUnload(kv.second);
   if (e->workspace) (void)hipFree(e->workspace);
-}
-
-netra_status_t check_device(netra_engine* e) {
-  int device = -1;
-  const hipError_t err = hipGetDevice(&device);
-  if (err != hipSuccess) return hip_fail(e, "hipGetDevice", err);
-  if (device != e->device)
-    return fail(e, NETRA_STATUS_UNSUPPORTED_TARGET,
-                "caller stream/device does not belong to engine device");
-  return NETRA_STATUS_OK;
 }
 
 // Restores the caller's current device when create returns.
@@ -259,6 +305,7 @@ extern "C" netra_status_t netra_engine_create(const char* directory,
         switch (as.kind) {
           case netra::ArgumentSpec::Kind::Binding:
             op.bindable[a] = true;
+            ++op.slot_count;
             break;
           case netra::ArgumentSpec::Kind::Workspace:
             op.pointers[a] = static_cast<unsigned char*>(e->workspace) + as.workspace_offset;
@@ -290,170 +337,228 @@ extern "C" netra_status_t netra_engine_query_profile(const netra_engine_t* e, ui
   return NETRA_STATUS_OK;
 }
 
+// bind, checks in order:
+//   null engine or pointer                          INVALID_ARGUMENT
+//   bindings finalized                              BUSY
+//   a launch in flight                              BUSY
+//   profile or operation index out of range         BINDING
+//   profile already captured                        BUSY
+//   argument index out of range                     BINDING
+//   argument is not a caller pointer slot           BINDING
 extern "C" netra_status_t netra_engine_bind(netra_engine_t* e, uint32_t profile_id,
                                             uint32_t op_index, uint32_t arg_index, void* ptr) {
   if (!e || !ptr) return NETRA_STATUS_INVALID_ARGUMENT;
-  if (e->finalized.load(std::memory_order_acquire))
-    return fail(e, NETRA_STATUS_BUSY, "bindings are finalized and immutable");
-  if (e->in_flight.load(std::memory_order_acquire))
-    return fail(e, NETRA_STATUS_BUSY, "cannot bind during launch");
-  if (profile_id >= e->profiles.size() || op_index >= e->profiles[profile_id].ops.size())
-    return fail(e, NETRA_STATUS_BINDING, "binding index out of range");
+  if (finalized(e)) return refuse(e, NETRA_STATUS_BUSY, "bindings are finalized and immutable");
+  if (busy(e)) return refuse(e, NETRA_STATUS_BUSY, "bind refused: a launch is in progress");
+  const bool indexed = profile_id < e->profiles.size() && op_index < e->profiles[profile_id].ops.size();
+  if (!indexed)
+    return refuse(e, NETRA_STATUS_BINDING, "bind refused: no operation %u in profile %u", op_index, profile_id);
   ProfileRecord& p = e->profiles[profile_id];
-  if (p.graph_ready) return fail(e, NETRA_STATUS_BUSY, "bindings are immutable after graph preparation");
+  if (p.captured)
+    return refuse(e, NETRA_STATUS_BUSY, "bind refused: profile %u is captured into a graph", profile_id);
   OpRecord& op = p.ops[op_index];
-  if (arg_index >= op.argument_count) return fail(e, NETRA_STATUS_BINDING, "argument index out of range");
+  if (arg_index >= op.argument_count)
+    return refuse(e, NETRA_STATUS_BINDING, "bind refused: operation %u has %u arguments, not %u", op_index,
+                  op.argument_count, arg_index + 1);
   if (!op.bindable[arg_index])
-    return fail(e, NETRA_STATUS_BINDING, "constant kernel arguments cannot be rebound");
+    return refuse(e, NETRA_STATUS_BINDING,
+                  "bind refused: argument %u of operation %u is fixed by the manifest", arg_index, op_index);
   op.pointers[arg_index] = ptr;
-  clear_error(e);
-  return NETRA_STATUS_OK;
+  return accept(e);
 }
 
+// finalize_bindings (idempotent), checks in order:
+//   null engine                                     INVALID_ARGUMENT
+//   a launch in flight                              BUSY
+//   a kernel operation with an unbound pointer slot BINDING
 extern "C" netra_status_t netra_engine_finalize_bindings(netra_engine_t* e) {
   if (!e) return NETRA_STATUS_INVALID_ARGUMENT;
-  if (e->in_flight.load(std::memory_order_acquire))
-    return fail(e, NETRA_STATUS_BUSY, "cannot finalize bindings during launch");
-  for (const ProfileRecord& p : e->profiles)
-    for (const OpRecord& op : p.ops)
-      if (!op.fallback && !all_bound(op))
-        return fail(e, NETRA_STATUS_BINDING,
-                    "all direct-launch pointers must be bound before finalization");
+  if (busy(e)) return refuse(e, NETRA_STATUS_BUSY, "finalize refused: a launch is in progress");
+  for (const ProfileRecord& p : e->profiles) {
+    for (size_t i = 0; i < p.ops.size(); ++i) {
+      if (p.ops[i].fallback) continue;
+      const int hole = first_unbound(p.ops[i]);
+      if (hole >= 0)
+        return refuse(e, NETRA_STATUS_BINDING,
+                      "finalize refused: profile %u operation %zu argument %d has no pointer bound",
+                      p.info.profile_id, i, hole);
+    }
+  }
   e->finalized.store(true, std::memory_order_release);
-  clear_error(e);
-  return NETRA_STATUS_OK;
+  return accept(e);
 }
 
+// prepare_profile, checks in order:
+//   null engine or profile out of range             INVALID_ARGUMENT
+//   capture disabled, or profile already captured   OK (nothing to do)
+//   profile has a framework-fallback operation      FALLBACK_REQUIRED
+//   finalize_bindings                               its status
+//   capture / instantiate                           HIP, or the dispatch status
 extern "C" netra_status_t netra_engine_prepare_profile(netra_engine_t* e, uint32_t profile_id,
                                                        hipStream_t stream) {
   if (!e || profile_id >= e->profiles.size()) return NETRA_STATUS_INVALID_ARGUMENT;
   ProfileRecord& p = e->profiles[profile_id];
-  if (!e->graph_capture || p.graph_ready) return NETRA_STATUS_OK;
+  if (!e->graph_capture || p.captured) return NETRA_STATUS_OK;
   if (p.info.requires_fallback)
-    return fail(e, NETRA_STATUS_FALLBACK_REQUIRED, "fallback profile cannot be captured");
-  const netra_status_t fin = netra_engine_finalize_bindings(e);
-  if (fin != NETRA_STATUS_OK) return fin;
+    return refuse(e, NETRA_STATUS_FALLBACK_REQUIRED,
+                  "capture refused: profile %u contains a framework-fallback operation", profile_id);
+  const netra_status_t bound = netra_engine_finalize_bindings(e);
+  if (bound != NETRA_STATUS_OK) return bound;
   hipError_t err = hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal);
-  if (err != hipSuccess) return hip_fail(e, "hipStreamBeginCapture", err);
-  const netra_status_t st = launch_all(e, p, stream);
+  if (err != hipSuccess) return hip_refusal(e, "hipStreamBeginCapture", err);
+  const netra_status_t recorded = dispatch_profile(e, p, stream);
   hipGraph_t graph = nullptr;
   err = hipStreamEndCapture(stream, &graph);
-  if (st != NETRA_STATUS_OK) {
+  if (recorded != NETRA_STATUS_OK || err != hipSuccess) {
     if (graph) (void)hipGraphDestroy(graph);
-    return st;
+    return recorded != NETRA_STATUS_OK ? recorded : hip_refusal(e, "hipStreamEndCapture", err);
   }
-  if (err != hipSuccess) return hip_fail(e, "hipStreamEndCapture", err);
-  err = hipGraphInstantiate(&p.graph_exec, graph, nullptr, nullptr, 0);
+  hipGraphExec_t exec = nullptr;
+  err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
   if (err != hipSuccess) {
     (void)hipGraphDestroy(graph);
-    return hip_fail(e, "hipGraphInstantiate", err);
+    return hip_refusal(e, "hipGraphInstantiate", err);
   }
   p.graph = graph;
-  p.graph_ready = true;
-  return NETRA_STATUS_OK;
+  p.graph_exec = exec;
+  p.captured = true;
+  return accept(e);
 }
 
+// launch, checks in order:
+//   null engine or shape, profile out of range      INVALID_ARGUMENT
+//   current device is not the engine's              UNSUPPORTED_TARGET
+//   shape outside the profile's guards              UNSUPPORTED_PROFILE
+//   profile has a framework-fallback operation      FALLBACK_REQUIRED
+//   not captured and bindings not finalized         BINDING
+//   graph launch / kernel launch                    HIP
 extern "C" netra_status_t netra_engine_launch(netra_engine_t* e, uint32_t profile_id,
                                               const netra_launch_shape_t* shape,
                                               hipStream_t stream) {
   if (!e || !shape || profile_id >= e->profiles.size()) return NETRA_STATUS_INVALID_ARGUMENT;
-  netra_status_t st = check_device(e);
-  if (st != NETRA_STATUS_OK) return st;
-  ProfileRecord& p = e->profiles[profile_id];
-  if (!guard_ok(p.info, *shape))
-    return fail(e, NETRA_STATUS_UNSUPPORTED_PROFILE,
-                "exact/bounded profile guard failed; framework fallback required");
+  const ProfileRecord& p = e->profiles[profile_id];
+  const netra_status_t admitted = admit(e, p, *shape);
+  if (admitted != NETRA_STATUS_OK) return admitted;
   if (p.info.requires_fallback)
-    return fail(e, NETRA_STATUS_FALLBACK_REQUIRED, "profile contains a framework fallback operation");
-  if (!p.graph_ready && !e->finalized.load(std::memory_order_acquire))
-    return fail(e, NETRA_STATUS_BINDING, "direct-launch bindings were not finalized");
-  e->in_flight.fetch_add(1, std::memory_order_acq_rel);
-  if (p.graph_ready) {
+    return refuse(e, NETRA_STATUS_FALLBACK_REQUIRED,
+                  "launch refused: profile %u contains a framework-fallback operation", profile_id);
+  if (!p.captured && !finalized(e))
+    return refuse(e, NETRA_STATUS_BINDING, "launch refused: bindings are not finalized");
+  LaunchScope scope(e);
+  if (p.captured) {
     const hipError_t err = hipGraphLaunch(p.graph_exec, stream);
-    st = err == hipSuccess ? NETRA_STATUS_OK : hip_fail(e, "hipGraphLaunch", err);
-  } else {
-    st = launch_all(e, p, stream);
+    return err == hipSuccess ? NETRA_STATUS_OK : hip_refusal(e, "hipGraphLaunch", err);
   }
-  e->in_flight.fetch_sub(1, std::memory_order_acq_rel);
-  return st;
+  return dispatch_profile(e, p, stream);
 }
 
+// launch_operation, checks in order:
+//   null engine or shape, profile/operation out of range   INVALID_ARGUMENT
+//   current device is not the engine's                      UNSUPPORTED_TARGET
+//   shape outside the profile's guards                      UNSUPPORTED_PROFILE
+//   profile captured (single operations are closed)         BUSY
+//   operation is a framework-fallback operation             FALLBACK_REQUIRED
+//   bindings not finalized                                  BINDING
+//   an unbound pointer slot                                 BINDING
+//   kernel launch                                           HIP
 extern "C" netra_status_t netra_engine_launch_operation(netra_engine_t* e, uint32_t profile_id,
                                                         uint32_t op_index,
                                                         const netra_launch_shape_t* shape,
                                                         hipStream_t stream) {
-  if (!e || !shape || profile_id >= e->profiles.size() ||
-      op_index >= e->profiles[profile_id].ops.size())
+  if (!e || !shape || profile_id >= e->profiles.size() || op_index >= e->profiles[profile_id].ops.size())
     return NETRA_STATUS_INVALID_ARGUMENT;
-  netra_status_t st = check_device(e);
-  if (st != NETRA_STATUS_OK) return st;
-  ProfileRecord& p = e->profiles[profile_id];
-  if (!guard_ok(p.info, *shape))
-    return fail(e, NETRA_STATUS_UNSUPPORTED_PROFILE,
-                "exact/bounded profile guard failed; framework fallback required");
-  if (p.graph_ready)
-    return fail(e, NETRA_STATUS_BUSY, "individual operations cannot launch after graph preparation");
-  OpRecord& op = p.ops[op_index];
-  if (op.fallback) return fail(e, NETRA_STATUS_FALLBACK_REQUIRED, "operation requires framework fallback");
-  if (!e->finalized.load(std::memory_order_acquire))
-    return fail(e, NETRA_STATUS_BINDING, "direct-launch bindings were not finalized");
-  if (!all_bound(op)) return fail(e, NETRA_STATUS_BINDING, "kernel pointer argument is unbound");
-  e->in_flight.fetch_add(1, std::memory_order_acq_rel);
-  const hipError_t err = submit(op, op.params.data(), stream);
-  st = err == hipSuccess ? NETRA_STATUS_OK : hip_fail(e, "hipModuleLaunchKernel", err);
-  e->in_flight.fetch_sub(1, std::memory_order_acq_rel);
-  return st;
+  const ProfileRecord& p = e->profiles[profile_id];
+  const netra_status_t admitted = admit(e, p, *shape);
+  if (admitted != NETRA_STATUS_OK) return admitted;
+  if (p.captured)
+    return refuse(e, NETRA_STATUS_BUSY,
+                  "launch refused: profile %u is captured; it launches only as its graph", profile_id);
+  const OpRecord& op = p.ops[op_index];
+  if (op.fallback)
+    return refuse(e, NETRA_STATUS_FALLBACK_REQUIRED,
+                  "launch refused: operation %u is a framework-fallback operation", op_index);
+  if (!finalized(e)) return refuse(e, NETRA_STATUS_BINDING, "launch refused: bindings are not finalized");
+  const int hole = first_unbound(op);
+  if (hole >= 0)
+    return refuse(e, NETRA_STATUS_BINDING, "launch refused: operation %u argument %d has no pointer bound",
+                  op_index, hole);
+  LaunchScope scope(e);
+  const hipError_t err = dispatch(op, const_cast<void**>(op.params.data()), stream);
+  return err == hipSuccess ? NETRA_STATUS_OK : hip_refusal(e, "hipModuleLaunchKernel", err);
 }
 
+// launch_operation_bound (caller-local pointers; the engine's records are not
+// touched, so concurrent calls need no lock), checks in order:
+//   null engine or shape, profile/operation out of range,
+//   more than 16 entries, entries without an array          INVALID_ARGUMENT
+//   current device is not the engine's                      UNSUPPORTED_TARGET
+//   shape outside the profile's guards                      UNSUPPORTED_PROFILE
+//   profile captured                                        BUSY
+//   operation is a framework-fallback operation             FALLBACK_REQUIRED
+//   entry count differs from the operation's pointer slots  BINDING
+//   an entry with reserved != 0, a null pointer, or an
+//   index that is not a pointer slot                        BINDING
+//   the same slot twice                                     BINDING
+//   kernel launch                                           HIP
 extern "C" netra_status_t netra_engine_launch_operation_bound(
     netra_engine_t* e, uint32_t profile_id, uint32_t op_index, const netra_launch_shape_t* shape,
     const netra_pointer_binding_t* bindings, uint32_t count, hipStream_t stream) {
-  if (!e || !shape || profile_id >= e->profiles.size() ||
-      op_index >= e->profiles[profile_id].ops.size() || (count && !bindings) || count > 16)
+  constexpr uint32_t kMaxEntries = 16;
+  if (!e || !shape || profile_id >= e->profiles.size() || op_index >= e->profiles[profile_id].ops.size() ||
+      count > kMaxEntries || (count != 0 && bindings == nullptr))
     return NETRA_STATUS_INVALID_ARGUMENT;
-  netra_status_t st = check_device(e);
-  if (st != NETRA_STATUS_OK) return st;
-  ProfileRecord& p = e->profiles[profile_id];
-  if (!guard_ok(p.info, *shape))
-    return fail(e, NETRA_STATUS_UNSUPPORTED_PROFILE,
-                "exact/bounded profile guard failed; framework fallback required");
-  if (p.graph_ready)
-    return fail(e, NETRA_STATUS_BUSY, "operation bindings are immutable after graph preparation");
+  const ProfileRecord& p = e->profiles[profile_id];
+  const netra_status_t admitted = admit(e, p, *shape);
+  if (admitted != NETRA_STATUS_OK) return admitted;
+  if (p.captured)
+    return refuse(e, NETRA_STATUS_BUSY,
+                  "bound launch refused: profile %u is captured; it launches only as its graph", profile_id);
   const OpRecord& op = p.ops[op_index];
-  if (op.fallback) return fail(e, NETRA_STATUS_FALLBACK_REQUIRED, "operation requires framework fallback");
-  uint32_t slots = 0;
-  for (uint32_t a = 0; a < op.argument_count; ++a) slots += op.bindable[a] ? 1u : 0u;
-  if (count != slots)
-    return fail(e, NETRA_STATUS_BINDING, "bound operation must provide every declared pointer slot");
+  if (op.fallback)
+    return refuse(e, NETRA_STATUS_FALLBACK_REQUIRED,
+                  "bound launch refused: operation %u is a framework-fallback operation", op_index);
+  if (count != op.slot_count)
+    return refuse(e, NETRA_STATUS_BINDING, "bound launch refused: operation %u has %u pointer slots, got %u",
+                  op_index, op.slot_count, count);
+  // Kernel arguments on this call's stack: manifest constants and workspace
+  // pointers from the record, pointer slots from the caller's entries.
   std::array<void*, netra::kMaxArguments> values{};
   std::array<void*, netra::kMaxArguments> params{};
-  std::array<bool, netra::kMaxArguments> seen{};
-  for (uint32_t a = 0; a < op.argument_count; ++a) values[a] = op.bindable[a] ? nullptr : op.pointers[a];
+  uint64_t supplied = 0;  // bit a: slot a has an entry (kMaxArguments <= 64)
+  static_assert(netra::kMaxArguments <= 64, "slot bitmap");
   for (uint32_t i = 0; i < count; ++i) {
-    const uint32_t a = bindings[i].argument_index;
-    if (bindings[i].reserved || !bindings[i].pointer || a >= op.argument_count || !op.bindable[a])
-      return fail(e, NETRA_STATUS_BINDING, "bound operation contains an invalid pointer slot");
-    if (seen[a]) return fail(e, NETRA_STATUS_BINDING, "bound operation contains a duplicate pointer slot");
-    seen[a] = true;
-    values[a] = bindings[i].pointer;
+    const netra_pointer_binding_t& b = bindings[i];
+    const uint32_t a = b.argument_index;
+    if (b.reserved != 0 || b.pointer == nullptr || a >= op.argument_count || !op.bindable[a])
+      return refuse(e, NETRA_STATUS_BINDING,
+                    "bound launch refused: entry %u (argument %u) is not a usable pointer slot", i, a);
+    if (supplied >> a & 1u)
+      return refuse(e, NETRA_STATUS_BINDING, "bound launch refused: argument %u is supplied twice", a);
+    supplied |= uint64_t{1} << a;
+    values[a] = b.pointer;
   }
-  for (uint32_t a = 0; a < op.argument_count; ++a)
-    params[a] = op.is_scalar[a] ? const_cast<uint32_t*>(&op.scalars[a]) : static_cast<void*>(&values[a]);
-  e->in_flight.fetch_add(1, std::memory_order_acq_rel);
-  const hipError_t err = submit(op, params.data(), stream);
-  st = err == hipSuccess ? NETRA_STATUS_OK : hip_fail(e, "hipModuleLaunchKernel", err);
-  e->in_flight.fetch_sub(1, std::memory_order_acq_rel);
-  return st;
+  for (uint32_t a = 0; a < op.argument_count; ++a) {
+    if (op.is_scalar[a]) {
+      params[a] = const_cast<uint32_t*>(&op.scalars[a]);
+    } else {
+      if (!op.bindable[a]) values[a] = op.pointers[a];
+      params[a] = &values[a];
+    }
+  }
+  LaunchScope scope(e);
+  const hipError_t err = dispatch(op, params.data(), stream);
+  return err == hipSuccess ? NETRA_STATUS_OK : hip_refusal(e, "hipModuleLaunchKernel", err);
 }
 
 extern "C" const char* netra_engine_last_error(const netra_engine_t* e) {
-  return e ? e->last_error : "netra_engine is null";
+  return e ? e->last_error : "no engine handle";
 }
 
+// destroy: null engine is OK; a launch in flight is BUSY; otherwise every
+// graph, module and the workspace are released.
 extern "C" netra_status_t netra_engine_destroy(netra_engine_t* e) {
   if (!e) return NETRA_STATUS_OK;
-  if (e->in_flight.load(std::memory_order_acquire))
-    return fail(e, NETRA_STATUS_BUSY, "launches remain in flight");
+  if (busy(e)) return refuse(e, NETRA_STATUS_BUSY, "destroy refused: a launch is in progress");
   release(e);
   delete e;
   return NETRA_STATUS_OK;

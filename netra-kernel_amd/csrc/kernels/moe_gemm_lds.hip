@@ -74,12 +74,13 @@ __device__ __forceinline__ u32x4 rsrc(const void* base, uint32_t bytes) {
 // the s_nop 4 supplies the five wait states a vector-memory instruction needs
 // after a VALU write (v_readfirstlane, v_readlane, carry outputs) of an SGPR
 // it reads (resource, offset), which also covers the M0 write before an
-// LDS-destination load.
+// LDS-destination load. m0 is declared clobbered so the compiler keeps no
+// value of its own there across the copy.
 __device__ __forceinline__ void copy16(uint32_t m0, u32x4 r, uint32_t voff, uint32_t soff) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :
                : "s"(m0), "v"(voff), "s"(r), "s"(soff)
-               : "memory");
+               : "memory", "m0");
 }
 
 template <uint32_t N>

@@ -392,6 +392,32 @@ def operations(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> list[
     return ops
 
 
+# Contract semantics. The layouts semantic names what the kernels read: W13 in
+# the gate/up-interleaved tile16x128 layout (netra_moe_pack_tiles_gate_up), W2
+# in tile16x128, sorted ids in 64-row expert blocks with (slot << 24) | token,
+# and h between the GEMMs in the path's own layout. A planner that matches on
+# semantics (as the reference's does, compiler/netra_compiler/backends/gfx950/
+# catalog.py:89-212) must not hand these kernels row-major or AITER-shuffled
+# weights. The numerical semantic differs by front end: the screen front end
+# leaves non-selected logits as bf16 MFMA screen values, not contract values.
+WEIGHT_LAYOUTS = "w13_tile16x128_gate_up_interleaved.w2_tile16x128"
+H_LAYOUTS = {"stream": "h_tile16x128_rowscale16", "tile": "h_row_major_rowscale"}
+NUMERICS = {
+    "exact": "router_16slice_fma_tree.topk_lowidx.exp_cw7.v1",
+    "screen": "router_bf16_mfma_screen_certified_exact_candidates.topk_lowidx.exp_cw7.v1",
+}
+QUANTIZATION = "fp8e4m3fn_block128x128_weights_1x128_activations.v1"
+
+
+def layouts_semantic(path: str) -> str:
+    return f"{WEIGHT_LAYOUTS}.sorted_m64_slot24.{H_LAYOUTS[path]}.v1"
+
+
+def layer_semantics(symbol: str, path: str, front: str) -> tuple[tuple[str, str], ...]:
+    return (("abi", f"{symbol}.ptr_then_u32.v1"), ("quantization", QUANTIZATION),
+            ("layouts", layouts_semantic(path)), ("numerical", NUMERICS[front]))
+
+
 def _dependencies(ops: list[dict]) -> list[list[int]]:
     deps = []
     for i, op in enumerate(ops):
@@ -453,10 +479,7 @@ def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ..
             operation=op["name"], family="moe.fp8_block128.gfx950_hip", symbol=op["symbol"],
             constants=(("T", cfg.T), ("H", cfg.H), ("I", cfg.I), ("E", cfg.E), ("K", cfg.K),
                        ("S", cfg.S), ("BLOCK_M", BLOCK_M), ("SCALE_BLOCK", 128)),
-            semantics=(("abi", f"{op['symbol']}.ptr_then_u32.v1"),
-                       ("quantization", "fp8e4m3fn_block128x128_weights_1x128_activations.v1"),
-                       ("layouts", "row_major_expert_nk.sorted_m64_slot24.v1"),
-                       ("numerical", "router_16slice_fma_tree.topk_lowidx.exp_cw7.v1")),
+            semantics=layer_semantics(op["symbol"], path, front),
             launch=launch, kernarg_size=kernarg, code_object_sha256=sha,
             source_refs=tuple(op["refs"]))
         contracts.append(contract.to_dict())

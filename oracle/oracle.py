@@ -151,16 +151,29 @@ def sort(ids: np.ndarray, Etot: int, cap_blocks: int | None = None, bm: int = BL
 
 
 def gate_up(x_q, x_s, w13, w13_s, sorted_ids, sorted_expert, num_valid_rows, T, H, I,
-            threads: int | None = None):
-    """a6 + a7 over the sorted rows: (h_q, h_s, h_bf16) in sorted layout."""
+            threads: int | None = None, bm: int = BLOCK_M):
+    """a6 + a7 over the sorted rows: (h_q, h_s, h_bf16) in sorted layout.
+    Row r uses expert sorted_expert[r // bm]; bm = 1 with per-row experts
+    evaluates an arbitrary selection of sorted rows."""
     rows = sorted_ids.shape[0]
     h_q = np.zeros((rows, I), np.uint8)
     h_s = np.zeros((rows, I // 128), np.float32)
     h_b = np.zeros((rows, I), np.uint16)
     arrs = [np.ascontiguousarray(a) for a in (x_q, x_s, w13, w13_s, sorted_ids, sorted_expert)]
-    lib().orc_gate_up(*[_p(a) for a in arrs], int(num_valid_rows), T, H, I, BLOCK_M,
+    lib().orc_gate_up(*[_p(a) for a in arrs], int(num_valid_rows), T, H, I, bm,
                       _p(h_q), _p(h_s), _p(h_b), threads or default_threads())
     return h_q, h_s, h_b
+
+
+def gate_up_rows(x_q, x_s, w13, w13_s, sorted_ids, sorted_expert, rows, T, H, I,
+                 threads: int | None = None):
+    """gate_up() on the sorted rows listed in `rows` only (any order):
+    (h_q, h_s) with one row per entry of `rows`."""
+    rows = np.asarray(rows, dtype=np.int64)
+    sid = np.ascontiguousarray(sorted_ids[rows], dtype=np.int32)
+    sexp = np.ascontiguousarray(sorted_expert[rows // BLOCK_M], dtype=np.int32)
+    h_q, h_s, _ = gate_up(x_q, x_s, w13, w13_s, sid, sexp, rows.size, T, H, I, threads, bm=1)
+    return h_q, h_s
 
 
 def down_combine(h_q, h_s, w2, w2_s, sorted_ids, sorted_expert, num_valid_rows, weights, T, H, I,

@@ -1,11 +1,19 @@
-"""Static check of the built gfx950 code object for one hazard the compiler
-cannot see: a vector-memory instruction (buffer/global/flat) that reads an
-SGPR fewer than five wait states after a VALU instruction wrote it
-(v_readfirstlane, v_readlane, VALU compares and carry-outs). The hardware
-needs those wait states; the compiler inserts them for its own instructions
-but not around inline assembly, and several kernels issue their copies from
-inline assembly. A missed case reads a stale resource descriptor or offset,
-which can address memory outside every buffer.
+"""Static checks of the built gfx950 code object for what the compiler
+cannot see around inline assembly:
+
+* a vector-memory instruction (buffer/global/flat) that reads an SGPR fewer
+  than five wait states after a VALU instruction wrote it (v_readfirstlane,
+  v_readlane, VALU compares and carry-outs). The hardware needs those wait
+  states; the compiler inserts them for its own instructions but not around
+  inline assembly, and several kernels issue their copies from inline
+  assembly. A missed case reads a stale resource descriptor or offset, which
+  can address memory outside every buffer.
+* the LDS-ring gate/up kernels wait for "this step's copies landed" with
+  s_waitcnt vmcnt(6): correct only while the six buffer-to-LDS copies a wave
+  issues per 128-K step are the only vector-memory operations in flight in
+  the K loop. If the compiler ever turned the per-step weight-scale loads
+  (uniform addresses, scalar loads today) into vector loads, the count would
+  be off and a step would read a stage before its data arrived.
 
 Runs on the CPU over the disassembly of this repository's own build (the
 ROCm llvm tools); skipped when the code object or the tools are absent.
@@ -116,3 +124,60 @@ def test_no_valu_sgpr_to_vmem_hazard_in_any_kernel():
     assert kernels, "no netra_moe_ kernels in the code object"
     report = {k: h for k, v in kernels.items() if (h := hazards(v))}
     assert not report, "\n".join(f"{k}: {h[0]}" for k, h in report.items())
+
+
+KCOPIES = 6  # buffer-to-LDS copies per wave per 128-K step (kCopiesPerWave in moe_gemm_lds.hip)
+_VMCNT = re.compile(r"vmcnt\((\d+)\)")
+
+
+def ring_violations(lines: list[str]) -> list[str]:
+    """Vector-memory accounting of one LDS-ring kernel (instructions in address
+    order): between its first and last buffer-to-LDS copy there is no other
+    vector-memory instruction and every vmcnt wait is 0 or KCOPIES; after the
+    last copy, the first other vector-memory instruction comes behind a
+    vmcnt(0)."""
+    text = [t.split("//")[0].strip() for t in lines]
+    text = [t for t in text if t and not t.endswith(":")]
+    is_copy = [bool(re.match(r"buffer_load_dword\w*\s.*\blds\b", t)) for t in text]
+    copies = [i for i, c in enumerate(is_copy) if c]
+    if not copies:
+        return ["no buffer-to-LDS copies"]
+    first, last = copies[0], copies[-1]
+    bad = []
+    for i in range(first, last + 1):
+        t = text[i]
+        if _VMEM.match(t) and not is_copy[i]:
+            bad.append(f"vector-memory op inside the copy ring: {t}")
+        m = _VMCNT.search(t) if t.startswith("s_waitcnt") else None
+        if m and int(m.group(1)) not in (0, KCOPIES):
+            bad.append(f"unexpected wait inside the copy ring: {t}")
+    drained = False
+    for t in text[last + 1:]:
+        m = _VMCNT.search(t) if t.startswith("s_waitcnt") else None
+        if m and int(m.group(1)) == 0:
+            drained = True
+        if _VMEM.match(t):
+            if not drained:
+                bad.append(f"vector-memory op before the ring drains: {t}")
+            break
+    return bad
+
+
+def test_ring_checker_flags_a_foreign_load():
+    ring = ["buffer_load_dwordx4 v1, s[4:7], s1 offen lds", "s_waitcnt vmcnt(6)",
+            "buffer_load_dwordx4 v2, s[4:7], s1 offen lds", "s_waitcnt vmcnt(0)",
+            "global_store_dword v[0:1], v3, off"]
+    assert ring_violations(ring) == []
+    foreign = ring[:2] + ["global_load_dword v5, v[6:7], off"] + ring[2:]
+    assert any("inside the copy ring" in v for v in ring_violations(foreign))
+    early = ring[:3] + ["global_store_dword v[0:1], v3, off"]
+    assert any("before the ring drains" in v for v in ring_violations(early))
+    assert ring_violations(ring[:1] + ["s_waitcnt vmcnt(5)"] + ring[2:])
+
+
+def test_lds_ring_kernels_issue_only_their_copies():
+    funcs = disassembly()
+    ring = {k: v for k, v in funcs.items() if k.startswith("netra_moe_gate_up_lds_")}
+    assert ring, "no netra_moe_gate_up_lds_ kernels in the code object"
+    report = {k: b for k, v in ring.items() if (b := ring_violations(v))}
+    assert not report, "\n".join(f"{k}: {b[0]}" for k, b in report.items())

@@ -95,3 +95,18 @@ def test_single_expert_layer_is_the_swiglu_ffn():
     # while gate and up swapped, or the down weights transposed per block, are far off
     bad = (torch.nn.functional.silu(xt @ wu.T) * (xt @ wg.T)) @ torch.from_numpy(w2[0].astype(np.float64)).T
     assert cos(r["out_f32"].astype(np.float64), bad.numpy()) < 0.9
+
+
+def test_gate_up_rows_equals_the_sorted_pass_on_a_selection():
+    """gate_up_rows (the row-sampled driver the GPU parity test uses at large T)
+    returns exactly the sorted pass's rows, in the order asked."""
+    T, H, E, K, I = 40, 256, 6, 3, 128
+    x, router, _, _, q13, s13, q2, s2 = make(T, H, E, K, I, seed=3)
+    r = oracle.moe_layer(bits(x), bits(router), None, q13, s13, q2, s2, E, K, 0, I, threads=2)
+    nv = int(r["num_valid"][0])
+    rows = np.array([nv - 1, 0, 5, 64, 63, nv // 2], dtype=np.int64)
+    hq, hs = oracle.gate_up_rows(r["x_q"], r["x_scale"], q13, s13, r["sorted_ids"], r["sorted_expert"],
+                                 rows, T, H, I, threads=2)
+    valid = (r["sorted_ids"][rows] & 0xFFFFFF) < T
+    np.testing.assert_array_equal(hq[valid], r["h_q"][rows][valid])
+    np.testing.assert_array_equal(hs[valid].view(np.uint32), r["h_scale"][rows][valid].view(np.uint32))

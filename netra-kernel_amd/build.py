@@ -3,7 +3,8 @@
 Outputs (git-ignored, shipped with the source tree to the GPU host):
   netra-kernel_amd/lib/netra_moe_gfx950.hsaco  code object loaded by the engine
   netra-kernel_amd/lib/libnetra_engine.so      C-ABI engine runtime
-  netra-kernel_amd/lib/libnetra_moe.so         direct entry points (weight prep)
+  netra-kernel_amd/lib/libnetra_moe.so         direct entry points (weight prep, no-alloc prefill)
+  netra-kernel_amd/lib/libnetra_bridges.so     the reference's per-operation bridge ABIs
 
 Run: python netra-kernel_amd/build.py  (or __graft_entry__.build()).
 """
@@ -38,6 +39,7 @@ DEVICE_FLAGS = [
 HSACO = LIB / "netra_moe_gfx950.hsaco"
 ENGINE_SO = LIB / "libnetra_engine.so"
 BRIDGE_SO = LIB / "libnetra_moe.so"
+OPS_SO = LIB / "libnetra_bridges.so"
 
 
 def _run(cmd: list[str]) -> None:
@@ -80,8 +82,24 @@ def build_bridge() -> Path:
     return BRIDGE_SO
 
 
+def build_op_bridges() -> Path:
+    """Host-only library (like the engine): module management and dispatch."""
+    LIB.mkdir(exist_ok=True)
+    tmp = OPS_SO.with_suffix(".so.tmp")
+    cxx = shutil.which("g++") or "g++"
+    _run([
+        cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
+        "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}", f"-I{REPO / 'include'}",
+        str(CSRC / "bridge" / "qwen36_bridges.cpp"),
+        f"-L{ROCM / 'lib'}", f"-Wl,-rpath,{ROCM / 'lib'}", "-lamdhip64",
+        "-o", str(tmp),
+    ])
+    tmp.replace(OPS_SO)
+    return OPS_SO
+
+
 def build_all() -> list[Path]:
-    return [build_hsaco(), build_engine(), build_bridge()]
+    return [build_hsaco(), build_engine(), build_bridge(), build_op_bridges()]
 
 
 if __name__ == "__main__":

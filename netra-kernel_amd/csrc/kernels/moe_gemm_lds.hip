@@ -74,13 +74,17 @@ __device__ __forceinline__ u32x4 rsrc(const void* base, uint32_t bytes) {
 // the s_nop 4 supplies the five wait states a vector-memory instruction needs
 // after a VALU write (v_readfirstlane, v_readlane, carry outputs) of an SGPR
 // it reads (resource, offset), which also covers the M0 write before an
-// LDS-destination load. m0 is declared clobbered so the compiler keeps no
-// value of its own there across the copy.
+// LDS-destination load. The compiler treats m0 as a reserved register and
+// does not honour it in a clobber list, so the copy saves m0 and puts it back
+// (the LDS address is taken from m0 when the load issues): any value the
+// compiler keeps in m0 survives the copy.
 __device__ __forceinline__ void copy16(uint32_t m0, u32x4 r, uint32_t voff, uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 4\n\tbuffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+               "s_mov_b32 m0, %0"
+               : "=&s"(saved)
                : "s"(m0), "v"(voff), "s"(r), "s"(soff)
-               : "memory", "m0");
+               : "memory");
 }
 
 template <uint32_t N>
@@ -92,9 +96,10 @@ __device__ __forceinline__ void wait_copies() {
 // copies in flight (a full __syncthreads would drain those).
 __device__ __forceinline__ void barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+template <bool kAiter = false>
 __device__ __forceinline__ v8i lds_operand(const uint8_t* tile, uint32_t lane) {
-  const uint4 lo = *reinterpret_cast<const uint4*>(tile + lane * 16u);
-  const uint4 hi = *reinterpret_cast<const uint4*>(tile + 1024u + lane * 16u);
+  const uint4 lo = *reinterpret_cast<const uint4*>(tile + nk::operand_lo<kAiter>(lane));
+  const uint4 hi = *reinterpret_cast<const uint4*>(tile + nk::operand_hi<kAiter>(lane));
   v8i r;
   r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
   r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
@@ -109,7 +114,11 @@ __device__ __forceinline__ bool xcd_item(uint32_t i, uint32_t n, uint32_t& item)
   return i / 8u < per && item < n;
 }
 
-template <uint32_t KB>  // H / 128
+// kAiter: W13 in the reference's AITER 16x16 shuffle (gate rows 0..I-1, up
+// rows I..2I-1 as plain row tiles) instead of the gate/up-interleaved
+// tile16x128 layout; the copies move the same 2 KiB blocks, only the up tile's
+// place and the operand reads out of LDS differ.
+template <uint32_t KB, bool kAiter = false>  // H / 128
 __device__ __forceinline__ void gate_up_lds(
     const uint8_t* __restrict__ xq, const float* __restrict__ xs, const uint8_t* __restrict__ w13,
     const float* __restrict__ w13s, const int32_t* __restrict__ sorted_ids,
@@ -163,8 +172,11 @@ __device__ __forceinline__ void gate_up_lds(
   const uint32_t avoff1 = atok >= 0 ? avoff0 + 16u : kFar;
   const u32x4 ra = rsrc(xq, T * H);
   const uint8_t* w13e = w13 + (size_t)e * 2u * I * H;
-  // gate tile t and up tile t are adjacent (gate/up-interleaved W13): one range
-  const u32x4 rg = rsrc(nk::tile_base(w13e, 2u * (ng * 8u + wave), 0, KB), 2u * KB * 2048u);
+  // gate tile t and up tile t are adjacent (gate/up-interleaved W13), or I/16
+  // row tiles apart (AITER): one range from the gate tile through the up tile
+  const uint32_t up_tiles = kAiter ? I / 16u : 1u;  // row tiles from gate tile t to up tile t
+  const u32x4 rg = rsrc(nk::tile_base(w13e, kAiter ? ng * 8u + wave : 2u * (ng * 8u + wave), 0, KB),
+                        (up_tiles + 1u) * KB * 2048u);
   const uint32_t bvoff = lane * 16u;
   const uint32_t lds0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_offset(&s_stage[0][0]));
   // copy q = 0..5 of step kb (A halves, gate halves, up halves) into its stage
@@ -173,7 +185,7 @@ __device__ __forceinline__ void gate_up_lds(
     const uint32_t half = (q & 1u) * 1024u;
     if (q < 2u) copy16(st + wave * 2048u + half, ra, q ? avoff1 : avoff0, kb * 128u);
     else if (q < 4u) copy16(st + kABytes + wave * 2048u + half, rg, bvoff + half, kb * 2048u);
-    else copy16(st + kABytes + (8u + wave) * 2048u + half, rg, bvoff + half, (KB + kb) * 2048u);
+    else copy16(st + kABytes + (8u + wave) * 2048u + half, rg, bvoff + half, (up_tiles * KB + kb) * 2048u);
   };
   auto issue = [&](uint32_t kb) __attribute__((always_inline)) {
 #pragma unroll
@@ -208,7 +220,7 @@ __device__ __forceinline__ void gate_up_lds(
         v8i bw[4];
 #pragma unroll
         for (uint32_t c = 0; c < 4; ++c)  // gate tiles 2n, 2n + 1, up tiles 8 + 2n, 8 + 2n + 1
-          bw[c] = lds_operand(st + kABytes + ((c >> 1) * 8u + 2u * n + (c & 1u)) * 2048u, lane);
+          bw[c] = lds_operand<kAiter>(st + kABytes + ((c >> 1) * 8u + 2u * n + (c & 1u)) * 2048u, lane);
         const float sg = wsg[kb], su = wsu[kb];
 #pragma unroll
         for (uint32_t i = 0; i < NT; ++i) {
@@ -309,3 +321,17 @@ __device__ __forceinline__ void gate_up_lds(
 NK_GATE_UP_LDS(512)
 NK_GATE_UP_LDS(1024)
 NK_GATE_UP_LDS(2048)
+
+// W13 in the reference's AITER layout (the M768 prefill bridge): same ABI.
+#define NK_GATE_UP_LDS_AITER(HV)                                                                   \
+  NK_KERNEL __launch_bounds__(512) void netra_moe_gate_up_lds_aiter_h##HV##_gfx950(                \
+      const uint8_t* __restrict__ xq, const float* __restrict__ xs, const uint8_t* __restrict__ w13, \
+      const float* __restrict__ w13s, const int32_t* __restrict__ sorted_ids,                      \
+      const int32_t* __restrict__ sorted_expert, const int32_t* __restrict__ num_valid,            \
+      const int32_t* __restrict__ pair_map, uint8_t* __restrict__ hq, float* __restrict__ hs,      \
+      uint32_t T, uint32_t H, uint32_t I, uint32_t Ktot, uint32_t Etot) {                          \
+    (void)H;                                                                                       \
+    nklds::gate_up_lds<HV / 128, true>(xq, xs, w13, w13s, sorted_ids, sorted_expert, num_valid,    \
+                                       pair_map, hq, hs, T, I, Ktot, Etot);                        \
+  }
+NK_GATE_UP_LDS_AITER(2048)

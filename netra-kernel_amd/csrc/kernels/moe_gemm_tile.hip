@@ -383,14 +383,27 @@ __device__ __forceinline__ void down_tile(
 // buffers, one barrier per group) so each route row leaves as 256 contiguous
 // bytes; rows past the block's valid count take an offset past the buffer
 // and the hardware drops their stores.
+//
+// kAiter: W2 in the reference's AITER 16x16 shuffle. kSplitF16: the output
+// format of the reference's prefill producer (moe_prefill_m768_bridge.hip:
+// 144-147, route_reduce_splitk2_f16.inc:44-61): two fp16 partial tensors,
+// half h holding the sum over K blocks [h KB/2, (h + 1) KB/2) of each route
+// row, the second one half_rows rows after the first.
 constexpr uint32_t kDownWaves = 8;
 
-template <uint32_t KB>  // I / 128
+__device__ __forceinline__ uint16_t f16_bits(float x) {
+  const _Float16 h = (_Float16)x;  // v_cvt_f16_f32, round to nearest even
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+template <uint32_t KB, bool kAiter = false, bool kSplitF16 = false>  // I / 128
 __device__ __forceinline__ void down_rows(
     const uint8_t* __restrict__ hq, const float* __restrict__ hs, const uint8_t* __restrict__ w2,
     const float* __restrict__ w2s, const int32_t* __restrict__ sorted_ids,
     const int32_t* __restrict__ sorted_expert, const int32_t* __restrict__ num_valid,
-    uint16_t* __restrict__ partial, uint32_t T, uint32_t H, uint32_t Ktot, uint32_t Etot, uint32_t NBC) {
+    uint16_t* __restrict__ partial, uint32_t T, uint32_t H, uint32_t Ktot, uint32_t Etot, uint32_t NBC,
+    uint32_t half_rows = 0) {
+  static_assert(!kSplitF16 || KB % 2 == 0, "split-K halves need an even K block count");
   constexpr uint32_t I = 128u * KB;
   constexpr uint32_t kThreads = 64u * kDownWaves;
   constexpr uint32_t kStride = I + 16u;  // LDS bytes per A row
@@ -422,7 +435,8 @@ __device__ __forceinline__ void down_rows(
   const float* wse = w2s + (size_t)e * NB * KB;
   v8i bq[KB];
 #pragma unroll
-  for (uint32_t kb = 0; kb < KB; ++kb) bq[kb] = nk::load_tile_operand(wt, ((nb0 * 8u + wave) * KB + kb) * 2048u, lane);
+  for (uint32_t kb = 0; kb < KB; ++kb)
+    bq[kb] = nk::load_tile_operand<kAiter>(wt, ((nb0 * 8u + wave) * KB + kb) * 2048u, lane);
   float wsv = wse[nb0 * KB + (lane & (KB - 1u))];
   // the block's A rows (64 x I bytes, contiguous) and scales
   constexpr uint32_t kA16 = kRows * I / 16u / kThreads;  // uint4 per thread
@@ -448,14 +462,38 @@ __device__ __forceinline__ void down_rows(
   // output stores (64 rows x 256 bytes, 2 uint4 per thread): rows past nvalid
   // (or padding) take offset 2^31, past the buffer's range (the engine keeps
   // the partial buffer below 2^31 bytes), so their stores are dropped
-  const __amdgpu_buffer_rsrc_t pr = nk::buffer_rsrc(partial, T * Ktot * H * 2u);
+  const uint32_t half_bytes = half_rows * H * 2u;
+  const __amdgpu_buffer_rsrc_t pr = nk::buffer_rsrc(partial, kSplitF16 ? 2u * half_bytes : T * Ktot * H * 2u);
   uint32_t soff[2];
+  bool live[2];
 #pragma unroll
   for (uint32_t p = 0; p < 2u; ++p) {
     const uint32_t idx = p * kThreads + tid, row = idx >> 4, c16 = idx & 15u;
     const int32_t route = s_route[row];
-    soff[p] = (row < nvalid && route >= 0) ? ((uint32_t)route * H + c16 * 8u) * 2u : 0x80000000u;
+    live[p] = row < nvalid && route >= 0;
+    soff[p] = live[p] ? ((uint32_t)route * H + c16 * 8u) * 2u : 0x80000000u;
   }
+  // One output tile through the LDS transpose: buffer v & 1, one barrier (the
+  // other buffer was read before the previous barrier); `extra` moves live
+  // rows to the second split-K half.
+  auto emit = [&](auto ntc, const v4f* acc, uint32_t v, uint32_t nb, uint32_t extra) __attribute__((always_inline)) {
+    constexpr uint32_t NT = decltype(ntc)::value;
+    uint8_t* so = s_out[v & 1u];
+#pragma unroll
+    for (uint32_t rt = 0; rt < NT; ++rt)
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j)
+        *reinterpret_cast<uint16_t*>(&so[(rt * 16u + g * 4u + j) * kOut + (wave * 16u + (lane & 15u)) * 2u]) =
+            kSplitF16 ? f16_bits(acc[rt][j]) : nk::bf16_rne(acc[rt][j]);
+    lds_barrier();
+#pragma unroll
+    for (uint32_t p = 0; p < 2u; ++p) {
+      const uint32_t idx = p * kThreads + tid, row = idx >> 4, c16 = idx & 15u;
+      const uint4 val = *reinterpret_cast<const uint4*>(&so[row * kOut + c16 * 16u]);
+      __builtin_amdgcn_raw_buffer_store_b128(nk::u32x4{val.x, val.y, val.z, val.w}, pr,
+                                             (int)(soff[p] + (live[p] ? extra : 0u)), (int)(nb * 256u), 0);
+    }
+  };
 
   auto run = [&](auto ntc) __attribute__((always_inline)) {
     constexpr uint32_t NT = decltype(ntc)::value;
@@ -474,7 +512,7 @@ __device__ __forceinline__ void down_rows(
         for (uint32_t rt = 0; rt < NT; ++rt)
           d[rt] = nk::mfma_e4m3_16x16x128(lds_fp8x32(&s_a[(rt * 16u + (lane & 15u)) * kStride + kb * 128u + g * 32u]),
                                           bq[kb]);
-        bq[kb] = nk::load_tile_operand(wt, ((nbn * 8u + wave) * KB + kb) * 2048u, lane);  // next group's tile
+        bq[kb] = nk::load_tile_operand<kAiter>(wt, ((nbn * 8u + wave) * KB + kb) * 2048u, lane);  // next group's tile
 #pragma unroll
         for (uint32_t rt = 0; rt < NT; ++rt) {
           const float4 h4 = *reinterpret_cast<const float4*>(&s_hs[kb * kRows + rt * 16u + g * 4u]);
@@ -489,23 +527,17 @@ __device__ __forceinline__ void down_rows(
         // first and holds all their results, which costs ~128 VGPRs.
 #pragma unroll
         for (uint32_t rt = 0; rt < NT; ++rt) asm volatile("" : "+v"(acc[rt]) : : "memory");
+        if constexpr (kSplitF16) {
+          if (kb == KB / 2u - 1u) {  // first split-K half complete
+            emit(ntc, acc, 2u * q, nb, 0u);
+#pragma unroll
+            for (uint32_t rt = 0; rt < NT; ++rt) acc[rt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+          }
+        }
       }
       wsv = wsn;
-      uint8_t* so = s_out[q & 1u];
-#pragma unroll
-      for (uint32_t rt = 0; rt < NT; ++rt)
-#pragma unroll
-        for (uint32_t j = 0; j < 4; ++j)
-          *reinterpret_cast<uint16_t*>(&so[(rt * 16u + g * 4u + j) * kOut + (wave * 16u + (lane & 15u)) * 2u]) =
-              nk::bf16_rne(acc[rt][j]);
-      lds_barrier();  // the group's tile is complete; the other buffer was read before the last barrier
-#pragma unroll
-      for (uint32_t p = 0; p < 2u; ++p) {
-        const uint32_t idx = p * kThreads + tid, row = idx >> 4, c16 = idx & 15u;
-        const uint4 v = *reinterpret_cast<const uint4*>(&so[row * kOut + c16 * 16u]);
-        __builtin_amdgcn_raw_buffer_store_b128(nk::u32x4{v.x, v.y, v.z, v.w}, pr, (int)soff[p],
-                                               (int)(nb * 256u), 0);
-      }
+      if constexpr (kSplitF16) emit(ntc, acc, 2u * q + 1u, nb, half_bytes);
+      else emit(ntc, acc, q, nb, 0u);
     }
   };
   switch (ntiles) {
@@ -567,3 +599,19 @@ NK_DOWN_TILE(1024)
   }
 NK_DOWN_ROWS(256)
 NK_DOWN_ROWS(512)
+
+// The M768 prefill bridge's producer format: W2 in the AITER layout, fp16
+// split-K2 route partials (half 1 starts half_rows rows after half 0).
+#define NK_DOWN_ROWS_AITER_F16X2(IV)                                                               \
+  NK_KERNEL __launch_bounds__(512)                                                                \
+  void netra_moe_down_rows_aiter_f16x2_i##IV##_gfx950(                                            \
+      const uint8_t* __restrict__ hq, const float* __restrict__ hs, const uint8_t* __restrict__ w2, \
+      const float* __restrict__ w2s, const int32_t* __restrict__ sorted_ids,                       \
+      const int32_t* __restrict__ sorted_expert, const int32_t* __restrict__ num_valid,            \
+      uint16_t* __restrict__ partial, uint32_t T, uint32_t H, uint32_t I, uint32_t Ktot,           \
+      uint32_t Etot, uint32_t NBC, uint32_t half_rows) {                                           \
+    (void)I;                                                                                       \
+    nktile::down_rows<IV / 128, true, true>(hq, hs, w2, w2s, sorted_ids, sorted_expert, num_valid, \
+                                            partial, T, H, Ktot, Etot, NBC, half_rows);            \
+  }
+NK_DOWN_ROWS_AITER_F16X2(512)

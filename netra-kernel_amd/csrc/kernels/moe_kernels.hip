@@ -7,7 +7,9 @@
 //   front end, screen: route_screen -> route_select -> sort_count -> sort_place
 //   then gate_up_{stream|lds|tile} -> down_{stream|tile} -> combine
 // Every kernel takes plain pointers followed by u32 shape constants, in the
-// order documented in include/netra_moe.h. Host code validates shapes before
+// order documented in include/netra_moe.h. moe_bridge_kernels.hip adds the
+// kernels behind the reference's per-operation bridge ABIs
+// (include/netra_qwen36_bridges.h). Host code validates shapes before
 // a launch; kernels also bound-check data-dependent indices (expert ids,
 // sorted positions) so malformed routing cannot address memory outside the
 // buffers the shapes describe.
@@ -17,3 +19,4 @@
 #include "moe_gemm_tile.hip"
 #include "moe_gemm_lds.hip"
 #include "moe_misc.hip"
+#include "moe_bridge_kernels.hip"

@@ -137,6 +137,34 @@ __device__ __forceinline__ v8i load_tile_operand(const uint8_t* tile, uint32_t l
   return r;
 }
 
+// The reference's weight layout ("aiter_shuffle_16x16_fp8_block128",
+// compiler/netra_compiler/layouts.py:90-106): [N, K] bytes stored as
+// [N/16][K/32][2][16][16], i.e. element (n, k) at
+// [n/16][k/32][(k%32)/16][n%16][k%16]. Like tile16x128 it keeps a 16-row
+// tile's K extent contiguous and one (16-row, 128-K) block in 2 KiB, so row
+// tiles and K blocks are addressed the same way (tile_base); only the place of
+// a lane's two 16-byte operand halves inside the block differs: the 32-K chunk
+// (l >> 4) is 512 bytes, its low K half of rows 0..15 first, then the high
+// half. Each half-operand wave load reads four 256-byte runs.
+template <bool kAiter>
+__host__ __device__ __forceinline__ uint32_t operand_lo(uint32_t lane) {
+  return kAiter ? lane * 16u + (lane >> 4) * 256u : lane * 16u;
+}
+template <bool kAiter>
+__host__ __device__ __forceinline__ uint32_t operand_hi(uint32_t lane) {
+  return kAiter ? lane * 16u + (lane >> 4) * 256u + 256u : 1024u + lane * 16u;
+}
+
+template <bool kAiter>
+__device__ __forceinline__ v8i load_block_operand(const uint8_t* tile, uint32_t lane) {
+  const uint4 lo = *reinterpret_cast<const uint4*>(tile + operand_lo<kAiter>(lane));
+  const uint4 hi = *reinterpret_cast<const uint4*>(tile + operand_hi<kAiter>(lane));
+  v8i r;
+  r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
+  r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
+  return r;
+}
+
 // The same operand through a raw buffer resource (SGPR base, per-lane offset
 // lane * 16 and a uniform scalar offset per tile): a run of tiles costs one
 // address VGPR instead of a 64-bit address per load. Loads past `bytes`
@@ -145,10 +173,11 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
+template <bool kAiter = false>
 __device__ __forceinline__ v8i load_tile_operand(__amdgpu_buffer_rsrc_t r, uint32_t tile_offset,
                                                  uint32_t lane) {
-  const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(lane * 16u), (int)tile_offset, 0);
-  const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(lane * 16u + 1024u), (int)tile_offset, 0);
+  const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(r, (int)operand_lo<kAiter>(lane), (int)tile_offset, 0);
+  const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(r, (int)operand_hi<kAiter>(lane), (int)tile_offset, 0);
   v8i v;
   v[0] = (int)lo.x; v[1] = (int)lo.y; v[2] = (int)lo.z; v[3] = (int)lo.w;
   v[4] = (int)hi.x; v[5] = (int)hi.y; v[6] = (int)hi.z; v[7] = (int)hi.w;

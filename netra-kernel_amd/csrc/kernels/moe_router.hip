@@ -27,7 +27,8 @@
 // column 0 also quantise their tokens from the staging registers: each 16-lane
 // group holds one 128-element block, scale = max(amax, 1e-10) * 0x3b124925,
 // q = e4m3(x * (1 / scale)). Every workgroup zeroes a slice of the routing
-// bitmask that topk fills later on the same stream.
+// bitmask that topk fills later on the same stream. With xq and mask null
+// (the router bridge) only the logits are written.
 template <uint32_t NJ>
 __device__ __forceinline__ void load_slice(uint4 (&v)[NJ], const uint16_t* p) {
 #pragma unroll
@@ -65,7 +66,7 @@ __device__ __forceinline__ void router(const uint16_t* __restrict__ x, const uin
   __shared__ float4 s_x[NT * H / 4];
   const uint32_t tid = threadIdx.x;
   const uint32_t wg = blockIdx.y * gridDim.x + blockIdx.x;
-  if (wg * 256u + tid < mask_words) mask[wg * 256u + tid] = 0ull;
+  if (mask != nullptr && wg * 256u + tid < mask_words) mask[wg * 256u + tid] = 0ull;
   const uint32_t t0 = blockIdx.y * NT;
   const uint32_t r = blockIdx.x * 16u + (tid >> 4);
   const uint32_t s = tid & 15u;
@@ -81,7 +82,7 @@ __device__ __forceinline__ void router(const uint16_t* __restrict__ x, const uin
     const uint32_t t = t0 + k < T ? t0 + k : T - 1u;  // missing tokens repeat a valid row
     sv[p] = *reinterpret_cast<const uint4*>(x + (size_t)t * H + (e - k * H));
   }
-  const bool quant = blockIdx.x == 0;
+  const bool quant = blockIdx.x == 0 && xq != nullptr;  // logits only when xq is null
 #pragma unroll
   for (uint32_t p = 0; p < kPasses; ++p) {
     const uint32_t e = (p * 256u + tid) * 8u;

@@ -20,5 +20,9 @@ def bridge_library() -> Path:
     return LIB_DIR / "libnetra_moe.so"
 
 
+def ops_bridge_library() -> Path:
+    return LIB_DIR / "libnetra_bridges.so"
+
+
 def header_paths() -> list[Path]:
     return sorted((REPO_ROOT / "include").glob("*.h"))

@@ -444,3 +444,69 @@ void orc_moe_tokens(const uint8_t* x_q, const float* x_s, const uint8_t* w13,
     free(hq); free(hs); free(scratch); free(part); free(acc);
   }
 }
+
+/* ---------------------------------------------------------------------- */
+/* Per-operation bridge contracts (runtime/gfx950/fp8/moe/
+ * qwen36_moe_silu_mul_quant_bridge.h:14-64). */
+
+void orc_stage1_routes(const uint8_t* x_q, const float* x_s, const uint8_t* w13,
+                       const float* w13_s, const int32_t* ids, int64_t T, int64_t Ktot,
+                       int64_t Etot, int64_t H, int64_t I, float* out, int threads) {
+  ensure_table();
+  (void)threads;
+  const int64_t kb = H / 128;
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(dynamic, 1)
+  for (int64_t r = 0; r < T * Ktot; ++r) {
+    const int64_t t = r / Ktot, e = ids[r];
+    float* o = out + r * 2 * I;
+    if (e < 0 || e >= Etot) {
+      memset(o, 0, sizeof(float) * (size_t)(2 * I));
+      continue;
+    }
+    const uint8_t* w13e = w13 + e * 2 * I * H;
+    const float* w13se = w13_s + e * (2 * I / 128) * kb;
+    for (int64_t n = 0; n < 2 * I; ++n)
+      o[n] = (float)fp8_row_dot(x_q + t * H, x_s + t * kb, w13e + n * H, w13se + (n / 128) * kb, H);
+  }
+}
+
+void orc_silu_mul_quant(const float* in, int64_t rows, int64_t I, uint8_t* q, float* s) {
+  float* h = (float*)malloc(sizeof(float) * (size_t)I);
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* g = in + r * 2 * I;
+    const float* u = g + I;
+    for (int64_t n = 0; n < I; ++n) h[n] = orc_f32_from_bf16(orc_bf16_from_f32(orc_silu(g[n]) * u[n]));
+    quant_row_f32(h, I, q + r * I, s + r * (I / 128));
+  }
+  free(h);
+}
+
+void orc_down_reduce_routes(const uint8_t* h_q, const float* h_s, const uint8_t* w2,
+                            const float* w2_s, const int32_t* ids, const float* weights,
+                            int64_t T, int64_t Ktot, int64_t Etot, int64_t H, int64_t I,
+                            float* out_f32, uint16_t* out, int threads) {
+  ensure_table();
+  (void)threads;
+#pragma omp parallel num_threads(threads > 0 ? threads : 1)
+  {
+    double* part = (double*)malloc(sizeof(double) * (size_t)H);
+    double* acc = (double*)malloc(sizeof(double) * (size_t)H);
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t t = 0; t < T; ++t) {
+      for (int64_t n = 0; n < H; ++n) acc[n] = 0.0;
+      for (int64_t s = 0; s < Ktot; ++s) {
+        const int64_t r = t * Ktot + s, e = ids[r];
+        if (e < 0 || e >= Etot) continue;
+        route_stage2(h_q + r * I, h_s + r * (I / 128), w2 + e * H * I,
+                     w2_s + e * (H / 128) * (I / 128), H, I, part);
+        for (int64_t n = 0; n < H; ++n) acc[n] += part[n] * (double)weights[r];
+      }
+      for (int64_t n = 0; n < H; ++n) {
+        if (out_f32) out_f32[t * H + n] = (float)acc[n];
+        out[t * H + n] = orc_bf16_from_f32((float)acc[n]);
+      }
+    }
+    free(part);
+    free(acc);
+  }
+}

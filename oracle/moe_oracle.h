@@ -83,6 +83,24 @@ void orc_moe_tokens(const uint8_t* x_q, const float* x_s, const uint8_t* w13,
                     int64_t n_tokens, int64_t H, int64_t I, int64_t Ktot,
                     float* out_f32, uint16_t* out, int threads);
 
+/* ---- per-operation bridge contracts ------------------------------------ */
+/* Stage 1 per route, before SiLU (export_qwen36_moe_stage1_capture.py:80-97):
+ * out f32 [T*Ktot, 2I], route r = t*Ktot + s with expert ids[r]; rows with an
+ * expert id outside [0, Etot) are zero. */
+void orc_stage1_routes(const uint8_t* x_q, const float* x_s, const uint8_t* w13,
+                       const float* w13_s, const int32_t* ids, int64_t T, int64_t Ktot,
+                       int64_t Etot, int64_t H, int64_t I, float* out, int threads);
+/* SiLU.mul + 1x128 quant of fp32 rows [g | u] (qwen36_moe_silu_mul_quant_fp8_gfx950.hip:41-94):
+ * q e4m3 [rows, I], s f32 [rows, I/128]. */
+void orc_silu_mul_quant(const float* in, int64_t rows, int64_t I, uint8_t* q, float* s);
+/* Down per route + slot-ordered weighted reduce per token
+ * (export_qwen36_moe_stage2_capture.py:90-110,151-155): h rows are route-major
+ * [T*Ktot, I]; out_f32 [T, H] (may be NULL), out bf16 [T, H]. */
+void orc_down_reduce_routes(const uint8_t* h_q, const float* h_s, const uint8_t* w2,
+                            const float* w2_s, const int32_t* ids, const float* weights,
+                            int64_t T, int64_t Ktot, int64_t Etot, int64_t H, int64_t I,
+                            float* out_f32, uint16_t* out, int threads);
+
 #ifdef __cplusplus
 }
 #endif

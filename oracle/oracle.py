@@ -48,6 +48,9 @@ def lib() -> ctypes.CDLL:
         L.orc_gate_up.argtypes = [P, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P, I]
         L.orc_down_combine.argtypes = [P, P, P, P, P, P, I64, P, I64, I64, I64, I64, I64, P, P, P, I]
         L.orc_moe_tokens.argtypes = [P, P, P, P, P, P, P, P, P, I64, I64, I64, I64, P, P, I]
+        L.orc_stage1_routes.argtypes = [P, P, P, P, P, I64, I64, I64, I64, I64, P, I]
+        L.orc_silu_mul_quant.argtypes = [P, I64, I64, P, P]
+        L.orc_down_reduce_routes.argtypes = [P, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, I]
         _lib = L
     return _lib
 
@@ -217,6 +220,75 @@ def moe_layer(x_bf16, router_w, bias, w13, w13_s, w2, w2_s, E, K, S, I, threads:
     return dict(logits=logits, topk_ids=ids, topk_weights=wts, x_q=x_q, x_scale=x_s,
                 sorted_ids=sid, sorted_expert=sexp, num_valid=nv, expert_counts=counts,
                 h_q=h_q, h_scale=h_s, h_bf16=h_b, partial=partial, out_f32=out_f, out=out)
+
+
+def stage1_routes(x_q, x_s, w13, w13_s, ids, Etot: int, I: int, threads: int | None = None) -> np.ndarray:
+    """Per-route gate/up before SiLU: f32 [T*Ktot, 2I] (route r = t*Ktot + s)."""
+    T, Ktot = ids.shape
+    H = x_q.shape[1]
+    out = np.empty((T * Ktot, 2 * I), np.float32)
+    arrs = [np.ascontiguousarray(a) for a in (x_q, x_s, w13, w13_s)]
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    lib().orc_stage1_routes(*[_p(a) for a in arrs], _p(ids), T, Ktot, Etot, H, I, _p(out),
+                            threads or default_threads())
+    return out
+
+
+def silu_mul_quant(gu: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """fp32 rows [g | u] [rows, 2I] -> (h e4m3 [rows, I], scales f32 [rows, I/128])."""
+    gu = np.ascontiguousarray(gu, dtype=np.float32)
+    rows, I = gu.shape[0], gu.shape[1] // 2
+    q = np.empty((rows, I), np.uint8)
+    s = np.empty((rows, I // 128), np.float32)
+    lib().orc_silu_mul_quant(_p(gu), rows, I, _p(q), _p(s))
+    return q, s
+
+
+def down_reduce_routes(h_q, h_s, w2, w2_s, ids, weights, Etot: int, threads: int | None = None):
+    """Per-route down + slot-ordered reduce per token: (out f32 [T, H], out bf16 bits [T, H])."""
+    T, Ktot = ids.shape
+    H, I = w2.shape[1], w2.shape[2]
+    out_f = np.empty((T, H), np.float32)
+    out = np.empty((T, H), np.uint16)
+    arrs = [np.ascontiguousarray(a) for a in (h_q, h_s, w2, w2_s)]
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    wts = np.ascontiguousarray(weights, dtype=np.float32)
+    lib().orc_down_reduce_routes(*[_p(a) for a in arrs], _p(ids), _p(wts), T, Ktot, Etot, H, I,
+                                 _p(out_f), _p(out), threads or default_threads())
+    return out_f, out
+
+
+def shared_gate_append(x_bf16, wsg_bf16, ids, weights, E: int):
+    """Shared-expert append (export_qwen36_shared_gate_append_capture.py:97-107,134-139):
+    slots 0..K-1 copy the routed ids/weights, slot K = (E, f32(bf16(sigmoid(logit)))) with
+    the logit in the router contract order."""
+    T, K = ids.shape
+    logit = router_logits(x_bf16, np.ascontiguousarray(wsg_bf16).reshape(1, -1))[:, 0]
+    gate = np.array([lib().orc_f32_from_bf16(lib().orc_bf16_from_f32(
+        lib().orc_sigmoid(lib().orc_f32_from_bf16(int(b))))) for b in logit], dtype=np.float32)
+    out_ids = np.concatenate([ids.astype(np.int32), np.full((T, 1), E, np.int32)], axis=1)
+    out_w = np.concatenate([weights.astype(np.float32), gate[:, None]], axis=1)
+    return out_ids, out_w
+
+
+def stage2_split_halves(h_q, h_s, w2, w2_s, experts) -> tuple[np.ndarray, np.ndarray]:
+    """Split-K2 down partials per route row (the format of the reference's
+    prefill producer, moe_prefill_m768_bridge.hip:144-147): half j sums the
+    K blocks [j I/256, (j+1) I/256) of sum_kb ((h8 . w8) * h_s) * w_s, in
+    float64. h rows [R, I] with their experts [R]; returns two [R, H] arrays."""
+    table = e4m3_table().astype(np.float64)
+    R, I = h_q.shape
+    KB = I // 128
+    out = [np.zeros((R, w2.shape[1])), np.zeros((R, w2.shape[1]))]
+    for r in range(R):
+        e = int(experts[r])
+        h = table[h_q[r]].reshape(KB, 128)
+        w = table[w2[e]].reshape(-1, KB, 128)
+        ws = np.repeat(w2_s[e].astype(np.float64), 128, axis=0)  # [H, KB]
+        dots = np.einsum("nkc,kc->nk", w, h) * h_s[r].astype(np.float64)[None, :] * ws
+        out[0][r] = dots[:, : KB // 2].sum(axis=1)
+        out[1][r] = dots[:, KB // 2:].sum(axis=1)
+    return out[0], out[1]
 
 
 def max_abs_rel(y: np.ndarray, ref: np.ndarray) -> float:

@@ -34,9 +34,13 @@ def test_headers_declare_the_reference_engine_abi():
     assert set(names) == set(runtime.ENGINE_SYMBOLS)
 
 
-@pytest.mark.parametrize("header,lib", [("netra_engine.h", "engine"), ("netra_moe.h", "bridge")])
+LIBRARIES = {"engine": paths.engine_library, "bridge": paths.bridge_library, "ops": paths.ops_bridge_library}
+
+
+@pytest.mark.parametrize("header,lib", [("netra_engine.h", "engine"), ("netra_moe.h", "bridge"),
+                                        ("netra_qwen36_bridges.h", "ops")])
 def test_libraries_load_and_export_every_declared_symbol(header, lib):
-    path = paths.engine_library() if lib == "engine" else paths.bridge_library()
+    path = LIBRARIES[lib]()
     dll = ctypes.CDLL(str(path))
     for name in declared(REPO / "include" / header):
         assert hasattr(dll, name), f"{path.name} does not export {name}"
@@ -195,3 +199,15 @@ def test_engine_create_without_a_gpu_reports_a_status():
     with pytest.raises(nm.NetraError) as err:
         nm.Engine(d)
     assert err.value.status in (nm.Status.HIP, nm.Status.UNSUPPORTED_TARGET)
+
+
+def test_op_bridges_declare_the_reference_bridge_abis():
+    """Every load/launch/unload/last_error entry point of the reference's four
+    bridge headers (runtime/gfx950/fp8/moe/qwen36_moe_silu_mul_quant_bridge.h:14-64,
+    moe_prefill_m768_bridge.h:10-23, routing/verify/qwen36_router_bf16_bridge.h:10-21,
+    routing/decode/qwen36_shared_gate_append_bridge.h:10-24) is declared, and the
+    ctypes binding covers exactly those."""
+    from netra_moe import bridges
+    names = declared(REPO / "include" / "netra_qwen36_bridges.h")
+    assert sorted(names) == sorted(bridges.BRIDGE_SYMBOLS)
+    assert len(names) == 24

@@ -38,6 +38,11 @@ EXTRA_CONFIGS = {
     "shape_h1024_i1024": MoEConfig("shape_h1024_i1024", T=40, H=1024, E=24, K=3, I=1024, S=1, seed=1102),
     "shape_hot_experts": MoEConfig("shape_hot_experts", T=300, H=1024, E=64, K=4, I=256, S=1,
                                    router_bias="hot", seed=1103),
+    # the reference's only instantiated prefill shape: 64 requests x 12 draft
+    # tokens = 768 tokens, 6912 routes, capacity 365 blocks
+    # (manifests/gfx950/models/qwen36-35b-c64-fp8.json:43-49)
+    "verify_t768": MoEConfig("verify_t768", T=768, H=2048, E=256, K=8, I=512, S=1, seed=1105,
+                             notes="64 requests x 12 draft tokens"),
     # more than 256 experts: the 512-expert route_select / top-k / sort variants
     "shape_e384": MoEConfig("shape_e384", T=96, H=1024, E=384, K=6, I=256, S=1,
                             router_bias="zipf1.1", seed=1104),

@@ -81,15 +81,23 @@ int ok(Family& f) {
 
 bool loaded(const Family& f) { return !f.functions.empty() && f.functions.back() != nullptr; }
 
-void release(Family& f) {
-  if (f.scratch) (void)hipFree(f.scratch);
+// Frees the scratch and unloads each distinct module once (both paths may
+// name one module); returns the first HIP error.
+hipError_t release(Family& f) {
+  hipError_t first = hipSuccess;
+  if (f.scratch) first = hipFree(f.scratch);
   f.scratch = nullptr;
+  const hipModule_t shared = f.modules[1] == f.modules[0] ? f.modules[0] : nullptr;
   for (int m = 0; m < 2; ++m) {
-    if (f.modules[m] && (m == 0 || f.modules[m] != f.modules[0])) (void)hipModuleUnload(f.modules[m]);
+    if (f.modules[m] && !(m == 1 && f.modules[1] == shared)) {
+      const hipError_t err = hipModuleUnload(f.modules[m]);
+      if (first == hipSuccess) first = err;
+    }
     f.modules[m] = nullptr;
     f.paths[m].clear();
   }
   f.functions.clear();
+  return first;
 }
 
 // Loads the family's code object(s); paths[1] may repeat paths[0] (one module).
@@ -119,7 +127,7 @@ int load(Family& f, const char* path0, const char* path1) {
       err = hipModuleLoad(&f.modules[m], paths[m]);
       if (err != hipSuccess) {
         f.modules[m] = nullptr;
-        release(f);
+        (void)release(f);
         return hip_error(f, "hipModuleLoad", err);
       }
     }
@@ -129,7 +137,7 @@ int load(Family& f, const char* path0, const char* path1) {
   for (size_t i = 0; i < f.symbols.size(); ++i) {
     err = hipModuleGetFunction(&functions[i], f.modules[f.module_of[i]], f.symbols[i]);
     if (err != hipSuccess) {
-      release(f);
+      (void)release(f);
       return hip_error(f, "hipModuleGetFunction", err);
     }
   }
@@ -137,7 +145,7 @@ int load(Family& f, const char* path0, const char* path1) {
     err = hipMalloc(&f.scratch, f.scratch_bytes);
     if (err != hipSuccess) {
       f.scratch = nullptr;
-      release(f);
+      (void)release(f);
       return hip_error(f, "hipMalloc(scratch)", err);
     }
   }
@@ -147,8 +155,8 @@ int load(Family& f, const char* path0, const char* path1) {
 
 int unload(Family& f) {
   std::lock_guard<std::mutex> lock(f.mutex);
-  release(f);
-  return ok(f);
+  const hipError_t err = release(f);
+  return err == hipSuccess ? ok(f) : hip_error(f, "hipModuleUnload", err);
 }
 
 int dispatch(Family& f, size_t kernel, dim3 grid, dim3 block, void** args, hipStream_t stream) {

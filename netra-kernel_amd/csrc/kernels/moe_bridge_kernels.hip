@@ -249,6 +249,8 @@ __device__ __forceinline__ void down_reduce_route(const uint8_t* __restrict__ hq
   }
 }
 
+}  // namespace nkbridge
+
 // ---------------------------------------------------------------------------
 // Block pairs of an AITER-sorted routing (the format of entry_routing.inc:
 // 27-112: 64-row blocks, an expert's blocks consecutive, sorted_expert_ids per
@@ -326,8 +328,6 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_route_reduce_f16x2_gfx950(
   o.w = (uint32_t)nk::bf16_rne(acc[6]) | ((uint32_t)nk::bf16_rne(acc[7]) << 16);
   *reinterpret_cast<uint4*>(out + (size_t)t * H + n) = o;
 }
-
-}  // namespace nkbridge
 
 #define NK_SHARED_GATE_APPEND(HV)                                                                  \
   NK_KERNEL __launch_bounds__(64) void netra_moe_shared_gate_append_h##HV##_gfx950(                \

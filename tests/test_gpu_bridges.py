@@ -19,77 +19,32 @@ the oracle's h on some elements, and a single route row has no slot average
 to smooth that out; a swapped half, a wrong K range or a misplaced route row
 shows as an error of order 1.)
 """
-import ctypes
-
 import numpy as np
 import pytest
 import torch
 
 import oracle
+from bridge_case import (DEV, E, ETOT, H, I, K, KTOT, M768, build_model, capacity, half_rows, prefill_args,
+                         prefill_buffers, prefill_inputs, ptr, routing, stream, tokens)
 from conftest import gpu_available
 from moe_case import bf16_bits
 from netra_moe import bridges as B
-from netra_moe import weights as W
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a GPU")]
 
-DEV = torch.device("cuda", 0)
-H, E, K, I = 2048, 256, 8, 512
-ETOT, KTOT = E + 1, K + 1
 TOL = 2e-2
-SEED = 2024
-
-
-def ptr(t: torch.Tensor) -> ctypes.c_void_p:
-    return ctypes.c_void_p(t.data_ptr())
-
-
-def stream() -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream)
-
-
-def aiter(q: torch.Tensor) -> torch.Tensor:
-    """Row-major e4m3 bytes [G, N, K] -> the AITER 16x16 shuffle [N/16][K/32][2][16][16] per group."""
-    g, n, k = q.shape
-    return q.view(g, n // 16, 16, k // 32, 2, 16).permute(0, 1, 3, 4, 2, 5).contiguous().view(g, n, k)
 
 
 @pytest.fixture(scope="module")
 def model():
     print(f"\n[bridges] building weights H={H} E={ETOT} I={I}", flush=True)
-    gen = torch.Generator().manual_seed(SEED)
-    router = (torch.randn((E + 1, H), generator=gen) * 0.02).to(torch.bfloat16)
-    w13f, w2f = W.synthetic_expert_weights_f32(
-        type("C", (), {"Etot": ETOT, "I": I, "H": H})(), SEED, DEV)
-    q13, s13 = W.quantize_blocks(w13f)
-    q2, s2 = W.quantize_blocks(w2f)
-    del w13f, w2f
-    torch.cuda.synchronize()
-    m = {
-        "router_w": router[:E].contiguous().to(DEV), "shared_w": router[E:].contiguous().to(DEV),
-        "w13": aiter(q13), "w13_scale": s13, "w2": aiter(q2), "w2_scale": s2,
-        "host": {"router": bf16_bits(router), "w13": q13.cpu().numpy(), "w13_scale": s13.cpu().numpy(),
-                 "w2": q2.cpu().numpy(), "w2_scale": s2.cpu().numpy()},
-    }
+    m = build_model()
     for fam in B.FAMILIES:
         B.check(fam, B.load(fam))
     yield m
     torch.cuda.synchronize()
     for fam in B.FAMILIES:
         B.check(fam, B.unload(fam))
-
-
-def tokens(rows: int, seed: int):
-    g = torch.Generator().manual_seed(seed)
-    x = torch.randn((rows, H), generator=g).to(torch.bfloat16)
-    return x, bf16_bits(x)
-
-
-def routing(m, xb):
-    """Oracle routing of the tokens: logits, top-8 + shared ids / weights."""
-    logits = oracle.router_logits(xb, m["host"]["router"])
-    ids, wts = oracle.topk(logits, None, E, K, 1)
-    return logits, ids, wts
 
 
 @pytest.mark.parametrize("rows", [1, 16])
@@ -226,38 +181,20 @@ def test_decode_chain_through_the_bridges(model):
     assert err <= TOL
 
 
-M768 = 768
-CAP = (M768 * KTOT + 63) // 64 + ETOT      # 365 blocks
-HALF = M768 * KTOT + CAP                  # 7277 rows between the split-K2 halves
+CAP = capacity(M768)      # 365 blocks
+HALF = half_rows(M768)    # 7277 rows between the split-K2 halves
 
 
-def prefill_inputs(model, seed=70):
-    x, xb = tokens(M768, seed)
-    _, ids, wts = routing(model, xb)
-    x_q, x_s = oracle.quant_rows_bf16(xb)
-    sid, sexp, nv, _ = oracle.sort(ids, ETOT, CAP)
-    return xb, x_q, x_s, ids, wts, sid, sexp, nv
-
-
-def run_m768(model, inp, launch=None):
-    xb, x_q, x_s, ids, wts, sid, sexp, nv = inp
-    d = {k: torch.from_numpy(np.ascontiguousarray(v)).to(DEV) for k, v in
-         dict(x_q=x_q, x_s=x_s, sid=sid, sexp=sexp, nv=nv[:1], wts=wts).items()}
-    d["sorted_w"] = torch.zeros(sid.size, dtype=torch.float32, device=DEV)  # unused by the producer
-    rs = torch.full((CAP * 64, I // 128), -1.0, dtype=torch.float32, device=DEV)
-    parts = torch.zeros((2, HALF, H), dtype=torch.float16, device=DEV)
-    out = torch.empty((M768, H), dtype=torch.bfloat16, device=DEV)
-    args = (ptr(d["x_q"]), ptr(d["x_s"]), ptr(model["w13"]), ptr(model["w13_scale"]), ptr(model["w2"]),
-            ptr(model["w2_scale"]), ptr(d["sid"]), ptr(d["sorted_w"]), ptr(d["sexp"]), ptr(d["nv"]),
-            ptr(d["wts"]), ptr(rs), ptr(parts), ptr(out))
-    rc = (launch or (lambda *a: B.launch("netra_moe_prefill_m768", *a)))(*args, stream())
+def run_m768(model, inp):
+    d = prefill_buffers(inp)
+    rc = B.launch("netra_moe_prefill_m768", *prefill_args(model, d), stream())
     torch.cuda.synchronize()
-    return rc, out, rs, parts
+    return rc, d["out"], d["rs"], d["parts"]
 
 
 def test_prefill_m768_bridge(model):
-    inp = prefill_inputs(model)
-    xb, x_q, x_s, ids, wts, sid, sexp, nv = inp
+    inp = prefill_inputs(model, tokens(M768, 70)[1])
+    x_q, x_s, ids, wts, sid, sexp, nv = (inp[k] for k in ("x_q", "x_s", "ids", "wts", "sid", "sexp", "nv"))
     print(f"[bridges] m768: {int(nv[0])} sorted rows of {CAP * 64}", flush=True)
     rc, out, rs, parts = run_m768(model, inp)
     B.check("netra_moe_prefill_m768", rc)
@@ -317,3 +254,11 @@ def test_bridge_refusals(model):
     assert "not loaded" in B.last_error(fam)
     assert B.load(fam) == 0
     assert B.last_error(fam) == ""
+    # the prefill pair loads one module when both paths name the same code
+    # object; unloading it releases that module once and leaves no HIP error
+    # behind for the caller's next call
+    pre = "netra_moe_prefill_m768"
+    assert B.unload(pre) == 0, B.last_error(pre)
+    torch.cuda.synchronize()
+    assert float(torch.ones(4, device=DEV).sum()) == 4.0
+    assert B.load(pre) == 0, B.last_error(pre)

@@ -141,6 +141,24 @@ int netra_moe_e4m3_check(const float* in, uint8_t* sw, uint8_t* hw, uint32_t n,
 // achievable copy bandwidth.
 int netra_moe_copy(const void* src, void* dst, uint64_t bytes, hipStream_t stream);
 
+// Allocation-free prefill producer/reducer. No counterpart in the reference:
+// it is for callers that cannot allocate device memory (code under HIP stream
+// capture, tight serving loops, harnesses that forbid hipMalloc). It computes
+// what netra_moe_prefill_m768_launch (include/netra_qwen36_bridges.h)
+// computes, with the same arguments and formats, for `rows` tokens in
+// 1..768 (capacity ceil(rows * 9 / 64) + 257 sorted blocks; partials_f16 is
+// [2, rows * 9 + capacity, 2048]; route_scale_workspace_f32 [capacity * 64,
+// 4]; output_bf16 [rows, 2048]), needs no load call, and allocates nothing:
+// its 11.7 MiB of scratch is a static device array of this library, resolved
+// once per device. Calls that overlap on one GPU share that array and race.
+// rows outside 1..768 are refused (-1). Same error convention as above.
+int netra_moe_prefill_launch_noalloc(const void* hidden_fp8, const float* hidden_scale_f32, const void* w13_fp8,
+                                     const float* w13_scale_f32, const void* w2_fp8, const float* w2_scale_f32,
+                                     const int32_t* sorted_token_ids_i32, const float* sorted_weights_f32,
+                                     const int32_t* sorted_expert_ids_i32, const int32_t* num_valid_ids_i32,
+                                     const float* topk_weights_f32, float* route_scale_workspace_f32,
+                                     void* partials_f16, void* output_bf16, uint32_t rows, hipStream_t stream);
+
 const char* netra_moe_last_error(void);
 
 #ifdef __cplusplus

@@ -42,6 +42,8 @@ def bridge_library() -> ctypes.CDLL:
         lib.netra_moe_e4m3_check.restype = ctypes.c_int
         lib.netra_moe_copy.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_uint64, ctypes.c_void_p]
         lib.netra_moe_copy.restype = ctypes.c_int
+        lib.netra_moe_prefill_launch_noalloc.argtypes = [ctypes.c_void_p] * 14 + [ctypes.c_uint32, ctypes.c_void_p]
+        lib.netra_moe_prefill_launch_noalloc.restype = ctypes.c_int
         lib.netra_moe_last_error.argtypes = []
         lib.netra_moe_last_error.restype = ctypes.c_char_p
         _bridge = lib

@@ -236,9 +236,13 @@ extern "C" netra_status_t netra_engine_create(const char* directory,
     return NETRA_STATUS_MANIFEST;
   }
 
+  // The workspace starts zeroed (kernels that hand work between workgroups
+  // keep counters there that every launch leaves at zero again).
   e->workspace_bytes = manifest.workspace_bytes;
   if (e->workspace_bytes) {
     err = hipMalloc(&e->workspace, static_cast<size_t>(e->workspace_bytes));
+    if (err == hipSuccess) err = hipMemset(e->workspace, 0, static_cast<size_t>(e->workspace_bytes));
+    if (err == hipSuccess) err = hipDeviceSynchronize();
     if (err != hipSuccess) { release(e); delete e; return NETRA_STATUS_HIP; }
   }
 

@@ -16,6 +16,7 @@
 #include "moe_router.hip"
 #include "moe_route_prefill.hip"
 #include "moe_gemm_stream.hip"
+#include "moe_ffn_decode.hip"
 #include "moe_gemm_tile.hip"
 #include "moe_gemm_lds.hip"
 #include "moe_misc.hip"

@@ -55,7 +55,10 @@ __device__ __forceinline__ void quant8(const float (&f)[8], uint8_t* __restrict_
   if (first_lane) *s_dst = scale;
 }
 
-template <uint32_t NJ, uint32_t NT>  // NJ = H / 128, NT tokens per workgroup
+// kCoherent: logits are stored at agent scope (write-through, sc1), so a
+// workgroup of the same launch on another XCD can read them once this
+// workgroup's stores have completed (the route kernel's top-k hand-off).
+template <uint32_t NJ, uint32_t NT, bool kCoherent = false>  // NJ = H / 128, NT tokens per workgroup
 __device__ __forceinline__ void router(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                        uint16_t* __restrict__ logits, uint8_t* __restrict__ xq,
                                        float* __restrict__ xs, unsigned long long* __restrict__ mask,
@@ -132,7 +135,11 @@ __device__ __forceinline__ void router(const uint16_t* __restrict__ x, const uin
     a = a + __shfl_down(a, 4u, 16);
     a = a + __shfl_down(a, 2u, 16);
     a = a + __shfl_down(a, 1u, 16);
-    if (s == 0 && row_ok && t0 + k < T) logits[(size_t)(t0 + k) * rows + r] = nk::bf16_rne(a);
+    if (s == 0 && row_ok && t0 + k < T) {
+      uint16_t* dst = logits + (size_t)(t0 + k) * rows + r;
+      if constexpr (kCoherent) __hip_atomic_store(dst, nk::bf16_rne(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else *dst = nk::bf16_rne(a);
+    }
   }
 }
 
@@ -146,6 +153,20 @@ __device__ __forceinline__ void router(const uint16_t* __restrict__ x, const uin
     (void)H;                                                                                   \
     router<HV / 128, NT>(x, w, logits, xq, xs, mask, T, rows, mask_words);                     \
   }
+// Logits and the input quant only (no bitmask): the router in front of the
+// fused decode FFN, which runs top-k and the sort itself.
+#define NK_ROUTER_LOGITS(HV, NT)                                                                   \
+  NK_KERNEL __launch_bounds__(256) void netra_moe_router_logits_h##HV##_t##NT##_gfx950(              \
+      const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, uint16_t* __restrict__ logits, \
+      uint8_t* __restrict__ xq, float* __restrict__ xs, uint32_t T, uint32_t H, uint32_t rows) {     \
+    (void)H;                                                                                       \
+    router<HV / 128, NT>(x, w, logits, xq, xs, nullptr, T, rows, 0u);                              \
+  }
+NK_ROUTER_LOGITS(512, 4)
+NK_ROUTER_LOGITS(1024, 2)
+NK_ROUTER_LOGITS(2048, 1)
+NK_ROUTER_LOGITS(4096, 2)
+
 // Symbol netra_moe_router_h<H>_t<NT>_gfx950: NT tokens per workgroup (for
 // small T the fewest the staging allows, NT * H a multiple of 2048: each
 // wave's fmaf chains run fewer tokens and more workgroups share the weight
@@ -174,7 +195,15 @@ NK_ROUTER(4096, 2)
 // expert (id E) is appended at slot K with weight
 // f32(bf16(sigmoid(f32(logit_E)))). Each (token, expert) pair sets bit t % 64
 // of mask[e][t / 64]; the sort ranks tokens inside an expert from these bits.
-template <uint32_t P>  // experts per lane, P * 64 >= E
+// A logit as fp32; kCoherent reads at agent scope (the logits of the same
+// launch, written by other workgroups with agent-scope stores).
+template <bool kCoherent>
+__device__ __forceinline__ float logit_f32(const uint16_t* p) {
+  if constexpr (kCoherent) return nk::bf16_f32(__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  else return nk::bf16_f32(*p);
+}
+
+template <uint32_t P, bool kCoherent = false>  // experts per lane, P * 64 >= E
 __device__ __forceinline__ void topk_token(const uint16_t* __restrict__ lrow, const float* __restrict__ bias,
                                            int32_t* __restrict__ ids, float* __restrict__ weights,
                                            unsigned long long* __restrict__ mask, uint32_t t, uint32_t E,
@@ -184,7 +213,7 @@ __device__ __forceinline__ void topk_token(const uint16_t* __restrict__ lrow, co
 #pragma unroll
   for (uint32_t j = 0; j < P; ++j) {
     const uint32_t e = lane + 64u * j;
-    code[j] = e < E ? nk::order_bits(nk::bf16_f32(lrow[e]) + bias[e]) : 0u;
+    code[j] = e < E ? nk::order_bits(logit_f32<kCoherent>(lrow + e) + bias[e]) : 0u;
   }
   uint32_t my_id = 0, my_code = 0;
   for (uint32_t r = 0; r < K; ++r) {
@@ -221,9 +250,9 @@ __device__ __forceinline__ void topk_token(const uint16_t* __restrict__ lrow, co
   if (S != 0 && lane == K) {
     my_id = E;
     ids[(size_t)t * Ktot + K] = (int32_t)E;
-    weights[(size_t)t * Ktot + K] = nk::bf16_f32(nk::bf16_rne(nk::sigmoid(nk::bf16_f32(lrow[E]))));
+    weights[(size_t)t * Ktot + K] = nk::bf16_f32(nk::bf16_rne(nk::sigmoid(logit_f32<kCoherent>(lrow + E))));
   }
-  if (lane < Ktot) atomicOr(&mask[(size_t)my_id * W + (t >> 6)], 1ull << (t & 63u));
+  if (mask != nullptr && lane < Ktot) atomicOr(&mask[(size_t)my_id * W + (t >> 6)], 1ull << (t & 63u));
 }
 
 NK_KERNEL __launch_bounds__(256) void netra_moe_topk_gfx950(
@@ -240,6 +269,64 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_topk_gfx950(
   else if (E <= 256u) topk_token<4>(lrow, bias, ids, weights, mask, t, E, K, S, W, lane);
   else topk_token<8>(lrow, bias, ids, weights, mask, t, E, K, S, W, lane);
 }
+
+// ---------------------------------------------------------------------------
+// Router + top-k in one launch (the exact front end): the router above, with
+// the logits stored at agent scope; the last of the gridDim.x row-group
+// workgroups of a token group to finish runs top-k for those NT tokens (one
+// wave each, the top-k below). Workgroups of a token group count their
+// arrivals on counters[kCounterStride * blockIdx.y] (an atomic per workgroup,
+// after its logit stores have completed; one counter per 256-byte line, as
+// atomics on one line serialise); the last arriver reads the logits at agent
+// scope and puts the counter back to zero for the next launch (counters start
+// at zero: the engine zeroes its workspace when it is created). No workgroup
+// waits on another, so the launch cannot deadlock whatever the residency.
+constexpr uint32_t kCounterStride = 64;  // u32 words between hand-off counters
+template <uint32_t NJ, uint32_t NT>
+__device__ __forceinline__ void route(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                      const float* __restrict__ bias, uint16_t* __restrict__ logits,
+                                      uint8_t* __restrict__ xq, float* __restrict__ xs, int32_t* __restrict__ ids,
+                                      float* __restrict__ weights, uint32_t* __restrict__ counters, uint32_t T,
+                                      uint32_t rows, uint32_t E, uint32_t K, uint32_t S) {
+  static_assert(NT <= 4, "one top-k wave per token of the group");
+  __shared__ uint32_t s_arrival;
+  router<NJ, NT, true>(x, w, logits, xq, xs, nullptr, T, rows, 0u);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this workgroup's logit stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_arrival = __hip_atomic_fetch_add(&counters[kCounterStride * blockIdx.y], 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (s_arrival != gridDim.x - 1u) return;
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+  const uint32_t t = blockIdx.y * NT + wave;
+  if (wave < NT && t < T && E <= 512u && K <= E && K + S <= 64u) {  // wave-uniform
+    const uint16_t* lrow = logits + (size_t)t * rows;
+    if (E <= 64u) topk_token<1, true>(lrow, bias, ids, weights, nullptr, t, E, K, S, 0u, lane);
+    else if (E <= 128u) topk_token<2, true>(lrow, bias, ids, weights, nullptr, t, E, K, S, 0u, lane);
+    else if (E <= 256u) topk_token<4, true>(lrow, bias, ids, weights, nullptr, t, E, K, S, 0u, lane);
+    else topk_token<8, true>(lrow, bias, ids, weights, nullptr, t, E, K, S, 0u, lane);
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(&counters[kCounterStride * blockIdx.y], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+#define NK_ROUTE(HV, NT)                                                                          \
+  NK_KERNEL __launch_bounds__(256) void netra_moe_route_h##HV##_t##NT##_gfx950(                     \
+      const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias, \
+      uint16_t* __restrict__ logits, uint8_t* __restrict__ xq, float* __restrict__ xs,            \
+      int32_t* __restrict__ ids, float* __restrict__ weights, uint32_t* __restrict__ counters,     \
+      uint32_t T, uint32_t H, uint32_t rows, uint32_t E, uint32_t K, uint32_t S) {                 \
+    (void)H;                                                                                      \
+    route<HV / 128, NT>(x, w, bias, logits, xq, xs, ids, weights, counters, T, rows, E, K, S);     \
+  }
+// Symbol netra_moe_route_h<H>_t<NT>_gfx950: the tokens-per-workgroup choices of the router.
+NK_ROUTE(512, 4)
+NK_ROUTE(1024, 2)
+NK_ROUTE(1024, 4)
+NK_ROUTE(2048, 1)
+NK_ROUTE(2048, 4)
+NK_ROUTE(4096, 2)
 
 // ---------------------------------------------------------------------------
 // Count / scan / pad / scatter into 64-row expert blocks (a4: AITER
@@ -273,7 +360,7 @@ __host__ __device__ constexpr bool sort_mask_in_lds(uint32_t Etot, uint32_t W, u
 }
 
 NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_gfx950(
-    const int32_t* __restrict__ ids, const unsigned long long* __restrict__ mask,
+    const int32_t* __restrict__ ids, unsigned long long* __restrict__ mask,
     int32_t* __restrict__ sorted_ids, int32_t* __restrict__ sorted_expert,
     int32_t* __restrict__ tile_map, int32_t* __restrict__ pair_map, int32_t* __restrict__ num_valid,
     int32_t* __restrict__ counts, uint32_t T, uint32_t Ktot, uint32_t Etot, uint32_t W,
@@ -299,11 +386,35 @@ NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_gfx950(
     const uint32_t r = tid + 1024u * i;
     pre[i] = r < routes ? ids[r] : -1;
   }
+  // The routing bitmask (bit t % 64 of word [e][t / 64]: token t routes to
+  // expert e), built here from the ids: in LDS when it fits, else in the
+  // global workspace, whose words are then written and read at agent scope
+  // (so no stale L1 copy is read back).
+  for (uint32_t i = tid; i < Etot * W; i += 1024u) {
+    if (mlds) mcopy[i] = 0ull;
+    else __hip_atomic_store(&mask[i], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  auto mark = [&](uint32_t r, int32_t eid) {
+    const uint32_t e = (uint32_t)eid, t = r / Ktot;
+    if (e >= Etot) return;
+    const unsigned long long bit = 1ull << (t & 63u);
+    if (mlds) atomicOr(&mcopy[e * W + (t >> 6)], bit);
+    else __hip_atomic_fetch_or(&mask[(size_t)e * W + (t >> 6)], bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+#pragma unroll
+  for (uint32_t i = 0; i < kSortPrefetch; ++i)
+    if (tid + 1024u * i < routes) mark(tid + 1024u * i, pre[i]);
+  for (uint32_t r = tid + 1024u * kSortPrefetch; r < routes; r += 1024u) mark(r, ids[r]);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  auto mword = [&](uint32_t i) -> unsigned long long {
+    return mlds ? mcopy[i] : __hip_atomic_load(&mask[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
   uint32_t run = 0;
   if (tid < Etot) {
     for (uint32_t w = 0; w < W; ++w) {
-      const unsigned long long m = mask[(size_t)tid * W + w];
-      if (mlds) mcopy[tid * W + w] = m;
+      const unsigned long long m = mword(tid * W + w);
       prefix[tid * W + w] = run;
       run += (uint32_t)__popcll(m);
     }
@@ -368,7 +479,7 @@ NK_KERNEL __launch_bounds__(1024) void netra_moe_sort_gfx950(
     if (e >= Etot) return;
     const uint32_t t = r / Ktot, s = r - t * Ktot;
     const uint32_t w = t >> 6, bit = t & 63u;
-    const unsigned long long word = mlds ? mcopy[e * W + w] : mask[(size_t)e * W + w];
+    const unsigned long long word = mword(e * W + w);
     const uint32_t pos = block_off[e] * 64u + prefix[e * W + w] +
                          (uint32_t)__popcll(word & ((1ull << bit) - 1ull));
     if (pos < cap_blocks * 64u) sorted_ids[pos] = (int32_t)((s << 24) | t);

@@ -30,7 +30,7 @@ from .contracts import HipKernelContract, Launch, canonical_json
 from .profiles import profile_for
 from . import paths
 
-DTYPE_BYTES = {"bf16": 2, "f32": 4, "e4m3": 1, "i32": 4, "u64": 8}
+DTYPE_BYTES = {"bf16": 2, "f32": 4, "e4m3": 1, "i32": 4, "u32": 4, "u64": 8}
 ALIGN = 256
 
 
@@ -49,7 +49,12 @@ class TensorSpec:
         return n
 
 
-GEMM_PATHS = ("stream", "tile")
+GEMM_PATHS = ("fused", "stream", "tile")
+FUSED_HI = ((512, 256), (1024, 1024), (2048, 512), (4096, 256))  # netra_moe_ffn_{gate_up,down}_h<H>_i<I>_<v>_gfx950
+FUSED_MAX_T = 64                     # one bitmask word per expert in the gate/up prologue
+FFN_NARROW_T = 8                     # T at or below which the decode FFN splits K (the "narrow" variant)
+FFN_COUNTERS = 64 * 64               # combine hand-off counters [token][column group] (kCounters)
+FFN_WIDE_P = {(512, 256): 2, (1024, 1024): 4, (2048, 512): 4, (4096, 256): 2}  # wide gate/up items per wave (PG)
 STREAM_H = (512, 1024, 2048, 4096)   # netra_moe_gate_up_stream_h<H>_c<CH>_gfx950
 STREAM_I = (256, 512, 1024, 2048)    # netra_moe_down_stream_i<I>_c<DC>_gfx950
 TILE_H = (512, 1024, 2048, 4096)     # netra_moe_gate_up_tile_h<H>_gfx950
@@ -81,12 +86,24 @@ def stream_chunks(cfg: MoEConfig) -> tuple[int, int]:
     return cu, cd
 
 
+def fused_supported(cfg: MoEConfig) -> bool:
+    """The decode FFN kernels (netra_moe_ffn_gate_up / netra_moe_ffn_down) cover T <= 64 for the
+    instantiated (H, I), up to 512 experts, 16 routes per token and 1024
+    capacity blocks."""
+    return (cfg.T <= FUSED_MAX_T and (cfg.H, cfg.I) in FUSED_HI and cfg.Etot <= 512 and cfg.Ktot <= 16
+            and cfg.cap_blocks <= 1024)
+
+
 def resolve_path(cfg: MoEConfig, path: str = "auto") -> str:
-    """stream: split-K weight streaming (decode-sized T); tile: 64-row block tiles."""
+    """fused: router + one decode FFN launch (T <= 64); stream: split-K weight
+    streaming (decode-sized T); tile: 64-row block tiles."""
     if path == "auto":
-        path = "stream" if cfg.T <= 256 else "tile"
+        path = "fused" if fused_supported(cfg) else "stream" if cfg.T <= 256 else "tile"
     if path not in GEMM_PATHS:
         raise ValueError(f"unknown GEMM path {path!r}")
+    if path == "fused" and not fused_supported(cfg):
+        raise ValueError("the fused decode FFN needs T <= 64, (H, I) in "
+                         f"{FUSED_HI}, at most 512 experts and 16 routes per token")
     if path == "stream" and (cfg.H not in STREAM_H or cfg.I not in STREAM_I):
         raise ValueError(f"stream path kernels exist for H in {STREAM_H} and I in {STREAM_I}")
     if path == "tile" and (cfg.H not in TILE_H or cfg.I not in TILE_I):
@@ -114,6 +131,8 @@ def resolve_front(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> st
     ok = cfg.H in SCREEN_H and cfg.E <= SCREEN_EMAX[-1]
     if front == "auto":
         front = "screen" if path == "tile" and ok else "exact"
+    if path == "fused" and front != "exact":
+        raise ValueError("the fused decode path computes every logit (exact front end)")
     if front not in FRONTS:
         raise ValueError(f"unknown front end {front!r}")
     if front == "screen" and not ok:
@@ -181,24 +200,35 @@ def tensor_table(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> dic
         TensorSpec("num_valid", "i32", (4,), "temporary"),
         TensorSpec("expert_counts", "i32", (cfg.Etot,), "temporary"),
     ]
-    if front == "exact":
-        specs.append(TensorSpec("mask", "u64", (cfg.Etot, cfg.mask_words_per_expert), "temporary"))
+    if path == "fused":
+        # hand-off counters (route: one per token group, padded to a line; decode
+        # FFN combine: one per (token, column range)); zero at engine creation
+        # and put back to zero by every launch
+        specs += [TensorSpec("route_counters", "u32", (route_groups(cfg), COUNTER_STRIDE), "temporary"),
+                  TensorSpec("ffn_counters", "u32", (FFN_COUNTERS,), "temporary"),
+                  # bf16 h rows of every tile (the narrow gate/up hands them to down)
+                  TensorSpec("h_rows", "bf16", (cfg.cap_tiles * 16, I), "temporary")]
+    elif front == "exact":
+        specs += [TensorSpec("mask", "u64", (cfg.Etot, cfg.mask_words_per_expert), "temporary"),
+                  # top-k hand-off counters of the route kernel, one per token group;
+                  # zero at engine creation and put back to zero by every launch
+                  TensorSpec("route_counters", "u32", (route_groups(cfg), COUNTER_STRIDE), "temporary")]
     else:
         specs += [TensorSpec("screen", "f32", (screen_splits(cfg), T, screen_row_pad(cfg)), "temporary"),
                   TensorSpec("route_wsq", "f32", (screen_splits(cfg), screen_row_pad(cfg)), "temporary"),
                   TensorSpec("route_base", "i32", (cfg.Etot, screen_groups(cfg)), "temporary"),
                   TensorSpec("route_rank", "i32", (T * cfg.Ktot,), "temporary")]
-    if path == "stream":
+    if path in ("stream", "fused"):
         specs += [TensorSpec("h_q", "e4m3", (cfg.cap_rows, I), "temporary"),
                   TensorSpec("h_scale", "f32", (cfg.cap_rows // 16, I // 128, 16), "temporary")]
     else:
         specs += [TensorSpec("h_q", "e4m3", (cfg.cap_rows, I), "temporary"),
                   TensorSpec("h_scale", "f32", (cfg.cap_rows, I // 128), "temporary")]
-    specs.append(TensorSpec("partial", "f32" if path == "stream" else "bf16", (cfg.routes, H), "temporary"))
+    specs.append(TensorSpec("partial", "bf16" if path == "tile" else "f32", (cfg.routes, H), "temporary"))
     return {s.name: s for s in specs}
 
 
-EXACT_FRONT_OPS = ("router", "topk", "sort")
+EXACT_FRONT_OPS = ("route", "sort")
 SCREEN_FRONT_OPS = ("route_screen", "route_select", "sort_count", "sort_place")
 PATH_OPS = {"stream": ("gate_up", "down", "combine"), "tile": ("gate_up", "down", "combine")}
 
@@ -206,6 +236,8 @@ PATH_OPS = {"stream": ("gate_up", "down", "combine"), "tile": ("gate_up", "down"
 def op_names(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> tuple[str, ...]:
     """Engine operation names of one layer call, in launch order."""
     path = resolve_path(cfg, path)
+    if path == "fused":
+        return ("route", "gate_up", "down") + (("combine",) if ffn_variant(cfg) == "wide" else ())
     front_ops = EXACT_FRONT_OPS if resolve_front(cfg, path, front) == "exact" else SCREEN_FRONT_OPS
     return front_ops + PATH_OPS[path]
 ROUTER_H = (512, 1024, 2048, 4096)   # netra_moe_router_h<H>_t<NT>_gfx950
@@ -223,6 +255,15 @@ def router_tokens(H: int, T: int) -> int:
     if H >= 4096:
         return 2
     return max(1, 2048 // H) if T <= ROUTER_SMALL_T else 4
+
+
+COUNTER_STRIDE = 64  # u32 words per hand-off counter (one 256-byte line each; kCounterStride)
+
+
+def route_groups(cfg: MoEConfig) -> int:
+    """Token groups of the route kernel (its grid's y extent, one hand-off counter each)."""
+    nt = router_tokens(cfg.H, cfg.T)
+    return (cfg.T + nt - 1) // nt
 
 
 def _screen_front(cfg: MoEConfig) -> list[dict]:
@@ -277,6 +318,94 @@ def down_rows_groups(cfg: MoEConfig) -> int:
     return nbc
 
 
+def _route_op(cfg: MoEConfig) -> dict:
+    """Router logits + input quant + top-k (hand-off to the last row-group workgroup of each token group)."""
+    T, H = cfg.T, cfg.H
+    u = lambda v: ("u32", int(v))  # noqa: E731
+    NT = router_tokens(H, T)
+    return dict(name="moe.route", symbol=f"netra_moe_route_h{H}_t{NT}_gfx950",
+                grid=((cfg.router_rows + 15) // 16, route_groups(cfg), 1),
+                block=(256, 1, 1), lds=4 * NT * H + 4, dyn=0,
+                args=["x", "router_w", "router_bias", "logits", "x_q", "x_scale", "topk_ids", "topk_weights",
+                      "route_counters", u(T), u(H), u(cfg.router_rows), u(cfg.E), u(cfg.K), u(cfg.S)],
+                reads=["x", "router_w", "router_bias", "route_counters"],
+                writes=["logits", "x_q", "x_scale", "topk_ids", "topk_weights", "route_counters"],
+                refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150",
+                      "tools/benchmark/export_qwen36_router_bf16_capture.py:78",
+                      "runtime/gfx950/routing/decode/qwen36_shared_gate_append_bridge.hip:76-112",
+                      "tools/benchmark/export_qwen36_shared_gate_append_capture.py:97-107,134-139"])
+
+
+def ffn_variant(cfg: MoEConfig) -> str:
+    """narrow (K split over waves) for a handful of tokens, else wide."""
+    return "narrow" if cfg.T <= FFN_NARROW_T else "wide"
+
+
+def ffn_lds_bytes(cfg: MoEConfig) -> tuple[int, int]:
+    """Static LDS of netra_moe_ffn_{gate_up,down}_h<H>_i<I>_<v> (their
+    __shared__ arrays, rounded up)."""
+    kb, kbi = cfg.H // 128, cfg.I // 128
+    narrow = ffn_variant(cfg) == "narrow"
+    red = 8 * 8 * 64 * 4 if narrow else 0
+    gu = max(kb * 2048, red, 1024 * 4 + 513 * 4) + 64 * kb + (8 if narrow else 16 * (128 * FFN_WIDE_P[(cfg.H, cfg.I)] + 8)) * 2
+    gu += 64 * 16 * 4 + 512 * 8 + 2 * 513 * 4 + 48 * 4
+    dn = max(kbi * 2048, red) + 64 * kbi + 4
+    return (gu + 255) // 256 * 256, (dn + 255) // 256 * 256
+
+
+# Workgroups of the decode FFN kernels per (operation, variant), measured at
+# T = 64 / T = 1 on one MI355X: wide gate/up streams a whole tile per
+# workgroup and fills the chip once at 2 waves per SIMD (its register budget);
+# narrow gate/up runs two 8-wave workgroups per CU; down deals its items over
+# more workgroups than are resident (two per CU at a time). H = 4096 gate/up
+# runs one per CU: the LDS of two does not fit.
+FFN_GRID = {("gate_up", "wide"): 256, ("gate_up", "narrow"): 512, ("down", "wide"): 2048, ("down", "narrow"): 1024}
+
+
+def ffn_grid(cfg: MoEConfig, op: str) -> int:
+    g = FFN_GRID[(op, ffn_variant(cfg))]
+    return 256 if op == "gate_up" and cfg.H > 2048 else g
+
+
+def _fused_decode(cfg: MoEConfig) -> list[dict]:
+    """Route (router + top-k), gate/up with the sort as its prologue, down with
+    the combine folded in (narrow) or followed by the combine kernel (wide)."""
+    T, H, I = cfg.T, cfg.H, cfg.I
+    u = lambda v: ("u32", int(v))  # noqa: E731
+    v = ffn_variant(cfg)
+    lds_gu, lds_dn = ffn_lds_bytes(cfg)
+    sort_out = ["sorted_ids", "sorted_expert", "tile_map", "pair_map", "num_valid", "expert_counts"]
+    ops = [
+        _route_op(cfg),
+        dict(name="moe.gate_up", symbol=f"netra_moe_ffn_gate_up_h{H}_i{I}_{v}_gfx950",
+             grid=(ffn_grid(cfg, "gate_up"), 1, 1), block=(512, 1, 1), lds=lds_gu, dyn=0,
+             args=["topk_ids", "x_q", "x_scale", "w13", "w13_scale", *sort_out, "h_rows", "h_q", "h_scale",
+                   u(T), u(cfg.E), u(cfg.K), u(cfg.S), u(cfg.cap_blocks)],
+             reads=["topk_ids", "x_q", "x_scale", "w13", "w13_scale"],
+             writes=[*sort_out, "h_rows", "h_q", "h_scale"],
+             refs=["kernels/gfx950/templates/moe/decode/gate_up_mfma.inc:12-161",
+                   "kernels/gfx950/templates/moe/decode/silu_quant.inc:16-236",
+                   "kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]),
+        dict(name="moe.down", symbol=f"netra_moe_ffn_down_h{H}_i{I}_{v}_gfx950",
+             grid=(ffn_grid(cfg, "down"), 1, 1), block=(512, 1, 1), lds=lds_dn, dyn=0,
+             args=["topk_weights", "w2", "w2_scale", "sorted_ids", "sorted_expert", "tile_map", "num_valid",
+                   "h_rows", "h_q", "h_scale", "partial", "ffn_counters", "out",
+                   u(T), u(cfg.E), u(cfg.K), u(cfg.S)],
+             reads=["topk_weights", "w2", "w2_scale", "sorted_ids", "sorted_expert", "tile_map", "num_valid",
+                    "h_rows", "h_q", "h_scale", "ffn_counters"],
+             writes=["h_q", "h_scale", "partial", "ffn_counters", "out"],
+             refs=["kernels/gfx950/templates/moe/decode/down_reduce_mfma_2wave.inc:14-291"]),
+    ]
+    if v == "wide":  # the wide down leaves the fp32 partials to the combine kernel
+        ops[-1]["writes"] = ["partial"]
+        ops.append(dict(name="moe.combine", symbol="netra_moe_combine_gfx950",
+                        grid=((H + 1023) // 1024, T, 1), block=(256, 1, 1), lds=0, dyn=0,
+                        args=["partial", "topk_weights", "out", u(T), u(H), u(cfg.Ktot)],
+                        reads=["partial", "topk_weights"], writes=["out"],
+                        refs=["kernels/gfx950/templates/moe/prefill/route_reduce_splitk2_f16.inc:6-117"]))
+    return ops
+
+
 def _tile_down(cfg: MoEConfig) -> dict:
     T, H, I = cfg.T, cfg.H, cfg.I
     u = lambda v: ("u32", int(v))  # noqa: E731
@@ -309,32 +438,20 @@ def operations(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> list[
         raise ValueError(f"router kernels exist for H in {ROUTER_H}")
     u = lambda v: ("u32", int(v))  # noqa: E731
     ops = [
-        dict(name="moe.router", symbol=f"netra_moe_router_h{H}_t{router_tokens(H, T)}_gfx950",
-             grid=((cfg.router_rows + 15) // 16, (T + router_tokens(H, T) - 1) // router_tokens(H, T), 1),
-             block=(256, 1, 1), lds=4 * router_tokens(H, T) * H, dyn=0,
-             args=["x", "router_w", "logits", "x_q", "x_scale", "mask",
-                   u(T), u(H), u(cfg.router_rows), u(cfg.Etot * W)],
-             reads=["x", "router_w"], writes=["logits", "x_q", "x_scale", "mask"],
-             refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150",
-                   "tools/benchmark/export_qwen36_router_bf16_capture.py:78"]),
-        dict(name="moe.topk", symbol="netra_moe_topk_gfx950",
-             grid=((T + 3) // 4, 1, 1), block=(256, 1, 1), lds=0, dyn=0,
-             args=["logits", "router_bias", "topk_ids", "topk_weights", "mask",
-                   u(T), u(cfg.E), u(cfg.K), u(cfg.S), u(W)],
-             reads=["logits", "router_bias", "mask"], writes=["topk_ids", "topk_weights", "mask"],
-             refs=["runtime/gfx950/routing/decode/qwen36_shared_gate_append_bridge.hip:76-112",
-                   "tools/benchmark/export_qwen36_shared_gate_append_capture.py:97-107,134-139"]),
+        _route_op(cfg),
         dict(name="moe.sort", symbol="netra_moe_sort_gfx950",
              grid=(1, 1, 1), block=(1024, 1, 1), lds=0, dyn=cfg.sort_lds_bytes,
              args=["topk_ids", "mask", "sorted_ids", "sorted_expert", "tile_map", "pair_map", "num_valid",
                    "expert_counts",
                    u(T), u(cfg.Ktot), u(cfg.Etot), u(W), u(cfg.cap_blocks)],
-             reads=["topk_ids", "mask"],
-             writes=["sorted_ids", "sorted_expert", "tile_map", "pair_map", "num_valid", "expert_counts"],
+             reads=["topk_ids"],
+             writes=["mask", "sorted_ids", "sorted_expert", "tile_map", "pair_map", "num_valid", "expert_counts"],
              refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]),
     ]
     if front == "screen":
         ops = _screen_front(cfg)
+    if path == "fused":
+        return _fused_decode(cfg)
     common = ["sorted_ids", "sorted_expert", "num_valid"]
     if path == "stream":
         ops += [
@@ -401,7 +518,7 @@ def operations(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> list[
 # weights. The numerical semantic differs by front end: the screen front end
 # leaves non-selected logits as bf16 MFMA screen values, not contract values.
 WEIGHT_LAYOUTS = "w13_tile16x128_gate_up_interleaved.w2_tile16x128"
-H_LAYOUTS = {"stream": "h_tile16x128_rowscale16", "tile": "h_row_major_rowscale"}
+H_LAYOUTS = {"fused": "h_tile16x128_rowscale16", "stream": "h_tile16x128_rowscale16", "tile": "h_row_major_rowscale"}
 NUMERICS = {
     "exact": "router_16slice_fma_tree.topk_lowidx.exp_cw7.v1",
     "screen": "router_bf16_mfma_screen_certified_exact_candidates.topk_lowidx.exp_cw7.v1",

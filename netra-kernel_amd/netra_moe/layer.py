@@ -19,7 +19,7 @@ from .engine import compile_moe_engine, op_names, resolve_front, resolve_path, t
 from .runtime import Engine, LaunchShape
 
 TORCH_DTYPES = {"bf16": torch.bfloat16, "f32": torch.float32, "e4m3": torch.uint8,
-                "i32": torch.int32, "u64": torch.int64}
+                "i32": torch.int32, "u32": torch.int32, "u64": torch.int64}
 WEIGHT_NAMES = ("router_w", "router_bias", "w13", "w13_scale", "w2", "w2_scale")
 
 
@@ -65,7 +65,9 @@ class MoELayer:
         for name, info in self.recipe["tensors"].items():
             if info["storage"] == "binding" and name not in self.buffers:
                 spec = self.specs[name]
-                self.buffers[name] = torch.empty(spec.shape, dtype=TORCH_DTYPES[spec.dtype], device=self.device)
+                # zeroed: some temporaries (hand-off counters) must start at zero,
+                # as the engine's own workspace does
+                self.buffers[name] = torch.zeros(spec.shape, dtype=TORCH_DTYPES[spec.dtype], device=self.device)
         for name, slots in self.recipe["bindings"].items():
             ptr = self.buffers[name].data_ptr()
             for profile, op, arg in slots:

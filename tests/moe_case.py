@@ -14,12 +14,13 @@ from netra_moe import weights as W
 
 ROUTING = ("logits", "topk_ids", "topk_weights", "x_q", "x_scale", "sorted_ids",
            "sorted_expert", "tile_map", "pair_map", "num_valid", "expert_counts", "partial")
-PATH_INTERMEDIATES = {"stream": ("h_q", "h_scale"), "tile": ("h_q", "h_scale")}
+PATH_INTERMEDIATES = {"fused": ("h_q", "h_scale", "ffn_counters"), "stream": ("h_q", "h_scale"), "tile": ("h_q", "h_scale")}
 FRONT_INTERMEDIATES = {"exact": ("mask",), "screen": ()}
 
 
 def intermediates(path: str, front: str) -> tuple[str, ...]:
-    return ROUTING + PATH_INTERMEDIATES[path] + FRONT_INTERMEDIATES[front]
+    front_extra = () if path == "fused" else FRONT_INTERMEDIATES[front]  # the gate/up prologue keeps its bitmask in LDS
+    return ROUTING + PATH_INTERMEDIATES[path] + front_extra
 WEIGHT_SEED = 77
 
 

@@ -88,7 +88,9 @@ def test_emitted_engine_passes_the_native_manifest_check(engine_dir):
     assert st == nm.Status.OK, msg
     doc = json.loads((engine_dir / "engine.json").read_text())
     assert [op["name"] for op in doc["operations"]] == [f"moe.{n}" for n in op_names(nm.BASELINE_CONFIGS["decode_t64"])]
-    assert op_names(nm.BASELINE_CONFIGS["decode_t64"]) == ("router", "topk", "sort", "gate_up", "down", "combine")
+    assert op_names(nm.BASELINE_CONFIGS["decode_t64"]) == ("route", "gate_up", "down", "combine")
+    assert op_names(nm.BASELINE_CONFIGS["decode_t1"]) == ("route", "gate_up", "down")
+    assert op_names(nm.BASELINE_CONFIGS["decode_t64"], path="stream") == ("route", "sort", "gate_up", "down", "combine")
 
 
 def _corrupt(engine_dir: Path, mutate) -> tuple:
@@ -108,7 +110,7 @@ def _corrupt(engine_dir: Path, mutate) -> tuple:
     (lambda d: d["operations"][0].update(hsaco="/abs/x.hsaco"), "hsaco"),
     (lambda d: d["operations"][0]["launch"].update(grid=[0, 1, 1]), "nonzero"),
     (lambda d: d["operations"][0]["launch"].update(block=[2048, 1, 1]), "1024"),
-    (lambda d: d["operations"][2].update(launch={**d["operations"][2]["launch"], "dynamic_lds_bytes": 200000}), "LDS"),
+    (lambda d: d["operations"][-1].update(launch={**d["operations"][-1]["launch"], "dynamic_lds_bytes": 200000}), "LDS"),
     (lambda d: d["operations"][0]["arguments"].append({"kind": "pointer", "source": "workspace",
                                                        "workspace_offset": d["workspace_bytes"]}), "workspace"),
     (lambda d: d["operations"][0]["arguments"].extend([{"kind": "u32_constant", "value": 1}] * 40), "32"),

@@ -1,5 +1,6 @@
 """HIP path vs the CPU oracle on identical seeded inputs: the five benchmark
-configs and two extra shapes, each through both GEMM paths.
+configs and the extra shapes below, each through every GEMM path that
+covers it (fused decode FFN for T <= 64, stream, tile).
 
 Bars: router logits (every logit on the exact front end; the selected and
 shared-gate logits on the screen front end, the others within the screen's
@@ -21,6 +22,7 @@ from conftest import gpu_available
 from moe_case import make_inputs, oracle_routing, run_gpu, sample_tokens
 from netra_moe import weights as W
 from netra_moe.config import BASELINE_CONFIGS, MoEConfig
+from netra_moe.engine import fused_supported
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a GPU")]
 
@@ -48,7 +50,8 @@ EXTRA_CONFIGS = {
                             router_bias="zipf1.1", seed=1104),
 }
 CONFIGS = {**BASELINE_CONFIGS, **EXTRA_CONFIGS}
-CASES = [(name, path) for name in CONFIGS for path in ("stream", "tile")]
+CASES = [(name, path) for name in CONFIGS for path in ("fused", "stream", "tile")
+         if path != "fused" or fused_supported(CONFIGS[name])]
 
 
 @pytest.fixture(scope="module", params=CASES, ids=[f"{n}-{p}" for n, p in CASES])
@@ -148,7 +151,7 @@ def test_gate_up_silu_quant_rows(case):
     rows = h_sample_rows(cfg, ref)
     h_q, h_s = oracle.gate_up_rows(ref["x_q"], ref["x_scale"], host["w13"], host["w13_scale"],
                                    ref["sorted_ids"], ref["sorted_expert"], rows, cfg.T, cfg.H, cfg.I)
-    if got["path"] == "stream":  # tile16x128 FP8 tiles, scales [tile][block][row]
+    if got["path"] in ("stream", "fused"):  # tile16x128 FP8 tiles, scales [tile][block][row]
         gq = W.unpack_tiles_host(got["h_q"].reshape(1, -1, cfg.I))[0]
         gs = got["h_scale"].transpose(0, 2, 1).reshape(-1, cfg.I // 128)
     else:
@@ -189,3 +192,13 @@ def test_layer_output_within_tolerance(case):
 def test_repeat_launches_bitwise_identical(case):
     cfg, host, got, ref = case
     np.testing.assert_array_equal(got["runs"][0], got["runs"][1])
+
+
+def test_handoff_counters_back_to_zero(case):
+    """The decode down kernel's combine counters are all zero again after
+    every launch (the next launch counts from them)."""
+    cfg, host, got, ref = case
+    if got["path"] != "fused":
+        pytest.skip("combine hand-off counters belong to the fused decode path")
+    ctl = got["ffn_counters"]
+    assert not ctl.any(), f"counters left nonzero at {np.flatnonzero(ctl)[:8]}"

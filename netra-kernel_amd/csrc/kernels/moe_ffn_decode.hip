@@ -74,6 +74,7 @@ constexpr uint32_t kMaxE = 512;      // experts incl. shared, one per thread in 
 constexpr uint32_t kMaxCap = 1024;   // capacity blocks
 constexpr uint32_t kMaxGroups = 64;  // down column groups per token (H / 64 at most)
 constexpr uint32_t kCounters = kMaxT * kMaxGroups;  // combine counters [token][group]
+constexpr uint32_t kNarrowT = 8;     // tokens the narrow variant serves (their x rows staged in LDS)
 
 // Position of the j-th set bit (0-based) of m; 64 if there is none.
 __device__ __forceinline__ uint32_t nth_bit(unsigned long long m, uint32_t j) {
@@ -146,6 +147,10 @@ __device__ __forceinline__ void ffn_gate_up(
   __shared__ unsigned long long s_mask[kMaxE];
   __shared__ uint32_t s_boff[kMaxE + 1], s_toff[kMaxE + 1];
   __shared__ uint32_t s_chunk[48];
+  constexpr bool kStageAll = SA > 1;                   // narrow: T <= kNarrowT tokens' rows fit in LDS
+  constexpr uint32_t kAllPieces = kStageAll ? (kNarrowT * H / 16u + kThreads - 1u) / kThreads : 0u;
+  __shared__ uint4 s_xall[kStageAll ? kNarrowT * H / 16u : 1u];
+  __shared__ float s_xsall[kStageAll ? kNarrowT * KB : 1u];
   uint8_t* const s_a = s_big;
   float* const s_red = reinterpret_cast<float*>(s_big);
   int32_t* const s_owner = reinterpret_cast<int32_t*>(s_big);
@@ -153,10 +158,21 @@ __device__ __forceinline__ void ffn_gate_up(
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = nkstream::wave_id();
   const uint32_t Ktot = K + S, Etot = E + S, routes = T * Ktot;
-  if (T > kMaxT || Ktot > kMaxKtot || Etot > kMaxE || cap_blocks > kMaxCap || K > E) return;  // host-checked
+  if (T > (kStageAll ? kNarrowT : kMaxT) || Ktot > kMaxKtot || Etot > kMaxE || cap_blocks > kMaxCap || K > E)
+    return;  // host-checked
 
   // ---- routes into LDS, routing bitmask ------------------------------------------------------
   if (tid < Etot) s_mask[tid] = 0ull;
+  // narrow: every token's x row and scales go to LDS now, their loads in
+  // flight together with the ids', so no item waits for a gather from memory
+  if constexpr (kStageAll) {
+#pragma unroll
+    for (uint32_t q = 0; q < kAllPieces; ++q) {
+      const uint32_t i = tid + q * kThreads;  // 16-byte piece of the T x H rows
+      if (i < T * (H / 16u)) s_xall[i] = reinterpret_cast<const uint4*>(xq)[i];
+    }
+    for (uint32_t i = tid; i < T * KB; i += kThreads) s_xsall[i] = xs[i];
+  }
   for (uint32_t r = tid; r < routes; r += kThreads) s_ids[r] = topk_ids[r];
   lds_barrier();
   for (uint32_t r = tid; r < routes; r += kThreads) {
@@ -267,14 +283,20 @@ __device__ __forceinline__ void ffn_gate_up(
     for (uint32_t q = 0; q < kPieces; ++q) {
       const uint32_t pc = tid + q * kThreads, row = pc / (H / 16u), kk = (pc % (H / 16u)) * 16u;
       const int32_t t = __shfl(tok, row);
-      av[q] = t >= 0 ? *reinterpret_cast<const uint4*>(xq + (size_t)t * H + kk) : make_uint4(0u, 0u, 0u, 0u);
+      if constexpr (kStageAll)
+        av[q] = t >= 0 ? s_xall[(uint32_t)t * (H / 16u) + kk / 16u] : make_uint4(0u, 0u, 0u, 0u);
+      else
+        av[q] = t >= 0 ? *reinterpret_cast<const uint4*>(xq + (size_t)t * H + kk) : make_uint4(0u, 0u, 0u, 0u);
     }
     float xv[kScales];
 #pragma unroll
     for (uint32_t q = 0; q < kScales; ++q) {
       const uint32_t i = tid + q * kThreads;
       const int32_t t = __shfl(tok, (i / KB) & 15u);
-      xv[q] = (i < 16u * KB && t >= 0) ? xs[(size_t)t * KB + i % KB] : 0.0f;
+      if constexpr (kStageAll)
+        xv[q] = (i < 16u * KB && t >= 0) ? s_xsall[(uint32_t)t * KB + i % KB] : 0.0f;
+      else
+        xv[q] = (i < 16u * KB && t >= 0) ? xs[(size_t)t * KB + i % KB] : 0.0f;
     }
 #pragma unroll
     for (uint32_t q = 0; q < kPieces; ++q) {

@@ -94,11 +94,21 @@ def fused_supported(cfg: MoEConfig) -> bool:
             and cfg.cap_blocks <= 1024)
 
 
+def _planned(cfg: MoEConfig, path: str = "auto"):
+    from .planner import layer_request, plan_layer
+    plan = plan_layer(layer_request(cfg, path=path))
+    if plan.selected is None:
+        why = "; ".join(f"{c['tactic']}: {', '.join(c['reasons'])}" for c in plan.candidates)
+        raise ValueError(f"no gfx950 kernel path serves this configuration ({why})")
+    return plan.selected
+
+
 def resolve_path(cfg: MoEConfig, path: str = "auto") -> str:
-    """fused: router + one decode FFN launch (T <= 64); stream: split-K weight
-    streaming (decode-sized T); tile: 64-row block tiles."""
+    """fused: route, gate/up with the sort, down (+ combine) for T <= 64;
+    stream: split-K weight streaming (decode-sized T); tile: 64-row block
+    tiles. auto takes the planner's best-ranked tactic (netra_moe.planner)."""
     if path == "auto":
-        path = "fused" if fused_supported(cfg) else "stream" if cfg.T <= 256 else "tile"
+        path = _planned(cfg).path
     if path not in GEMM_PATHS:
         raise ValueError(f"unknown GEMM path {path!r}")
     if path == "fused" and not fused_supported(cfg):
@@ -130,7 +140,7 @@ def resolve_front(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> st
     path = resolve_path(cfg, path)
     ok = cfg.H in SCREEN_H and cfg.E <= SCREEN_EMAX[-1]
     if front == "auto":
-        front = "screen" if path == "tile" and ok else "exact"
+        front = _planned(cfg, path).front
     if path == "fused" and front != "exact":
         raise ValueError("the fused decode path computes every logit (exact front end)")
     if front not in FRONTS:
@@ -550,15 +560,57 @@ def _dependencies(ops: list[dict]) -> list[list[int]]:
     return deps
 
 
+# Tensors whose contents carry from one launch to the next: the hand-off
+# counters start at zero (the workspace is zeroed at engine creation) and every
+# launch puts them back to zero. They get bytes of their own in the workspace.
+PERSISTENT_TENSORS = frozenset({"route_counters", "ffn_counters"})
+
+
 def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ...] = (),
-                       hsaco: Path | None = None, path: str = "auto", front: str = "auto") -> dict:
-    """Write the engine directory; returns the graph recipe (also on disk)."""
-    path = resolve_path(cfg, path)
-    front = resolve_front(cfg, path, front)
+                       hsaco: Path | None = None, path: str = "auto", front: str = "auto",
+                       semantics: dict | None = None, allow_experimental: bool = False) -> dict:
+    """Plan the layer (netra_moe.planner), then write the engine directory:
+    engine.json, contracts.json, graph_recipe.json, memory_plan.json and
+    explain.json (every tactic considered, with its rejection reasons). When no
+    tactic serves the request the engine holds one framework-fallback operation
+    and no kernels. Returns the graph recipe (also on disk)."""
+    from .planner import layer_request, pack_workspace, plan_layer
     directory = Path(directory)
     hsaco = Path(hsaco) if hsaco else paths.hsaco_path()
     if not hsaco.is_file():
         raise FileNotFoundError(f"code object {hsaco} is missing; run the build first")
+    plan = plan_layer(layer_request(cfg, semantics=semantics, path=path, front=front),
+                      allow_experimental=allow_experimental)
+    profile = profile_for(cfg)
+    explain = {"format": "netra-explain-1", "profile": profile.to_dict(),
+               "operations": [plan.explain("moe.layer")]}
+    engine = {
+        "format_version": "netra-engine-1",
+        "target": "gfx950",
+        "wave_size": 64,
+        "required_rocm": {"minimum": "7.0", "code_object_version": 6},
+        "name": f"netra-moe-{cfg.name}",
+        "configuration": cfg.to_dict(),
+        "profiles": [{"name": profile.name, "guards": profile.to_dict()["guards"],
+                      "tensor_parallel": profile.tensor_parallel}],
+        "artifact_files": ["contracts.json", "graph_recipe.json", "memory_plan.json", "explain.json"],
+    }
+    directory.mkdir(parents=True, exist_ok=True)
+    if plan.selected is None:
+        engine.update(gemm_path=None, front_end=None, workspace_bytes=0, selected_tactics=[],
+                      operations=[{"name": "moe.layer", "execution": "fallback", "fallback": plan.fallback}],
+                      fallbacks={"moe.layer": plan.fallback})
+        recipe = {"format": "netra-graph-recipe-1", "execution": "fallback", "gemm_path": None,
+                  "front_end": None, "operations": [], "tensors": {}, "bindings": {}, "dependencies": []}
+        for fname, doc in (("engine.json", engine), ("contracts.json", {"contracts": []}),
+                           ("graph_recipe.json", recipe),
+                           ("memory_plan.json", {"format": "netra-memory-plan-1", "workspace_bytes": 0,
+                                                 "alignment": ALIGN, "buffers": [], "offsets": {}}),
+                           ("explain.json", explain)):
+            (directory / fname).write_text(canonical_json(doc))
+        return recipe
+
+    path, front = plan.selected.path, plan.selected.front
     tensors = tensor_table(cfg, path, front)
     unknown = set(expose) - set(tensors)
     if unknown:
@@ -567,14 +619,10 @@ def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ..
     code = hsaco.read_bytes()
     sha = hashlib.sha256(code).hexdigest()
 
-    # Workspace: engine-owned temporaries, 256-byte aligned, no reuse.
-    offsets: dict[str, int] = {}
-    cursor = 0
-    for name, spec in tensors.items():
-        if spec.role == "temporary" and name not in expose:
-            offsets[name] = cursor
-            cursor += (spec.nbytes + ALIGN - 1) // ALIGN * ALIGN
-    workspace_bytes = cursor
+    # Workspace: engine-owned temporaries, interval-packed, 256-byte aligned.
+    owned = {n: s.nbytes for n, s in tensors.items() if s.role == "temporary" and n not in expose}
+    workspace_bytes, slots = pack_workspace(owned, ops, set(PERSISTENT_TENSORS), ALIGN)
+    offsets = {sl.name: sl.offset for sl in slots}
 
     bindings: dict[str, list[list[int]]] = {}
     op_records, contracts = [], []
@@ -602,27 +650,15 @@ def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ..
         contracts.append(contract.to_dict())
         op_records.append({
             "name": op["name"], "execution": "kernel", "contract_id": contract.stable_id,
-            "launch": launch.to_dict(), "hsaco": "hsaco/" + hsaco.name,
+            "tactic": plan.selected.name, "launch": launch.to_dict(), "hsaco": "hsaco/" + hsaco.name,
             "kernel_symbol": op["symbol"], "arguments": arguments,
         })
 
-    profile = profile_for(cfg)
-    engine = {
-        "format_version": "netra-engine-1",
-        "target": "gfx950",
-        "wave_size": 64,
-        "required_rocm": {"minimum": "7.0", "code_object_version": 6},
-        "name": f"netra-moe-{cfg.name}",
-        "configuration": cfg.to_dict(),
-        "gemm_path": path,
-        "front_end": front,
-        "workspace_bytes": workspace_bytes,
-        "profiles": [{"name": profile.name, "guards": profile.to_dict()["guards"],
-                      "tensor_parallel": profile.tensor_parallel}],
-        "operations": op_records,
-    }
+    engine.update(gemm_path=path, front_end=front, workspace_bytes=workspace_bytes,
+                  selected_tactics=[plan.selected.name], operations=op_records, fallbacks={})
     recipe = {
         "format": "netra-graph-recipe-1",
+        "execution": "kernel",
         "gemm_path": path,
         "front_end": front,
         "operations": [op["name"] for op in ops],
@@ -632,15 +668,16 @@ def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ..
         "bindings": bindings,
         "dependencies": _dependencies(ops),
     }
-    memory_plan = {"workspace_bytes": workspace_bytes, "alignment": ALIGN,
-                   "offsets": offsets}
+    memory_plan = {"format": "netra-memory-plan-1", "workspace_bytes": workspace_bytes, "alignment": ALIGN,
+                   "unpacked_bytes": sum((b + ALIGN - 1) // ALIGN * ALIGN for b in owned.values()),
+                   "buffers": [sl.to_dict() for sl in slots], "offsets": offsets}
 
-    directory.mkdir(parents=True, exist_ok=True)
     (directory / "hsaco").mkdir(exist_ok=True)
     target = directory / "hsaco" / hsaco.name
     if not target.exists() or target.read_bytes() != code:
         shutil.copyfile(hsaco, target)
     for fname, doc in (("engine.json", engine), ("contracts.json", {"contracts": contracts}),
-                       ("graph_recipe.json", recipe), ("memory_plan.json", memory_plan)):
+                       ("graph_recipe.json", recipe), ("memory_plan.json", memory_plan),
+                       ("explain.json", explain)):
         (directory / fname).write_text(canonical_json(doc))
     return recipe

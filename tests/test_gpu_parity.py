@@ -62,6 +62,7 @@ def case(request):
           flush=True)
     x, gpu_w, host = make_inputs(cfg, DEV)
     got = run_gpu(cfg, x, gpu_w, DEV, repeats=2, path=path)
+    got["inputs"] = (x, gpu_w)
     print(f"[parity] front end: {got['front']}", flush=True)
     ref = oracle_routing(cfg, host)
     return cfg, host, got, ref
@@ -202,3 +203,14 @@ def test_handoff_counters_back_to_zero(case):
         pytest.skip("combine hand-off counters belong to the fused decode path")
     ctl = got["ffn_counters"]
     assert not ctl.any(), f"counters left nonzero at {np.flatnonzero(ctl)[:8]}"
+
+
+def test_packed_workspace_run_is_bitwise_identical(case):
+    """The same layer with its temporaries in the interval-packed workspace
+    (nothing exposed but the top-k ids) and replayed as a HIP graph gives the
+    output of the run that exposed every intermediate as its own binding."""
+    cfg, host, got, ref = case
+    x, gpu_w = got["inputs"]
+    again = run_gpu(cfg, x, gpu_w, DEV, expose=("topk_ids",), graph=True, repeats=2, path=got["path"])
+    np.testing.assert_array_equal(again["out"], got["out"])
+    np.testing.assert_array_equal(again["runs"][0], again["runs"][1])

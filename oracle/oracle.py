@@ -297,3 +297,59 @@ def max_abs_rel(y: np.ndarray, ref: np.ndarray) -> float:
     ref = np.asarray(ref, np.float64)
     denom = float(np.max(np.abs(ref)))
     return float(np.max(np.abs(y - ref))) / denom if denom > 0 else float(np.max(np.abs(y - ref)))
+
+
+# ---- checkpoint stacking ----------------------------------------------------------------
+# Restates the weight-prep plan of reference compiler/netra_compiler/layouts.py:109-206
+# (output shards concatenated along axis 0, bf16 block scales widened exactly to
+# fp32) for the layer's stacked tensors: routed experts 0..E-1, the shared expert
+# as expert E, W13 rows gate then up. Pinned by tests/test_prep_oracle.py
+# (element-wise tile placement against the documented permutation, shard and
+# shared-expert positions, exact widening).
+
+def tile16x128(q: np.ndarray, gate_up: bool = False) -> np.ndarray:
+    """Place every byte of row-major [G, N, K] e4m3 codes at its tile16x128
+    position, computed per element: row tile r = n // 16, K block b = k // 128,
+    half = (k % 32) // 16, lane = (k % 128) // 32 * 16 + n % 16, byte k % 16;
+    tile (r, b) is 2048 bytes at (r' * K/128 + b) * 2048 with the half at
+    half * 1024 and the lane at lane * 16. r' = r, or for W13 (gate_up) the
+    interleaved order: gate tile j (r = j < N/32) at 2j, up tile j (r = N/32 + j)
+    at 2j + 1."""
+    g, n, k = q.shape
+    nn, kk = np.meshgrid(np.arange(n), np.arange(k), indexing="ij")
+    r, b = nn // 16, kk // 128
+    if gate_up:
+        half_tiles = n // 32
+        r = np.where(r < half_tiles, 2 * r, 2 * (r - half_tiles) + 1)
+    lane = (kk % 128) // 32 * 16 + nn % 16
+    dst = (r * (k // 128) + b) * 2048 + ((kk % 32) // 16) * 1024 + lane * 16 + kk % 16
+    out = np.empty((g, n * k), dtype=np.uint8)
+    out[:, dst.reshape(-1)] = q.reshape(g, n * k)
+    return out.reshape(g, n, k)
+
+
+def _scale_f32(a: np.ndarray) -> np.ndarray:
+    """Scale block grid as fp32: uint16 arrays are bf16 bit patterns (exact widening)."""
+    return f32_from_bf16(a) if a.dtype == np.uint16 else np.asarray(a, np.float32)
+
+
+def stack_checkpoint(tensors: dict, E: int, S: int, H: int, I: int, prefix: str) -> dict:
+    """{name: array or list of output shards} -> w13 / w13_scale / w2 / w2_scale
+    as the layer binds them (weights in tile16x128, scales fp32)."""
+    def name(e, proj, scale=False):
+        owner = "shared_expert" if e is None else f"experts.{e}"
+        return f"{prefix}.{owner}.{proj}.{'weight_scale_inv' if scale else 'weight'}"
+
+    def cat(v):
+        return np.concatenate(v, axis=0) if isinstance(v, (list, tuple)) else np.asarray(v)
+
+    experts = list(range(E)) + [None] * S
+    w13 = np.stack([np.concatenate([cat(tensors[name(e, "gate_proj")]), cat(tensors[name(e, "up_proj")])], axis=0)
+                    for e in experts])
+    w2 = np.stack([cat(tensors[name(e, "down_proj")]) for e in experts])
+    s13 = np.stack([np.concatenate([_scale_f32(cat(tensors[name(e, "gate_proj", True)])),
+                                    _scale_f32(cat(tensors[name(e, "up_proj", True)]))], axis=0) for e in experts])
+    s2 = np.stack([_scale_f32(cat(tensors[name(e, "down_proj", True)])) for e in experts])
+    assert w13.shape == (E + S, 2 * I, H) and w2.shape == (E + S, H, I)
+    return {"w13": tile16x128(w13.astype(np.uint8), gate_up=True), "w13_scale": s13.astype(np.float32),
+            "w2": tile16x128(w2.astype(np.uint8)), "w2_scale": s2.astype(np.float32)}

@@ -70,35 +70,26 @@ def time_graph(layers, steps: int, warmup: int, torch):
     return start.elapsed_time(end) / steps, wall * 1e3 / steps
 
 
-# Operations that rewrite an input in place (sort_count turns route_select's
-# histograms into row prefixes): timed behind the operation that produces that
-# input, minus that operation's own time.
-IN_PLACE_INPUT_FROM = {"sort_count": "route_select"}
-
-
-def time_operation(layers, op: str, steps: int, torch):
-    """Average duration of one operation, HIP events around back-to-back launches
-    on the stream the operation is launched on (torch's current stream)."""
-    pre = IN_PLACE_INPUT_FROM.get(op)
-
-    def launch(lay):
-        if pre:
-            lay.run_operation(pre)
-        lay.run_operation(op)
-
+def time_operations(layers, steps: int, torch) -> dict[str, float]:
+    """Average duration (ms) of every operation of a layer call, from HIP events
+    recorded between the operations of whole eager layer calls on the stream
+    they are launched on (torch's current stream). Operations always run in
+    order: their inputs are the previous operations' outputs, and the packed
+    workspace lets a later operation's tensors reuse an earlier one's bytes,
+    so an operation launched on its own would read stale data."""
+    names = layers[0].op_names
     for lay in layers:
         lay.forward()
     torch.cuda.synchronize()
-    for i in range(4):
-        launch(layers[i % len(layers)])
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
+    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(steps)]
     for i in range(steps):
-        launch(layers[i % len(layers)])
-    end.record()
+        lay = layers[i % len(layers)]
+        marks[i][0].record()
+        for j, op in enumerate(names):
+            lay.run_operation(op)
+            marks[i][j + 1].record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
-    return ms - time_operation(layers, pre, steps, torch) if pre else ms
+    return {op: sum(m[j].elapsed_time(m[j + 1]) for m in marks) / steps for j, op in enumerate(names)}
 
 
 def cpu_baseline(cfg, act_cpu, w_host, threads: int, min_seconds: float):
@@ -313,9 +304,7 @@ def main() -> int:
                 lay = MoELayer(c, w, graph=False)
                 lay.x.copy_(act["x"].to(dev))
                 dl.append(lay)
-            kern = {}
-            for op in dl[0].op_names:
-                kern[op] = time_operation(dl, op, max(50, steps // 2), torch) * 1e3  # us
+            kern = {op: ms * 1e3 for op, ms in time_operations(dl, max(50, steps // 2), torch).items()}  # us
             for lay in dl:
                 lay.close()
         for lay in layers:

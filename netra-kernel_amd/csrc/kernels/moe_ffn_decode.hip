@@ -435,7 +435,9 @@ __device__ __forceinline__ void ffn_down(
   const uint32_t wave = nkstream::wave_id();
   const uint32_t Ktot = K + S, Etot = E + S;
   if (T > kMaxT || Ktot > kMaxKtot || Etot > kMaxE) return;  // host-checked
-  const uint32_t ntile = (uint32_t)num_valid[2];
+  // tiles as the sort counted them, never past the capacity (T Ktot / 16 + Etot):
+  // an operation launched out of order may find another tensor's bytes here
+  const uint32_t ntile = min((uint32_t)num_valid[2], (T * Ktot + 15u) / 16u + Etot);
 
   // Combine hand-off of the held items: once every wave's partial stores have
   // completed, wave w lane l counts the arrival of held item 4w + (l >> 4),

@@ -25,8 +25,11 @@
 // step: acc += (w_s * a_s) * mfma. Epilogue: h = bf16(silu(g) * u) with the
 // hardware exp2 / reciprocal / bf16 conversion (the GEMM outputs are checked
 // within a tolerance), 1x128 FP8 requant, bytes through LDS to 16-byte stores.
-// Both LDS operand layouts are the tile16x128 operand layout, so every
-// ds_read_b128 is 1 KiB contiguous across the wave.
+// Weight tiles sit in LDS in the tile16x128 operand layout (every ds_read_b128
+// 1 KiB contiguous across the wave); activation rows arrive as whole 128-byte
+// lines, 8 lanes per row, into a row-major tile with swizzled 16-byte chunks
+// (row_swizzle), whose operand reads are conflict-free as well. (Fetching
+// them straight in the operand layout read every activation line half.)
 //
 // (reference: kernels/gfx950/templates/moe/decode/gate_up_mfma.inc:12-161,
 // silu_quant.inc:16-236; oracle tools/benchmark/export_qwen36_moe_stage1_capture.py:80-97)
@@ -95,6 +98,26 @@ __device__ __forceinline__ void wait_copies() {
 // Barrier for LDS hand-off: waits for this wave's LDS traffic, not for its
 // copies in flight (a full __syncthreads would drain those).
 __device__ __forceinline__ void barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Swizzle of the activation rows in LDS: a 16-row x 128-byte tile is stored
+// row-major with the 16-byte chunk c of row r at position c ^ row_swizzle(r),
+// so that each copy can fetch whole 128-byte lines (8 lanes per row) while the
+// operand reads stay conflict-free: the 16 rows of one read land on 16
+// distinct chunk positions within each 64-bank (or each 8-lane, 32-bank)
+// pass.
+__device__ __forceinline__ uint32_t row_swizzle(uint32_t r) { return (r ^ (r >> 3)) & 7u; }
+
+// MFMA operand of a swizzled activation tile: lane l gets row l & 15, bytes
+// 32 (l >> 4) .. + 31 (chunks 2 (l >> 4) and 2 (l >> 4) + 1).
+__device__ __forceinline__ v8i lds_operand_rows(const uint8_t* tile, uint32_t lane) {
+  const uint32_t r = lane & 15u, c = 2u * (lane >> 4), f = row_swizzle(r);
+  const uint4 lo = *reinterpret_cast<const uint4*>(tile + r * 128u + (c ^ f) * 16u);
+  const uint4 hi = *reinterpret_cast<const uint4*>(tile + r * 128u + ((c + 1u) ^ f) * 16u);
+  v8i v;
+  v[0] = (int)lo.x; v[1] = (int)lo.y; v[2] = (int)lo.z; v[3] = (int)lo.w;
+  v[4] = (int)hi.x; v[5] = (int)hi.y; v[6] = (int)hi.z; v[7] = (int)hi.w;
+  return v;
+}
 
 template <bool kAiter = false>
 __device__ __forceinline__ v8i lds_operand(const uint8_t* tile, uint32_t lane) {
@@ -165,11 +188,16 @@ __device__ __forceinline__ void gate_up_lds(
   const float* wse = w13s + (size_t)e * (2u * I / 128u) * KB;
   const float* wsg = wse + (size_t)ng * KB;               // gate rows' 128-row block
   const float* wsu = wse + (size_t)(I / 128u + ng) * KB;  // up rows' block
-  // copy sources: wave w moves A row tile w and weight tiles w of gate and of up
-  const int32_t atok = s_tok[wave * 16u + (lane & 15u)];
-  const uint32_t apiece = (2u * (lane >> 4)) * 16u;  // bytes of the lane's first 16-byte piece
-  const uint32_t avoff0 = atok >= 0 ? (uint32_t)atok * H + apiece : kFar;
-  const uint32_t avoff1 = atok >= 0 ? avoff0 + 16u : kFar;
+  // copy sources: wave w moves A row tile w and weight tiles w of gate and of up.
+  // A copy h fetches rows 8 h .. 8 h + 7 of the tile as whole 128-byte lines:
+  // lane l takes row 8 h + (l >> 3), the chunk its swizzled slot l & 7 holds
+  uint32_t avoff[2];
+#pragma unroll
+  for (uint32_t h = 0; h < 2u; ++h) {
+    const uint32_t r = 8u * h + (lane >> 3);
+    const int32_t atok = s_tok[wave * 16u + r];
+    avoff[h] = atok >= 0 ? (uint32_t)atok * H + (((lane & 7u) ^ row_swizzle(r)) * 16u) : kFar;
+  }
   const u32x4 ra = rsrc(xq, T * H);
   const uint8_t* w13e = w13 + (size_t)e * 2u * I * H;
   // gate tile t and up tile t are adjacent (gate/up-interleaved W13), or I/16
@@ -183,7 +211,7 @@ __device__ __forceinline__ void gate_up_lds(
   auto issue_part = [&](uint32_t kb, uint32_t q) __attribute__((always_inline)) {
     const uint32_t st = lds0 + (kb % kStages) * kStageBytes;
     const uint32_t half = (q & 1u) * 1024u;
-    if (q < 2u) copy16(st + wave * 2048u + half, ra, q ? avoff1 : avoff0, kb * 128u);
+    if (q < 2u) copy16(st + wave * 2048u + half, ra, avoff[q], kb * 128u);
     else if (q < 4u) copy16(st + kABytes + wave * 2048u + half, rg, bvoff + half, kb * 2048u);
     else copy16(st + kABytes + (8u + wave) * 2048u + half, rg, bvoff + half, (up_tiles * KB + kb) * 2048u);
   };
@@ -225,7 +253,7 @@ __device__ __forceinline__ void gate_up_lds(
 #pragma unroll
         for (uint32_t i = 0; i < NT; ++i) {
           const uint32_t rt = 4u * m + i;
-          const v8i af = lds_operand(st + rt * 2048u, lane);
+          const v8i af = lds_operand_rows(st + rt * 2048u, lane);
           const float4 as4 = *reinterpret_cast<const float4*>(&s_as[kb][rt * 16u + g * 4u]);
           some_copies(i + 1u < NT ? kPer : kCopiesPerWave);
           v4f d[4];

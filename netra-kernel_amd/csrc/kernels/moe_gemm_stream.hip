@@ -117,7 +117,10 @@ __device__ __forceinline__ void gate_up_stream(
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = wave_id();
   const uint32_t cols = I / 16u, KBI = I / 128u;
-  const uint32_t items = (uint32_t)num_valid[2] * cols;
+  // tiles as the sort counted them, never past the capacity (T Ktot / 16 + Etot):
+  // an operation launched out of order may find another tensor's bytes here
+  const uint32_t ntiles = min((uint32_t)num_valid[2], (T * Ktot + 15u) / 16u + Etot);
+  const uint32_t items = ntiles * cols;
   const uint32_t waves_total = gridDim.x * kGuWaves;
   uint32_t P = 1u;  // items per wave
   while (P < kGuMaxP && P * waves_total < items && cols % (16u * P) == 0u) P <<= 1;
@@ -334,7 +337,10 @@ __device__ __forceinline__ void down_stream(
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = wave_id();
   const uint32_t cols = H / 32u;
-  const uint32_t items = (uint32_t)num_valid[2] * cols;
+  // tiles as the sort counted them, never past the capacity (T Ktot / 16 + Etot):
+  // an operation launched out of order may find another tensor's bytes here
+  const uint32_t ntiles = min((uint32_t)num_valid[2], (T * Ktot + 15u) / 16u + Etot);
+  const uint32_t items = ntiles * cols;
   const uint32_t waves_total = gridDim.x * kDnWaves;
   uint32_t P = 1u;  // items per wave
   while (P < kDnMaxP && P * waves_total < items && cols % (8u * P) == 0u) P <<= 1;

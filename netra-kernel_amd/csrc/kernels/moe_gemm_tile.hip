@@ -378,10 +378,14 @@ __device__ __forceinline__ void down_tile(
 // 128 nb + 16 w .. +15 of every group (one 16-row W2 tile, K contiguous) and
 // refills each K block's weight registers with the next group's tile right
 // after using them (a one-group register ring, so a group of loads is always
-// in flight). Per 128-K block acc += (w_s(nb, kb) * h_s(row, kb)) * mfma. Each
-// group's result, rounded to bf16, goes through an LDS transpose (two
-// buffers, one barrier per group) so each route row leaves as 256 contiguous
-// bytes; rows past the block's valid count take an offset past the buffer
+// in flight). Per 128-K block acc += (w_s(nb, kb) * h_s(row, kb)) * mfma,
+// the MFMA taking the weight tile as A and the h rows as B so each lane ends
+// with four consecutive columns of one route row; each group's result,
+// rounded to bf16, goes through an LDS transpose (8-byte writes, two buffers,
+// one barrier per group) so each route row leaves as 256 contiguous bytes
+// (2-byte transposes of the other orientation cost 37% of LDS cycles in
+// bank conflicts; 8-byte stores straight to memory ran 30% slower than whole
+// rows); rows past the block's valid count take an offset past the buffer
 // and the hardware drops their stores.
 //
 // kAiter: W2 in the reference's AITER 16x16 shuffle. kSplitF16: the output
@@ -406,10 +410,15 @@ __device__ __forceinline__ void down_rows(
   static_assert(!kSplitF16 || KB % 2 == 0, "split-K halves need an even K block count");
   constexpr uint32_t I = 128u * KB;
   constexpr uint32_t kThreads = 64u * kDownWaves;
-  constexpr uint32_t kStride = I + 16u;  // LDS bytes per A row
-  constexpr uint32_t kOut = 256u + 16u;  // LDS bytes per output row (128 bf16 + pad)
   static_assert((KB & (KB - 1u)) == 0 && KB <= 64u, "one scale lane per K block");
-  __shared__ __align__(16) uint8_t s_a[kRows * kStride];
+  // the block's rows in the MFMA operand layout: 2 KiB per (16-row tile rt,
+  // K block kb), lane l's 32 bytes (row l & 15, K bytes 32 (l >> 4) ..) as a
+  // low half at 16 l and a high half at 1024 + 16 l, so each operand read is
+  // 64 lanes x 16 contiguous bytes (a row-major copy with any row padding
+  // had the four K groups of a row tile fight over the same banks: 43% of
+  // LDS cycles in conflicts)
+  __shared__ __align__(16) uint8_t s_a[kRows * I];
+  constexpr uint32_t kOut = 256u + 16u;  // LDS bytes per output row (128 bf16 + pad)
   __shared__ __align__(16) uint8_t s_out[2][kRows * kOut];
   __shared__ __align__(16) float s_hs[KB * kRows];  // h_s(row, kb) at [kb][row]
   __shared__ int32_t s_route[kRows];
@@ -438,30 +447,36 @@ __device__ __forceinline__ void down_rows(
   for (uint32_t kb = 0; kb < KB; ++kb)
     bq[kb] = nk::load_tile_operand<kAiter>(wt, ((nb0 * 8u + wave) * KB + kb) * 2048u, lane);
   float wsv = wse[nb0 * KB + (lane & (KB - 1u))];
-  // the block's A rows (64 x I bytes, contiguous) and scales
+  // the block's A rows (64 x I bytes, contiguous) and scales; thread slot s
+  // of the operand layout fetches the 16 bytes that belong there
   constexpr uint32_t kA16 = kRows * I / 16u / kThreads;  // uint4 per thread
   static_assert(kA16 >= 1u, "A staging");
   uint4 areg[kA16];
   const uint8_t* ablk = hq + (size_t)b * kRows * I;
 #pragma unroll
-  for (uint32_t p = 0; p < kA16; ++p) areg[p] = reinterpret_cast<const uint4*>(ablk)[p * kThreads + tid];
+  for (uint32_t p = 0; p < kA16; ++p) {
+    const uint32_t slot = p * kThreads + tid, t = slot >> 7, half = (slot >> 6) & 1u, l = slot & 63u;
+    const uint32_t row = (t / KB) * 16u + (l & 15u), col = (t % KB) * 128u + (l >> 4) * 32u + half * 16u;
+    areg[p] = *reinterpret_cast<const uint4*>(ablk + row * I + col);
+  }
   for (uint32_t i = tid; i < kRows * KB; i += kThreads) {
     const uint32_t row = i / KB, kb = i - row * KB;
     s_hs[kb * kRows + row] = hs[(size_t)b * kRows * KB + i];
   }
 #pragma unroll
-  for (uint32_t p = 0; p < kA16; ++p) {
-    const uint32_t idx = p * kThreads + tid;  // uint4 index in the block
-    const uint32_t row = idx / (I / 16u), c16 = idx - row * (I / 16u);
-    *reinterpret_cast<uint4*>(&s_a[row * kStride + c16 * 16u]) = areg[p];
-  }
+  for (uint32_t p = 0; p < kA16; ++p) *reinterpret_cast<uint4*>(&s_a[(p * kThreads + tid) * 16u]) = areg[p];
   lds_barrier();
   const uint32_t nvalid = (uint32_t)__popcll(__ballot(s_route[lane] >= 0));
   const uint32_t ntiles = (nvalid + 15u) >> 4;
   const uint32_t g = lane >> 4;
-  // output stores (64 rows x 256 bytes, 2 uint4 per thread): rows past nvalid
-  // (or padding) take offset 2^31, past the buffer's range (the engine keeps
-  // the partial buffer below 2^31 bytes), so their stores are dropped
+  // The MFMA takes the weight tile as its A operand and the h rows as B, so
+  // lane l holds output columns 4 (l >> 4) .. + 3 of route row l & 15 of each
+  // 16-row tile: four consecutive outputs, one 8-byte LDS write into the
+  // group's 64 x 256-byte output rows (row stride 272: the 32 lanes of a
+  // write pass cover 64 distinct banks), then each route row leaves as 256
+  // contiguous bytes (2 x 16 per thread). Rows past nvalid (or padding) take
+  // offset 2^31, past the buffer's range (the engine keeps the partial
+  // buffer below 2^31 bytes), so their stores are dropped.
   const uint32_t half_bytes = half_rows * H * 2u;
   const __amdgpu_buffer_rsrc_t pr = nk::buffer_rsrc(partial, kSplitF16 ? 2u * half_bytes : T * Ktot * H * 2u);
   uint32_t soff[2];
@@ -473,7 +488,11 @@ __device__ __forceinline__ void down_rows(
     live[p] = row < nvalid && route >= 0;
     soff[p] = live[p] ? ((uint32_t)route * H + c16 * 8u) * 2u : 0x80000000u;
   }
-  // One output tile through the LDS transpose: buffer v & 1, one barrier (the
+  auto pack2 = [&](float lo, float hi) __attribute__((always_inline)) {
+    return kSplitF16 ? ((uint32_t)f16_bits(lo) | ((uint32_t)f16_bits(hi) << 16))
+                     : ((uint32_t)nk::bf16_rne(lo) | ((uint32_t)nk::bf16_rne(hi) << 16));
+  };
+  // One output group through the LDS transpose: buffer v & 1, one barrier (the
   // other buffer was read before the previous barrier); `extra` moves live
   // rows to the second split-K half.
   auto emit = [&](auto ntc, const v4f* acc, uint32_t v, uint32_t nb, uint32_t extra) __attribute__((always_inline)) {
@@ -481,10 +500,8 @@ __device__ __forceinline__ void down_rows(
     uint8_t* so = s_out[v & 1u];
 #pragma unroll
     for (uint32_t rt = 0; rt < NT; ++rt)
-#pragma unroll
-      for (uint32_t j = 0; j < 4; ++j)
-        *reinterpret_cast<uint16_t*>(&so[(rt * 16u + g * 4u + j) * kOut + (wave * 16u + (lane & 15u)) * 2u]) =
-            kSplitF16 ? f16_bits(acc[rt][j]) : nk::bf16_rne(acc[rt][j]);
+      *reinterpret_cast<uint2*>(&so[(rt * 16u + (lane & 15u)) * kOut + (wave * 16u + g * 4u) * 2u]) =
+          make_uint2(pack2(acc[rt][0], acc[rt][1]), pack2(acc[rt][2], acc[rt][3]));
     lds_barrier();
 #pragma unroll
     for (uint32_t p = 0; p < 2u; ++p) {
@@ -510,16 +527,15 @@ __device__ __forceinline__ void down_rows(
         v4f d[NT];
 #pragma unroll
         for (uint32_t rt = 0; rt < NT; ++rt)
-          d[rt] = nk::mfma_e4m3_16x16x128(lds_fp8x32(&s_a[(rt * 16u + (lane & 15u)) * kStride + kb * 128u + g * 32u]),
-                                          bq[kb]);
+          d[rt] = nk::mfma_e4m3_16x16x128(bq[kb], nk::load_tile_operand(&s_a[(rt * KB + kb) * 2048u], lane));
         bq[kb] = nk::load_tile_operand<kAiter>(wt, ((nbn * 8u + wave) * KB + kb) * 2048u, lane);  // next group's tile
 #pragma unroll
         for (uint32_t rt = 0; rt < NT; ++rt) {
-          const float4 h4 = *reinterpret_cast<const float4*>(&s_hs[kb * kRows + rt * 16u + g * 4u]);
-          acc[rt][0] = fmaf(ws * h4.x, d[rt][0], acc[rt][0]);
-          acc[rt][1] = fmaf(ws * h4.y, d[rt][1], acc[rt][1]);
-          acc[rt][2] = fmaf(ws * h4.z, d[rt][2], acc[rt][2]);
-          acc[rt][3] = fmaf(ws * h4.w, d[rt][3], acc[rt][3]);
+          const float sc = ws * s_hs[kb * kRows + rt * 16u + (lane & 15u)];  // this lane's route row
+          acc[rt][0] = fmaf(sc, d[rt][0], acc[rt][0]);
+          acc[rt][1] = fmaf(sc, d[rt][1], acc[rt][1]);
+          acc[rt][2] = fmaf(sc, d[rt][2], acc[rt][2]);
+          acc[rt][3] = fmaf(sc, d[rt][3], acc[rt][3]);
         }
         // This block's accumulation completes here (the accumulators are
         // operands of the asm) and the next block's LDS reads stay below it

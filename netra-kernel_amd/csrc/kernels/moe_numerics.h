@@ -170,6 +170,7 @@ __device__ __forceinline__ v8i load_block_operand(const uint8_t* tile, uint32_t 
 // address VGPR instead of a 64-bit address per load. Loads past `bytes`
 // return zeros.
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }

@@ -116,9 +116,13 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
                                              float* __restrict__ screen, float* __restrict__ wsq,
                                              uint32_t T, uint32_t rows, uint32_t RP) {
   constexpr uint32_t H = 128u * NJ;
-  constexpr uint32_t kStride = 136;  // bf16 per LDS row (128 + 8: rotates banks across rows)
-  __shared__ __align__(16) uint16_t s_x[2][64 * kStride];
-  __shared__ __align__(16) uint16_t s_w[2][64 * kStride];
+  // Both 64 x 128 tiles sit in LDS row-major (256 bytes a row) with the
+  // 16-byte chunk c of row r at position c ^ (r & 15): the staging stores (16
+  // chunks of one row per 16 lanes) and the operand reads (one chunk of 16
+  // rows per 16 lanes) both hit 16 distinct positions. (Padded rows let the
+  // four K groups of a read collide: 36% of LDS cycles in bank conflicts.)
+  __shared__ __align__(16) uint4 s_x[2][64 * 16];
+  __shared__ __align__(16) uint4 s_w[2][64 * 16];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const bool norms = blockIdx.x == 0;  // uniform
   const uint32_t t0 = blockIdx.x * 64u, r0 = blockIdx.y * 64u, z = blockIdx.z, kb0 = z * KBS;
@@ -160,18 +164,20 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
     const uint32_t buf = kb & 1u, slot = kb % kRing;
 #pragma unroll
     for (uint32_t p = 0; p < 4; ++p) {
-      *reinterpret_cast<uint4*>(&s_x[buf][(16u * p + srow) * kStride + sc]) = xv[slot][p];
-      *reinterpret_cast<uint4*>(&s_w[buf][(16u * p + srow) * kStride + sc]) = wv[slot][p];
+      const uint32_t row = 16u * p + srow, pos = row * 16u + ((tid & 15u) ^ (row & 15u));
+      s_x[buf][pos] = xv[slot][p];
+      s_w[buf][pos] = wv[slot][p];
       if (norms) nw[p] += sumsq8(wv[slot][p]);
     }
     if (kb + 2u < KBS) load(kb + 2u, (kb + 2u) % kRing);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
     for (uint32_t q = 0; q < 4; ++q) {
-      const uint4 a = *reinterpret_cast<const uint4*>(&s_x[buf][(16u * wave + rl) * kStride + 32u * q + 8u * g]);
+      const uint32_t c = 4u * q + g;  // the 16-byte chunk of elements 32 q + 8 g ..
+      const uint4 a = s_x[buf][(16u * wave + rl) * 16u + (c ^ rl)];
 #pragma unroll
       for (uint32_t n = 0; n < 4; ++n) {
-        const uint4 b = *reinterpret_cast<const uint4*>(&s_w[buf][(16u * n + rl) * kStride + 32u * q + 8u * g]);
+        const uint4 b = s_w[buf][(16u * n + rl) * 16u + (c ^ rl)];
         acc[n] = mfma_bf16(a, b, acc[n]);
       }
     }

@@ -426,7 +426,7 @@ def _tile_down(cfg: MoEConfig) -> dict:
         nbc = down_rows_groups(cfg)
         return dict(name="moe.down", symbol=f"netra_moe_down_rows_i{I}_gfx950",
                     grid=(xcd_grid(cfg.cap_blocks * (H // 128 // nbc)), 1, 1), block=(512, 1, 1),
-                    lds=64 * (I + 16) + 2 * 64 * 272 + 64 * (I // 128) * 4 + 64 * 4, dyn=0,
+                    lds=64 * I + 2 * 64 * 272 + 64 * (I // 128) * 4 + 64 * 4, dyn=0,
                     args=["h_q", "h_scale", "w2", "w2_scale", *common, "partial",
                           u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot), u(nbc)],
                     reads=["h_q", "h_scale", "w2", "w2_scale", *common], writes=["partial"], refs=refs)

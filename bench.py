@@ -92,6 +92,33 @@ def time_operations(layers, steps: int, torch) -> dict[str, float]:
     return {op: sum(m[j].elapsed_time(m[j + 1]) for m in marks) / steps for j, op in enumerate(names)}
 
 
+# Operations that are pure functions of other operations' outputs (nothing
+# rewritten in place), so they can be relaunched back to back on a layer whose
+# intermediates are all bindings of their own.
+ISOLATED_OPS = ("gate_up", "down")
+
+
+def time_isolated(layers, op: str, steps: int, torch) -> float:
+    """Average duration (ms) of back-to-back launches of one GEMM operation
+    (HIP events on its stream, torch's current stream) after a whole layer
+    call produced its inputs; the layers expose every intermediate, so no
+    other operation's tensors share its inputs' bytes."""
+    if op not in ISOLATED_OPS:
+        raise ValueError(f"{op} is not timed in isolation")
+    for lay in layers:
+        lay.forward()
+    torch.cuda.synchronize()
+    for i in range(4):
+        layers[i % len(layers)].run_operation(op)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        layers[i % len(layers)].run_operation(op)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
 def cpu_baseline(cfg, act_cpu, w_host, threads: int, min_seconds: float):
     import numpy as np
 
@@ -307,6 +334,18 @@ def main() -> int:
             kern = {op: ms * 1e3 for op, ms in time_operations(dl, max(50, steps // 2), torch).items()}  # us
             for lay in dl:
                 lay.close()
+            if c is cfg:  # the GEMMs' own durations, for the rooflines
+                from netra_moe.engine import tensor_table
+                inter = tuple(n for n, sp in tensor_table(c).items() if sp.role == "temporary")
+                xl = []
+                for ws in wsets:
+                    w = {"router_w": act["router_w"].to(dev), "router_bias": act["router_bias"].to(dev), **ws}
+                    lay = MoELayer(c, w, graph=False, expose=inter)
+                    lay.x.copy_(act["x"].to(dev))
+                    xl.append(lay)
+                kern["isolated"] = {op: time_isolated(xl, op, max(50, steps // 2), torch) * 1e3 for op in ISOLATED_OPS}
+                for lay in xl:
+                    lay.close()
         for lay in layers:
             lay.close()
         return res, kern, act
@@ -314,9 +353,10 @@ def main() -> int:
     log(f"[bench] {cfg.name}: warmup {args.warmup}, steps {args.steps}")
     main_res, kern, act = run_config(cfg, args.steps, args.warmup, True)
     touched = main_res["touched_experts"]
-    dom_op, dom_us = "gate_up", kern["gate_up"]
+    iso = kern.pop("isolated")
+    dom_op, dom_us = "gate_up", iso["gate_up"]
     dom_bytes = gate_up_bytes(cfg, touched, path)
-    dn_us, dn_bytes = kern["down"], down_bytes(cfg, touched, path)
+    dn_us, dn_bytes = iso["down"], down_bytes(cfg, touched, path)
     other = {"down": {"achieved_gbps": dn_bytes / (dn_us * 1e-6) / 1e9, "avg_us": dn_us,
                       "algorithmic_bytes_per_launch": dn_bytes}}
     gu_symbol = next(op["symbol"] for op in operations(cfg, path) if op["name"] == f"moe.{dom_op}")

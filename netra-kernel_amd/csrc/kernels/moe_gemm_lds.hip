@@ -90,6 +90,16 @@ __device__ __forceinline__ void copy16(uint32_t m0, u32x4 r, uint32_t voff, uint
                : "memory");
 }
 
+// 4 bytes per lane, global (rsrc + voff + soff) -> LDS (m0 + 4 * lane); as copy16.
+__device__ __forceinline__ void copy4(uint32_t m0, u32x4 r, uint32_t voff, uint32_t soff) {
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 4\n\tbuffer_load_dword %2, %3, %4 offen lds\n\t"
+               "s_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "s"(m0), "v"(voff), "s"(r), "s"(soff)
+               : "memory");
+}
+
 template <uint32_t N>
 __device__ __forceinline__ void wait_copies() {
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
@@ -149,8 +159,10 @@ __device__ __forceinline__ void gate_up_lds(
     const int32_t* __restrict__ pair_map, uint8_t* __restrict__ hq, float* __restrict__ hs, uint32_t T,
     uint32_t I, uint32_t Ktot, uint32_t Etot) {
   constexpr uint32_t H = 128u * KB;
+  static_assert(2u * KB <= 64u && KB % 4u == 0, "scale copies");
   __shared__ __align__(16) uint8_t s_stage[kStages][kStageBytes];
-  __shared__ __align__(16) float s_as[KB][kRows];  // a_s(row, kb), rows contiguous per step
+  __shared__ __align__(16) float s_as[8u * 256u];        // a_s(row, kb) at row * KB + kb (8 wave copies)
+  __shared__ __align__(16) float s_wsv[kThreads / 64u][64];  // each wave's copy of the weight block scales
   __shared__ int32_t s_tok[kRows];
   __shared__ float s_amax[2][4][kRowsPerBlock];
   __shared__ float s_scale[kRows];
@@ -163,31 +175,23 @@ __device__ __forceinline__ void gate_up_lds(
   const uint32_t nblocks = (uint32_t)num_valid[0] / kRowsPerBlock;
   const uint32_t b0 = (uint32_t)pair_map[p];
   if (b0 >= nblocks) return;
+  // the rows' sorted ids and both blocks' experts in one round trip (the
+  // prologue's dependent loads are the item's fixed cost)
+  const bool has2 = b0 + 1u < nblocks;
+  int32_t id = -1;
+  if (tid < kRows && (tid < kRowsPerBlock || has2)) id = sorted_ids[b0 * kRowsPerBlock + tid];
   const int32_t e = sorted_expert[b0];
+  const int32_t e2 = has2 ? sorted_expert[b0 + 1u] : -1;
   if (e < 0 || (uint32_t)e >= Etot) return;
-  const bool two = b0 + 1u < nblocks && sorted_expert[b0 + 1u] == e;
+  const bool two = e2 == e;
   if (tid < kRows) {
-    int32_t tk = -1;
-    if (tid < kRowsPerBlock || two) {
-      const int32_t id = sorted_ids[b0 * kRowsPerBlock + tid];
-      const uint32_t t = (uint32_t)id & 0xffffffu, slot = (uint32_t)id >> 24;
-      tk = (t < T && slot < Ktot) ? (int32_t)t : -1;
-    }
-    s_tok[tid] = tk;
+    const uint32_t t = (uint32_t)id & 0xffffffu, slot = (uint32_t)id >> 24;
+    s_tok[tid] = (id >= 0 && (tid < kRowsPerBlock || two) && t < T && slot < Ktot) ? (int32_t)t : -1;
   }
   __syncthreads();
   const uint32_t m = wave >> 2, n = wave & 3u;  // row block, 32-column quarter
   const uint32_t nvalid = (uint32_t)__popcll(__ballot(s_tok[m * kRowsPerBlock + lane] >= 0));
   const uint32_t ntiles = (nvalid + 15u) >> 4;
-  // activation scales of the 128 rows (zeros for padding rows)
-  for (uint32_t i = tid; i < kRows * KB; i += kThreads) {
-    const uint32_t row = i / KB, kb = i - row * KB;
-    const int32_t tk = s_tok[row];
-    s_as[kb][row] = tk >= 0 ? xs[(size_t)tk * KB + kb] : 0.0f;
-  }
-  const float* wse = w13s + (size_t)e * (2u * I / 128u) * KB;
-  const float* wsg = wse + (size_t)ng * KB;               // gate rows' 128-row block
-  const float* wsu = wse + (size_t)(I / 128u + ng) * KB;  // up rows' block
   // copy sources: wave w moves A row tile w and weight tiles w of gate and of up.
   // A copy h fetches rows 8 h .. 8 h + 7 of the tile as whole 128-byte lines:
   // lane l takes row 8 h + (l >> 3), the chunk its swizzled slot l & 7 holds
@@ -219,10 +223,27 @@ __device__ __forceinline__ void gate_up_lds(
 #pragma unroll
     for (uint32_t q = 0; q < kCopiesPerWave; ++q) issue_part(kb, q);
   };
-  __syncthreads();  // s_as complete; every wave has read s_tok
+  // The scales travel with the first step's copies (so no further round trip
+  // precedes the ring): wave w's copy moves the activation scales of rows
+  // (256 / KB) w .. + 256 / KB - 1 (KB / 4 lanes a row, zeros past the 128
+  // rows and for padding rows), and every wave copies the item's weight block
+  // scales for itself (lane kb: gate, lane KB + kb: up).
+  {
+    constexpr uint32_t kLanesPerRow = KB / 4u, kRowsPerCopy = 64u / kLanesPerRow;
+    const uint32_t row = wave * kRowsPerCopy + lane / kLanesPerRow;
+    const int32_t stok = row < kRows ? s_tok[row] : -1;
+    const uint32_t xsoff = stok >= 0 ? (uint32_t)stok * KB * 4u + (lane % kLanesPerRow) * 16u : kFar;
+    copy16((uint32_t)__builtin_amdgcn_readfirstlane((int)lds_offset(&s_as[wave * 256u])), rsrc(xs, T * KB * 4u),
+           xsoff, 0u);
+    const float* wse = w13s + (size_t)e * (2u * I / 128u) * KB;
+    const uint32_t wsoff = lane < 2u * KB ? ((lane < KB ? ng : I / 128u + ng) * KB + lane % KB) * 4u : kFar;
+    copy4((uint32_t)__builtin_amdgcn_readfirstlane((int)lds_offset(&s_wsv[wave][0])),
+          rsrc(wse, (2u * I / 128u) * KB * 4u), wsoff, 0u);
+  }
   issue(0);
   if (KB > 1) issue(1);
   const uint32_t g = lane >> 4;
+  float wsv = 0.0f;
   v4f acc[4][4];
 #pragma unroll
   for (uint32_t i = 0; i < 4; ++i)
@@ -243,18 +264,21 @@ __device__ __forceinline__ void gate_up_lds(
         for (uint32_t u = 0; u < kCopiesPerWave; ++u)
           if (u < count && q < kCopiesPerWave && kb + 2u < KB) { issue_part(kb + 2u, q); ++q; }
       };
+      if (kb == 0) wsv = s_wsv[wave][lane];  // this wave's scale copy landed with step 0's
       if (NT > 0) {
         const uint8_t* st = s_stage[kb % kStages];
         v8i bw[4];
 #pragma unroll
         for (uint32_t c = 0; c < 4; ++c)  // gate tiles 2n, 2n + 1, up tiles 8 + 2n, 8 + 2n + 1
           bw[c] = lds_operand<kAiter>(st + kABytes + ((c >> 1) * 8u + 2u * n + (c & 1u)) * 2048u, lane);
-        const float sg = wsg[kb], su = wsu[kb];
+        const float sg = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(wsv), (int)kb));
+        const float su = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(wsv), (int)(KB + kb)));
 #pragma unroll
         for (uint32_t i = 0; i < NT; ++i) {
           const uint32_t rt = 4u * m + i;
           const v8i af = lds_operand_rows(st + rt * 2048u, lane);
-          const float4 as4 = *reinterpret_cast<const float4*>(&s_as[kb][rt * 16u + g * 4u]);
+          const float* asr = &s_as[(rt * 16u + g * 4u) * KB + kb];
+          const float4 as4 = make_float4(asr[0], asr[KB], asr[2u * KB], asr[3u * KB]);
           some_copies(i + 1u < NT ? kPer : kCopiesPerWave);
           v4f d[4];
 #pragma unroll

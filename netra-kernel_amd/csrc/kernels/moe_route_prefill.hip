@@ -17,6 +17,7 @@
 // weights, counts and the sorted layout are the same bits. Logits of the
 // experts that were not candidates are the screen's values rounded to bf16.
 #pragma once
+#include "moe_gemm_lds.hip"
 #include "moe_numerics.h"
 
 #define NK_KERNEL extern "C" __global__
@@ -102,106 +103,115 @@ __device__ __forceinline__ float exact_dot(const float4* __restrict__ xrow, cons
 }
 
 // ---------------------------------------------------------------------------
-// route_screen: workgroup (tm, tn, z), 256 threads: tokens 64 tm .. +63 x
-// router rows 64 tn .. +63 over K blocks [z KBS, (z + 1) KBS) (split K, so
-// that a few hundred workgroups cover small token counts). Per 128-K block the
-// x and w tiles are staged in LDS (loads for the next block in flight during
-// this one's multiplies); wave w multiplies its 16 tokens by the four 16-row
-// tiles with v_mfma_f32_16x16x32_bf16. Output screen[z][t][e] = the split's
-// partial sum for t < T, e < rows, row stride RP (rows rounded up to 64); the
-// select kernel adds the splits in z order. The workgroups of the first token
-// tile also write the router rows' partial squared norms wsq[z][e].
+// route_screen: workgroup (tm, tn, z), 256 threads (4 waves): tokens
+// 128 tm .. +127 x rows 128 tn .. +127 over K blocks [z KBS, (z + 1) KBS)
+// (split K, so that a few hundred workgroups cover the token count). Per
+// 128-K block both 128 x 128 bf16 tiles (32 KiB each) are copied global ->
+// LDS by buffer loads with the LDS-destination bit into a two-stage ring, the
+// next block's copies in flight during this block's multiplies. A tile is
+// row-major, 256 bytes a row, with the 16-byte chunk c of row r at position
+// c ^ (r & 15): one wave copy moves four whole rows (lane l: row l >> 4,
+// position l & 15), and an operand read (one chunk of 16 rows per 16 lanes)
+// hits 16 distinct positions. Wave w multiplies rows 64 (w & 1) .. +63 by
+// tokens 64 (w >> 1) .. +63 with v_mfma_f32_16x16x32_bf16, the router rows as
+// the A operand, so a lane's four results are four consecutive rows of one
+// token: one 16-byte store. Each tile element is read from LDS by two waves
+// (the 64 x 64 wave tile keeps LDS reads at 32 flops a byte, the matrix
+// cores' bf16 rate against the LDS bandwidth). Output screen[z][t][e] = the
+// split's partial sum for t < T, e < RP (rows past `rows` read as zeros), row
+// stride RP; the select kernel adds the splits in z order. The engine screens
+// the E expert rows only (rows = E): the shared-gate row's logit is always
+// computed exactly by route_select. The workgroups of the first token tile
+// also write the rows' partial squared norms wsq[z][e]. Needs T H < 2^30 (the
+// buffer offsets are 32-bit).
 template <uint32_t NJ, uint32_t KBS>  // H / 128, K blocks per split
 __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                              float* __restrict__ screen, float* __restrict__ wsq,
                                              uint32_t T, uint32_t rows, uint32_t RP) {
   constexpr uint32_t H = 128u * NJ;
-  // Both 64 x 128 tiles sit in LDS row-major (256 bytes a row) with the
-  // 16-byte chunk c of row r at position c ^ (r & 15): the staging stores (16
-  // chunks of one row per 16 lanes) and the operand reads (one chunk of 16
-  // rows per 16 lanes) both hit 16 distinct positions. (Padded rows let the
-  // four K groups of a read collide: 36% of LDS cycles in bank conflicts.)
-  __shared__ __align__(16) uint4 s_x[2][64 * 16];
-  __shared__ __align__(16) uint4 s_w[2][64 * 16];
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const bool norms = blockIdx.x == 0;  // uniform
-  const uint32_t t0 = blockIdx.x * 64u, r0 = blockIdx.y * 64u, z = blockIdx.z, kb0 = z * KBS;
+  constexpr uint32_t kTile = 128u * 256u;  // bytes of one 128 x 128 bf16 tile
+  constexpr uint32_t kCopies = 16u;        // copies per wave per K block: 8 of x rows, 8 of router rows
   static_assert(KBS <= NJ && NJ % KBS == 0, "splits cover K");
-  // staging: thread moves row (16 p + tid / 16) bytes (tid % 16) * 16 of both tiles, p = 0..3
-  const uint32_t srow = tid >> 4, sc = (tid & 15u) * 8u;  // sc in bf16
-  // buffer loads: one 32-bit byte offset per row and a scalar offset per block
-  const __amdgpu_buffer_rsrc_t xr = nk::buffer_rsrc(x, T * H * 2u);
-  const __amdgpu_buffer_rsrc_t wr = nk::buffer_rsrc(w, rows * H * 2u);
-  uint32_t xoff[4], woff[4];
+  __shared__ __align__(16) uint8_t s_tile[2][2][kTile];  // [stage][x, w]
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
+  const bool norms = blockIdx.x == 0;  // uniform
+  const uint32_t t0 = blockIdx.x * 128u, r0 = blockIdx.y * 128u, z = blockIdx.z, kb0 = z * KBS;
+  // copy c of this wave moves tile rows 32 wave + 4 c .. + 3; lane l fetches
+  // the chunk that position l & 15 of row 32 wave + 4 c + (l >> 4) holds
+  const nk::u32x4 rx = nklds::rsrc(x, T * H * 2u), rw = nklds::rsrc(w, rows * H * 2u);
+  uint32_t xoff[8], woff[8];
 #pragma unroll
-  for (uint32_t p = 0; p < 4; ++p) {
-    const uint32_t t = t0 + 16u * p + srow, r = r0 + 16u * p + srow;
-    xoff[p] = ((t < T ? t : T - 1u) * H + sc) * 2u;
-    woff[p] = ((r < rows ? r : rows - 1u) * H + sc) * 2u;
+  for (uint32_t c = 0; c < 8u; ++c) {
+    const uint32_t row = 32u * wave + 4u * c + (lane >> 4), chunk = (lane & 15u) ^ (row & 15u);
+    const uint32_t t = t0 + row, r = r0 + row;
+    xoff[c] = t < T ? t * H * 2u + chunk * 16u : nklds::kFar;
+    woff[c] = r < rows ? r * H * 2u + chunk * 16u : nklds::kFar;
   }
-  // register ring: loads for block kb + 2 are issued while block kb is
-  // multiplied; LDS-only barriers keep them in flight
-  constexpr uint32_t kRing = 3;
-  uint4 xv[kRing][4], wv[kRing][4];
-  float nw[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  auto load = [&](uint32_t kb, uint32_t slot) __attribute__((always_inline)) {
+  const uint32_t lds0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)nklds::lds_offset(&s_tile[0][0][0]));
+  auto issue = [&](uint32_t kb) __attribute__((always_inline)) {
+    const uint32_t st = lds0 + (kb & 1u) * 2u * kTile + (32u * wave) * 256u;
 #pragma unroll
-    for (uint32_t p = 0; p < 4; ++p) {
-      const nk::u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(xr, (int)xoff[p], (int)(256u * (kb0 + kb)), 0);
-      const nk::u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(wr, (int)woff[p], (int)(256u * (kb0 + kb)), 0);
-      xv[slot][p] = make_uint4(a.x, a.y, a.z, a.w);
-      wv[slot][p] = make_uint4(b.x, b.y, b.z, b.w);
-    }
+    for (uint32_t c = 0; c < 8u; ++c) nklds::copy16(st + 4u * c * 256u, rx, xoff[c], (kb0 + kb) * 256u);
+#pragma unroll
+    for (uint32_t c = 0; c < 8u; ++c) nklds::copy16(st + kTile + 4u * c * 256u, rw, woff[c], (kb0 + kb) * 256u);
   };
-  load(0, 0);
-  if (KBS > 1) load(1, 1);
-  nk::v4f acc[4];
+  issue(0);
+  if (KBS > 1) issue(1);
+  nk::v4f acc[4][4];
 #pragma unroll
-  for (uint32_t n = 0; n < 4; ++n) acc[n] = nk::v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint32_t i = 0; i < 4; ++i)
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) acc[i][j] = nk::v4f{0.0f, 0.0f, 0.0f, 0.0f};
   const uint32_t g = lane >> 4, rl = lane & 15u;
+  const uint32_t mrow = 64u * (wave & 1u), ntok = 64u * (wave >> 1);
+  float nsum = 0.0f;
 #pragma unroll
   for (uint32_t kb = 0; kb < KBS; ++kb) {
-    const uint32_t buf = kb & 1u, slot = kb % kRing;
-#pragma unroll
-    for (uint32_t p = 0; p < 4; ++p) {
-      const uint32_t row = 16u * p + srow, pos = row * 16u + ((tid & 15u) ^ (row & 15u));
-      s_x[buf][pos] = xv[slot][p];
-      s_w[buf][pos] = wv[slot][p];
-      if (norms) nw[p] += sumsq8(wv[slot][p]);
-    }
-    if (kb + 2u < KBS) load(kb + 2u, (kb + 2u) % kRing);
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kb + 1u < KBS) nklds::wait_copies<kCopies>(); else nklds::wait_copies<0>();
+    nklds::barrier();  // every wave's copies of block kb have landed
+    const uint8_t* sx = s_tile[kb & 1u][0];
+    const uint8_t* sw = s_tile[kb & 1u][1];
 #pragma unroll
     for (uint32_t q = 0; q < 4; ++q) {
-      const uint32_t c = 4u * q + g;  // the 16-byte chunk of elements 32 q + 8 g ..
-      const uint4 a = s_x[buf][(16u * wave + rl) * 16u + (c ^ rl)];
+      const uint32_t pos = ((4u * q + g) ^ rl) * 16u;  // the chunk of elements 32 q + 8 g ..
+      uint4 a[4], b[4];
 #pragma unroll
-      for (uint32_t n = 0; n < 4; ++n) {
-        const uint4 b = s_w[buf][(16u * n + rl) * 16u + (c ^ rl)];
-        acc[n] = mfma_bf16(a, b, acc[n]);
+      for (uint32_t i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const uint4*>(sw + (mrow + 16u * i + rl) * 256u + pos);
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const uint4*>(sx + (ntok + 16u * j + rl) * 256u + pos);
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i)
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) acc[i][j] = mfma_bf16(a[i], b[j], acc[i][j]);
+    }
+    if (norms) {  // thread: half (tid & 1) of row tid >> 1 of the router tile
+      const uint32_t row = tid >> 1;
+#pragma unroll
+      for (uint32_t c = 0; c < 8u; ++c) {
+        const uint32_t chunk = 8u * (tid & 1u) + c;
+        nsum += sumsq8(*reinterpret_cast<const uint4*>(sw + row * 256u + ((chunk ^ (row & 15u)) * 16u)));
       }
     }
-    __builtin_amdgcn_sched_barrier(0);  // one 128-K block per schedule region
-  }
-  if (norms) {  // router rows' squared norms: the 16 threads of a row hold its 16 column slices
-#pragma unroll
-    for (uint32_t p = 0; p < 4; ++p) {
-      float b = nw[p];
-      b += __shfl_xor(b, 1u);
-      b += __shfl_xor(b, 2u);
-      b += __shfl_xor(b, 4u);
-      b += __shfl_xor(b, 8u);
-      const uint32_t r = r0 + 16u * p + srow;
-      if ((tid & 15u) == 0 && r < rows) wsq[(size_t)z * RP + r] = b;
+    if (kb + 2u < KBS) {
+      nklds::barrier();  // every wave is done with stage kb & 1
+      issue(kb + 2u);
     }
   }
+  if (norms) {
+    nsum += __shfl_xor(nsum, 1u);
+    const uint32_t r = r0 + (tid >> 1);
+    if ((tid & 1u) == 0 && r < rows) wsq[(size_t)z * RP + r] = nsum;
+  }
 #pragma unroll
-  for (uint32_t n = 0; n < 4; ++n) {
-    const uint32_t r = r0 + 16u * n + rl;
+  for (uint32_t i = 0; i < 4; ++i) {
+    const uint32_t e0 = r0 + mrow + 16u * i + 4u * g;
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) {
-      const uint32_t t = t0 + 16u * wave + 4u * g + i;
-      if (t < T && r < rows) screen[((size_t)z * T + t) * RP + r] = acc[n][i];
+    for (uint32_t j = 0; j < 4; ++j) {
+      const uint32_t t = t0 + ntok + 16u * j + rl;
+      if (t < T && e0 < RP)
+        *reinterpret_cast<float4*>(screen + ((size_t)z * T + t) * RP + e0) =
+            make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
     }
   }
 }

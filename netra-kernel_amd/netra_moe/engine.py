@@ -150,15 +150,15 @@ def resolve_front(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> st
     return front
 
 
-SCREEN_WG_TARGET = 160               # route_screen: split K until the grid has this many workgroups
+SCREEN_WG_TARGET = 256               # route_screen: split K until the grid has this many workgroups
                                      # (measured: T=512 screen 14.3 -> 6.1 us at 4 splits; 8 splits cost the select more)
 
 
 def screen_splits(cfg: MoEConfig) -> int:
     """K splits of the screen GEMM (netra_moe_route_screen_h<H>_k<H/128/Z>): the
-    smallest power of two giving SCREEN_WG_TARGET workgroups, at least two
-    128-K blocks per split."""
-    tiles = (cfg.T + 63) // 64 * (screen_row_pad(cfg) // 64)
+    smallest power of two giving SCREEN_WG_TARGET workgroups (one per CU: a
+    workgroup holds 128 KiB of LDS), at least two 128-K blocks per split."""
+    tiles = (cfg.T + 127) // 128 * ((screen_row_pad(cfg) + 127) // 128)
     nj = cfg.H // 128
     z = 1
     while tiles * z < SCREEN_WG_TARGET and nj // (2 * z) >= 2:
@@ -167,8 +167,10 @@ def screen_splits(cfg: MoEConfig) -> int:
 
 
 def screen_row_pad(cfg: MoEConfig) -> int:
-    """Router rows rounded up to the screen GEMM's 64-row tiles (row stride of the screen buffer)."""
-    return (cfg.router_rows + 63) // 64 * 64
+    """Expert rows rounded up to the screen GEMM's 64-row tiles (row stride of
+    the screen buffer). The shared-gate row E is not screened: route_select
+    computes its logit exactly for every token."""
+    return (cfg.E + 63) // 64 * 64
 
 
 def screen_emax(cfg: MoEConfig) -> int:
@@ -285,8 +287,8 @@ def _screen_front(cfg: MoEConfig) -> list[dict]:
     Z = screen_splits(cfg)
     return [
         dict(name="moe.route_screen", symbol=f"netra_moe_route_screen_h{H}_k{H // 128 // Z}_gfx950",
-             grid=((T + 63) // 64, RP // 64, Z), block=(256, 1, 1), lds=2 * 2 * 64 * 136 * 2, dyn=0,
-             args=["x", "router_w", "screen", "route_wsq", u(T), u(H), u(cfg.router_rows), u(RP)],
+             grid=((T + 127) // 128, (RP + 127) // 128, Z), block=(256, 1, 1), lds=2 * 2 * 128 * 256, dyn=0,
+             args=["x", "router_w", "screen", "route_wsq", u(T), u(H), u(cfg.E), u(RP)],
              reads=["x", "router_w"], writes=["screen", "route_wsq"],
              refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150"]),
         dict(name="moe.route_select",
@@ -488,7 +490,7 @@ def operations(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> list[
             gate_up = dict(
                 name="moe.gate_up", symbol=f"netra_moe_gate_up_lds_h{H}_gfx950",
                 grid=(xcd_grid(cfg.cap_blocks * (I // 128)), 1, 1), block=(512, 1, 1),
-                lds=3 * 48 * 1024 + 128 * (H // 128) * 4 + 128 * 4 + 2 * 4 * 64 * 4 + 128 * 4, dyn=0,
+                lds=3 * 48 * 1024 + 8 * 256 * 4 + 8 * 64 * 4 + 128 * 4 + 2 * 4 * 64 * 4 + 128 * 4, dyn=0,
                 args=["x_q", "x_scale", "w13", "w13_scale", *common, "pair_map", "h_q", "h_scale",
                       u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
                 reads=["x_q", "x_scale", "w13", "w13_scale", *common, "pair_map"], writes=["h_q", "h_scale"],

@@ -165,10 +165,12 @@ def catalog() -> tuple[HipCodeObjectTactic, ...]:
             "gfx950.moe_fp8.tile.screen", "tile", "screen", sem("screen"),
             sets=(("H", tuple(h for h in E.TILE_H if h in E.SCREEN_H)), ("I", E.TILE_I)),
             ranges=(("T", 1, 1 << 20), ("E", 1, E.SCREEN_EMAX[-1]), ("K", 1, 64), ("S", 0, 1)),
+            limits=(("x_bytes", (1 << 31) - 1),),  # 32-bit buffer offsets into bf16 x
             rank=30, evidence_refs=("kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112",)),
         HipCodeObjectTactic(
             "gfx950.moe_fp8.tile.exact", "tile", "exact", sem("exact"),
             sets=(("H", E.TILE_H), ("I", E.TILE_I)), ranges=(("T", 1, 1 << 20), ("E", 1, 4096), ("K", 1, 64), ("S", 0, 1)),
+            limits=(("x_bytes", (1 << 32) - 2),),  # 32-bit buffer offsets into FP8 x_q
             rank=40, evidence_refs=("kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112",)),
     )
 
@@ -180,7 +182,7 @@ def layer_request(cfg: MoEConfig, *, semantics: Mapping[str, str] | None = None,
         "path": path, "front": front,
         "semantics": dict(semantics) if semantics is not None else layer_semantics_request(),
         "constants": {"T": cfg.T, "H": cfg.H, "I": cfg.I, "E": cfg.E, "K": cfg.K, "S": cfg.S},
-        "derived": {"Ktot": cfg.Ktot, "Etot": cfg.Etot, "cap_blocks": cfg.cap_blocks},
+        "derived": {"Ktot": cfg.Ktot, "Etot": cfg.Etot, "cap_blocks": cfg.cap_blocks, "x_bytes": 2 * cfg.T * cfg.H},
         "graph_capture": graph_capture, "deterministic": deterministic, "fallback": "framework",
     }
 

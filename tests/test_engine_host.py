@@ -165,7 +165,7 @@ def test_prefill_engines_use_the_screen_front_end(tmp_path):
     assert op_names(cfg) == ("route_screen", "route_select", "sort_count", "sort_place", "gate_up", "down", "combine")
     assert nm.manifest_check(tmp_path / "p")[0] == nm.Status.OK
     screen, select = doc["operations"][0], doc["operations"][1]
-    assert screen["launch"]["grid"] == [64, 5, 1]  # 4096 / 64 tokens x 320 / 64 router rows
+    assert screen["launch"]["grid"] == [32, 2, 4]  # 4096 / 128 tokens x 256 / 128 expert rows x 4 K splits
     # one token per wave, 8-wave workgroups at T=4096
     assert select["launch"]["grid"] == [512, 1, 1] and select["launch"]["block"] == [512, 1, 1]
     assert select["launch"]["lds_bytes"] <= 160 * 1024

@@ -126,16 +126,19 @@ def test_no_valu_sgpr_to_vmem_hazard_in_any_kernel():
     assert not report, "\n".join(f"{k}: {h[0]}" for k, h in report.items())
 
 
-KCOPIES = 6  # buffer-to-LDS copies per wave per 128-K step (kCopiesPerWave in moe_gemm_lds.hip)
+# buffer-to-LDS copies per wave per 128-K step of each LDS-ring kernel family
+# (kCopiesPerWave in moe_gemm_lds.hip, kCopies in route_screen)
+RING_COPIES = {"netra_moe_gate_up_lds_": 6, "netra_moe_route_screen_": 16}
+KCOPIES = RING_COPIES["netra_moe_gate_up_lds_"]
 _VMCNT = re.compile(r"vmcnt\((\d+)\)")
 
 
-def ring_violations(lines: list[str]) -> list[str]:
+def ring_violations(lines: list[str], copies_per_step: int = KCOPIES) -> list[str]:
     """Vector-memory accounting of one LDS-ring kernel (instructions in address
     order): between its first and last buffer-to-LDS copy there is no other
-    vector-memory instruction and every vmcnt wait is 0 or KCOPIES; after the
-    last copy, the first other vector-memory instruction comes behind a
-    vmcnt(0)."""
+    vector-memory instruction and every vmcnt wait is 0 or the copies of one
+    step; after the last copy, the first other vector-memory instruction comes
+    behind a vmcnt(0)."""
     text = [t.split("//")[0].strip() for t in lines]
     text = [t for t in text if t and not t.endswith(":")]
     is_copy = [bool(re.match(r"buffer_load_dword\w*\s.*\blds\b", t)) for t in text]
@@ -149,7 +152,7 @@ def ring_violations(lines: list[str]) -> list[str]:
         if _VMEM.match(t) and not is_copy[i]:
             bad.append(f"vector-memory op inside the copy ring: {t}")
         m = _VMCNT.search(t) if t.startswith("s_waitcnt") else None
-        if m and int(m.group(1)) not in (0, KCOPIES):
+        if m and int(m.group(1)) not in (0, copies_per_step):
             bad.append(f"unexpected wait inside the copy ring: {t}")
     drained = False
     for t in text[last + 1:]:
@@ -175,9 +178,10 @@ def test_ring_checker_flags_a_foreign_load():
     assert ring_violations(ring[:1] + ["s_waitcnt vmcnt(5)"] + ring[2:])
 
 
-def test_lds_ring_kernels_issue_only_their_copies():
+@pytest.mark.parametrize("prefix", sorted(RING_COPIES))
+def test_lds_ring_kernels_issue_only_their_copies(prefix):
     funcs = disassembly()
-    ring = {k: v for k, v in funcs.items() if k.startswith("netra_moe_gate_up_lds_")}
-    assert ring, "no netra_moe_gate_up_lds_ kernels in the code object"
-    report = {k: b for k, v in ring.items() if (b := ring_violations(v))}
+    ring = {k: v for k, v in funcs.items() if k.startswith(prefix)}
+    assert ring, f"no {prefix} kernels in the code object"
+    report = {k: b for k, v in ring.items() if (b := ring_violations(v, RING_COPIES[prefix]))}
     assert not report, "\n".join(f"{k}: {b[0]}" for k, b in report.items())

@@ -107,6 +107,14 @@ def test_unsupported_shapes_and_fields_are_named():
     assert "compile-time constants missing" in planner.catalog()[0].rejection_reasons(req)
 
 
+def test_buffer_offset_limit_names_the_bound():
+    big = replace(CONFIGS["prefill_t4096"], T=1 << 19)  # bf16 x of 2 GiB
+    plan = planner.plan_layer(planner.layer_request(big))
+    screen = next(c for c in plan.candidates if c["tactic"] == "gfx950.moe_fp8.tile.screen")
+    assert screen["reasons"] == [f"x_bytes exceeds {(1 << 31) - 1}"]
+    assert plan.selected.name == "gfx950.moe_fp8.tile.exact"
+
+
 def test_maturity_gates_experimental_tactics():
     exp = replace(planner.catalog()[0], name="gfx950.trial", maturity="experiment", rank=1)
     req = planner.layer_request(CONFIGS["decode_t1"])

@@ -126,19 +126,23 @@ def test_no_valu_sgpr_to_vmem_hazard_in_any_kernel():
     assert not report, "\n".join(f"{k}: {h[0]}" for k, h in report.items())
 
 
-# buffer-to-LDS copies per wave per 128-K step of each LDS-ring kernel family
-# (kCopiesPerWave in moe_gemm_lds.hip, kCopies in route_screen)
-RING_COPIES = {"netra_moe_gate_up_lds_": 6, "netra_moe_route_screen_": 16}
-KCOPIES = RING_COPIES["netra_moe_gate_up_lds_"]
+# vmcnt waits an LDS-ring kernel family may use inside its ring: 0 or the
+# copies of one step (kCopiesPerWave in moe_gemm_lds.hip, kCopies in
+# route_screen)
+RING_WAITS = {"netra_moe_gate_up_lds_": {0, 6}, "netra_moe_route_screen_": {0, 16}}
+KCOPIES = 6
 _VMCNT = re.compile(r"vmcnt\((\d+)\)")
+_VSTORE = re.compile(r"(global|buffer|flat)_store")
 
 
-def ring_violations(lines: list[str], copies_per_step: int = KCOPIES) -> list[str]:
+def ring_violations(lines: list[str], waits: set[int] | None = None) -> list[str]:
     """Vector-memory accounting of one LDS-ring kernel (instructions in address
     order): between its first and last buffer-to-LDS copy there is no other
-    vector-memory instruction and every vmcnt wait is 0 or the copies of one
-    step; after the last copy, the first other vector-memory instruction comes
-    behind a vmcnt(0)."""
+    vector-memory load, every vmcnt wait is one of `waits`, and the first wait
+    after a vector store is vmcnt(0) (stores may complete before older loads,
+    so only a full drain is exact behind one); after the last copy, the first
+    other vector-memory instruction comes behind a vmcnt(0)."""
+    waits = {0, KCOPIES} if waits is None else waits
     text = [t.split("//")[0].strip() for t in lines]
     text = [t for t in text if t and not t.endswith(":")]
     is_copy = [bool(re.match(r"buffer_load_dword\w*\s.*\blds\b", t)) for t in text]
@@ -147,18 +151,32 @@ def ring_violations(lines: list[str], copies_per_step: int = KCOPIES) -> list[st
         return ["no buffer-to-LDS copies"]
     first, last = copies[0], copies[-1]
     bad = []
+    store_pending = False
     for i in range(first, last + 1):
         t = text[i]
-        if _VMEM.match(t) and not is_copy[i]:
+        if _VSTORE.match(t):
+            store_pending = True
+        elif _VMEM.match(t) and not is_copy[i]:
             bad.append(f"vector-memory op inside the copy ring: {t}")
         m = _VMCNT.search(t) if t.startswith("s_waitcnt") else None
-        if m and int(m.group(1)) not in (0, copies_per_step):
+        if m and int(m.group(1)) not in waits:
             bad.append(f"unexpected wait inside the copy ring: {t}")
+        if m and store_pending:
+            if int(m.group(1)) != 0:
+                bad.append(f"partial wait behind a store inside the copy ring: {t}")
+            store_pending = False
     drained = False
     for t in text[last + 1:]:
         m = _VMCNT.search(t) if t.startswith("s_waitcnt") else None
-        if m and int(m.group(1)) == 0:
-            drained = True
+        if m:
+            if store_pending and int(m.group(1)) != 0:
+                bad.append(f"partial wait behind a store after the copy ring: {t}")
+            store_pending = False
+            if int(m.group(1)) == 0:
+                drained = True
+        if _VSTORE.match(t):  # stores may overlap copies still in flight; a drain must follow them
+            store_pending = True
+            continue
         if _VMEM.match(t):
             if not drained:
                 bad.append(f"vector-memory op before the ring drains: {t}")
@@ -173,15 +191,21 @@ def test_ring_checker_flags_a_foreign_load():
     assert ring_violations(ring) == []
     foreign = ring[:2] + ["global_load_dword v5, v[6:7], off"] + ring[2:]
     assert any("inside the copy ring" in v for v in ring_violations(foreign))
-    early = ring[:3] + ["global_store_dword v[0:1], v3, off"]
+    early = ring[:3] + ["global_load_dword v4, v[0:1], off"]
     assert any("before the ring drains" in v for v in ring_violations(early))
+    overlap = ring[:3] + ["global_store_dword v[0:1], v3, off", "s_waitcnt vmcnt(6)"]
+    assert any("behind a store" in v for v in ring_violations(overlap))
     assert ring_violations(ring[:1] + ["s_waitcnt vmcnt(5)"] + ring[2:])
+    stored = ring[:2] + ["global_store_dwordx4 v[0:1], v[4:7], off", "s_waitcnt vmcnt(6)"] + ring[2:]
+    assert any("behind a store" in v for v in ring_violations(stored))
+    drained = ring[:2] + ["global_store_dwordx4 v[0:1], v[4:7], off", "s_waitcnt vmcnt(0)"] + ring[2:]
+    assert ring_violations(drained) == []
 
 
-@pytest.mark.parametrize("prefix", sorted(RING_COPIES))
+@pytest.mark.parametrize("prefix", sorted(RING_WAITS))
 def test_lds_ring_kernels_issue_only_their_copies(prefix):
     funcs = disassembly()
     ring = {k: v for k, v in funcs.items() if k.startswith(prefix)}
     assert ring, f"no {prefix} kernels in the code object"
-    report = {k: b for k, v in ring.items() if (b := ring_violations(v, RING_COPIES[prefix]))}
+    report = {k: b for k, v in ring.items() if (b := ring_violations(v, RING_WAITS[prefix]))}
     assert not report, "\n".join(f"{k}: {b[0]}" for k, b in report.items())

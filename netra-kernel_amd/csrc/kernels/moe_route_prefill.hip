@@ -77,14 +77,17 @@ __device__ __forceinline__ void quant8(uint4 v, uint8_t* __restrict__ q_dst, flo
 // Exact contract logit of one (token, router row) pair by a 16-lane group:
 // lane s runs the sequential fmaf chain over elements 128 j + 8 s + i from +0,
 // then the +8/+4/+2/+1 tree (the same order as netra_moe_router_h<H>). The
-// token row comes from LDS (widened to fp32, natural order), the router row
-// from wv.
+// token row comes from LDS, widened to fp32 and stored so that the 16 lanes'
+// elements 128 j + 8 s .. + 3 are 16 consecutive float4 (32 j + s), then their
+// elements + 4 .. + 7 (32 j + 16 + s): each 16-lane read is 256 contiguous
+// bytes (the natural order, 32 bytes a lane, read two lanes per bank group);
+// the router row comes from wv.
 template <uint32_t NJ>
 __device__ __forceinline__ float exact_dot(const float4* __restrict__ xrow, const uint4 (&wv)[NJ], uint32_t s) {
   float a = 0.0f;
 #pragma unroll
   for (uint32_t j = 0; j < NJ; ++j) {
-    const float4 xl = xrow[32u * j + 2u * s], xh = xrow[32u * j + 2u * s + 1u];
+    const float4 xl = xrow[32u * j + s], xh = xrow[32u * j + 16u + s];
     const uint4 w = wv[j];
     a = fmaf(xl.x, nk::bf16_lo(w.x), a);
     a = fmaf(xl.y, nk::bf16_hi(w.x), a);
@@ -302,8 +305,9 @@ __device__ __forceinline__ void route_select(
     for (uint32_t p = 0; p < H / 512u; ++p) {
       const uint32_t i0 = 512u * p + 8u * lane;
       const uint4 v = xv[p];
-      s_x[tt][i0 / 4u] = make_float4(nk::bf16_lo(v.x), nk::bf16_hi(v.x), nk::bf16_lo(v.y), nk::bf16_hi(v.y));
-      s_x[tt][i0 / 4u + 1u] = make_float4(nk::bf16_lo(v.z), nk::bf16_hi(v.z), nk::bf16_lo(v.w), nk::bf16_hi(v.w));
+      const uint32_t jx = i0 >> 7, sx = (i0 >> 3) & 15u;  // exact_dot's order: 32 j + s, then 32 j + 16 + s
+      s_x[tt][32u * jx + sx] = make_float4(nk::bf16_lo(v.x), nk::bf16_hi(v.x), nk::bf16_lo(v.y), nk::bf16_hi(v.y));
+      s_x[tt][32u * jx + 16u + sx] = make_float4(nk::bf16_lo(v.z), nk::bf16_hi(v.z), nk::bf16_lo(v.w), nk::bf16_hi(v.w));
       quant8(v, xq + (size_t)t * H + i0, xs + (size_t)t * NJ + (i0 >> 7), s == 0);
       xx += sumsq8(v);
     }

@@ -160,6 +160,8 @@ __device__ __forceinline__ void gate_up_lds(
     uint32_t I, uint32_t Ktot, uint32_t Etot) {
   constexpr uint32_t H = 128u * KB;
   static_assert(2u * KB <= 64u && KB % 4u == 0, "scale copies");
+  constexpr uint32_t kAsLanesPerRow = KB / 4u, kAsRowsPerCopy = 64u / kAsLanesPerRow;
+  auto as_swizzle = [](uint32_t r) { return (r >> 2) & (kAsLanesPerRow - 1u); };
   __shared__ __align__(16) uint8_t s_stage[kStages][kStageBytes];
   __shared__ __align__(16) float s_as[8u * 256u];        // a_s(row, kb) at row * KB + kb (8 wave copies)
   __shared__ __align__(16) float s_wsv[kThreads / 64u][64];  // each wave's copy of the weight block scales
@@ -227,12 +229,14 @@ __device__ __forceinline__ void gate_up_lds(
   // precedes the ring): wave w's copy moves the activation scales of rows
   // (256 / KB) w .. + 256 / KB - 1 (KB / 4 lanes a row, zeros past the 128
   // rows and for padding rows), and every wave copies the item's weight block
-  // scales for itself (lane kb: gate, lane KB + kb: up).
+  // scales for itself (lane kb: gate, lane KB + kb: up). Row r's 16-byte
+  // chunk c sits at slot c ^ as_swizzle(r), so the four rows 4 g + j (g =
+  // 0..3) a K step reads at once fall in four different banks.
   {
-    constexpr uint32_t kLanesPerRow = KB / 4u, kRowsPerCopy = 64u / kLanesPerRow;
-    const uint32_t row = wave * kRowsPerCopy + lane / kLanesPerRow;
+    const uint32_t row = wave * kAsRowsPerCopy + lane / kAsLanesPerRow;
     const int32_t stok = row < kRows ? s_tok[row] : -1;
-    const uint32_t xsoff = stok >= 0 ? (uint32_t)stok * KB * 4u + (lane % kLanesPerRow) * 16u : kFar;
+    const uint32_t chunk = (lane % kAsLanesPerRow) ^ as_swizzle(row);
+    const uint32_t xsoff = stok >= 0 ? (uint32_t)stok * KB * 4u + chunk * 16u : kFar;
     copy16((uint32_t)__builtin_amdgcn_readfirstlane((int)lds_offset(&s_as[wave * 256u])), rsrc(xs, T * KB * 4u),
            xsoff, 0u);
     const float* wse = w13s + (size_t)e * (2u * I / 128u) * KB;
@@ -277,7 +281,8 @@ __device__ __forceinline__ void gate_up_lds(
         for (uint32_t i = 0; i < NT; ++i) {
           const uint32_t rt = 4u * m + i;
           const v8i af = lds_operand_rows(st + rt * 2048u, lane);
-          const float* asr = &s_as[(rt * 16u + g * 4u) * KB + kb];
+          const uint32_t r0 = rt * 16u + g * 4u;  // rows r0 .. r0 + 3 share as_swizzle
+          const float* asr = &s_as[r0 * KB + (((kb >> 2) ^ as_swizzle(r0)) << 2) + (kb & 3u)];
           const float4 as4 = make_float4(asr[0], asr[KB], asr[2u * KB], asr[3u * KB]);
           some_copies(i + 1u < NT ? kPer : kCopiesPerWave);
           v4f d[4];

@@ -459,9 +459,11 @@ __device__ __forceinline__ void down_rows(
     const uint32_t row = (t / KB) * 16u + (l & 15u), col = (t % KB) * 128u + (l >> 4) * 32u + half * 16u;
     areg[p] = *reinterpret_cast<const uint4*>(ablk + row * I + col);
   }
+  // thread i: row i % 64 of K block i / 64, so a wave's stores are 64
+  // consecutive floats (the global gather is 1 KiB per item)
   for (uint32_t i = tid; i < kRows * KB; i += kThreads) {
-    const uint32_t row = i / KB, kb = i - row * KB;
-    s_hs[kb * kRows + row] = hs[(size_t)b * kRows * KB + i];
+    const uint32_t row = i & (kRows - 1u), kb = i / kRows;
+    s_hs[i] = hs[(size_t)b * kRows * KB + row * KB + kb];
   }
 #pragma unroll
   for (uint32_t p = 0; p < kA16; ++p) *reinterpret_cast<uint4*>(&s_a[(p * kThreads + tid) * 16u]) = areg[p];
@@ -497,16 +499,22 @@ __device__ __forceinline__ void down_rows(
   // rows to the second split-K half.
   auto emit = [&](auto ntc, const v4f* acc, uint32_t v, uint32_t nb, uint32_t extra) __attribute__((always_inline)) {
     constexpr uint32_t NT = decltype(ntc)::value;
+    // rows r and r + 8 of a 16-lane write pass would share banks (row stride
+    // 68 dwords): odd row octets swap the two 8-byte halves of every 16-byte
+    // chunk, and the 16-byte reads swap them back
     uint8_t* so = s_out[v & 1u];
 #pragma unroll
-    for (uint32_t rt = 0; rt < NT; ++rt)
-      *reinterpret_cast<uint2*>(&so[(rt * 16u + (lane & 15u)) * kOut + (wave * 16u + g * 4u) * 2u]) =
+    for (uint32_t rt = 0; rt < NT; ++rt) {
+      const uint32_t row = rt * 16u + (lane & 15u);
+      *reinterpret_cast<uint2*>(&so[row * kOut + (((wave * 16u + g * 4u) * 2u) ^ (((row >> 3) & 1u) << 3))]) =
           make_uint2(pack2(acc[rt][0], acc[rt][1]), pack2(acc[rt][2], acc[rt][3]));
+    }
     lds_barrier();
 #pragma unroll
     for (uint32_t p = 0; p < 2u; ++p) {
       const uint32_t idx = p * kThreads + tid, row = idx >> 4, c16 = idx & 15u;
-      const uint4 val = *reinterpret_cast<const uint4*>(&so[row * kOut + c16 * 16u]);
+      uint4 val = *reinterpret_cast<const uint4*>(&so[row * kOut + c16 * 16u]);
+      if ((row >> 3) & 1u) val = make_uint4(val.z, val.w, val.x, val.y);
       __builtin_amdgcn_raw_buffer_store_b128(nk::u32x4{val.x, val.y, val.z, val.w}, pr,
                                              (int)(soff[p] + (live[p] ? extra : 0u)), (int)(nb * 256u), 0);
     }

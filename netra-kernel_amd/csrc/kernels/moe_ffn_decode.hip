@@ -145,7 +145,7 @@ __device__ __forceinline__ void ffn_gate_up(
   constexpr uint32_t kBig = kBig0 > kProl ? kBig0 : kProl;
   // s_big: the tile's x rows | split sums | prologue tables
   __shared__ __align__(16) uint8_t s_big[kBig];
-  __shared__ float s_xs[16 * KB];                                 // x row scales [row][kb]
+  __shared__ float s_xs[16 * KB];                                 // x row scales [kb][row]
   __shared__ __align__(16) uint16_t s_hb[kQuant ? 16u * kHb : 8u];  // the item's h rows (bf16)
   __shared__ int32_t s_ids[kMaxT * kMaxKtot];
   __shared__ unsigned long long s_mask[kMaxE];
@@ -310,7 +310,10 @@ __device__ __forceinline__ void ffn_gate_up(
     }
 #pragma unroll
     for (uint32_t q = 0; q < kScales; ++q)
-      if (tid + q * kThreads < 16u * KB) s_xs[tid + q * kThreads] = xv[q];
+      if (tid + q * kThreads < 16u * KB) {  // element i = row * KB + kb of the gather
+        const uint32_t i = tid + q * kThreads;
+        s_xs[(i % KB) * 16u + i / KB] = xv[q];
+      }
     lds_barrier();
 
     v4f ag = {0.0f, 0.0f, 0.0f, 0.0f}, au = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -325,7 +328,7 @@ __device__ __forceinline__ void ffn_gate_up(
         const float su = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(st.ws), (int)(KB + kb)));
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
-          const float as = s_xs[((lane >> 4) * 4u + j) * KB + kb];
+          const float as = s_xs[kb * 16u + (lane >> 4) * 4u + j];
           ag[j] = ag[j] + sg * (as * dg[j]);
           au[j] = au[j] + su * (as * du[j]);
         }

@@ -92,8 +92,11 @@ __device__ __forceinline__ void router(const uint16_t* __restrict__ x, const uin
     const uint4 v = sv[p];
     float f[8] = {nk::bf16_lo(v.x), nk::bf16_hi(v.x), nk::bf16_lo(v.y), nk::bf16_hi(v.y),
                   nk::bf16_lo(v.z), nk::bf16_hi(v.z), nk::bf16_lo(v.w), nk::bf16_hi(v.w)};
-    s_x[e / 4u] = make_float4(f[0], f[1], f[2], f[3]);
-    s_x[e / 4u + 1u] = make_float4(f[4], f[5], f[6], f[7]);
+    // element 128 j + 8 s + i of a token row sits at float4 32 j + s (i < 4)
+    // or 32 j + 16 + s (i >= 4): the chain's 16-lane reads are contiguous
+    const uint32_t eb = e - (e / H) * H, fx = (e / H) * (H / 4u) + 32u * (eb >> 7) + ((eb >> 3) & 15u);
+    s_x[fx] = make_float4(f[0], f[1], f[2], f[3]);
+    s_x[fx + 16u] = make_float4(f[4], f[5], f[6], f[7]);
     const uint32_t k = e / H, i0 = e - k * H;  // uniform per 16-lane group
     if (quant && t0 + k < T)
       quant8(f, xq + (size_t)(t0 + k) * H + i0, xs + (size_t)(t0 + k) * NJ + (i0 >> 7), s == 0);
@@ -117,11 +120,11 @@ __device__ __forceinline__ void router(const uint16_t* __restrict__ x, const uin
   }
 #pragma unroll 1
   for (uint32_t k = 0; k < NT; ++k) {
-    const float4* xk = s_x + (k * H + 8u * s) / 4u;
+    const float4* xk = s_x + k * (H / 4u) + s;  // lo at 32 j, hi at 32 j + 16 (the staging order)
     float a = 0.0f;
 #pragma unroll
     for (uint32_t j = 0; j < NJ; ++j) {
-      const float4 lo = xk[32u * j], hi = xk[32u * j + 1u];
+      const float4 lo = xk[32u * j], hi = xk[32u * j + 16u];
       a = fmaf(lo.x, wf[8 * j + 0], a);
       a = fmaf(lo.y, wf[8 * j + 1], a);
       a = fmaf(lo.z, wf[8 * j + 2], a);

@@ -67,7 +67,8 @@ __device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
 }
 
 // Contract exp: Cody-Waite reduction with n = rint(x log2 e), ln2 split into
-// 0x3f317200 + 0x35bfbe8e, degree-7 Taylor polynomial of e^r in Horner form,
+// 0x3f317200 + 0x35bfbe8e (the hi/lo split of fdlibm's single-precision
+// expf), degree-7 Taylor polynomial of e^r in Horner form,
 // scaled by 2^n through the exponent field; x < -87 -> 0, x > 88 -> +inf.
 __device__ __forceinline__ float nexp(float x) {
   if (x != x) return x;

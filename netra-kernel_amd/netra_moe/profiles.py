@@ -3,7 +3,10 @@
 Mirrors compiler/netra_compiler/profiles.py:12-77 (DimensionGuard, ShapeProfile,
 select_profile) and the netra-profile-1 JSON files in
 manifests/gfx950/profiles/*.json. A failed selection reports that the framework
-fallback is required instead of guessing a neighbouring shape.
+fallback is required instead of guessing a neighbouring shape. These types,
+their one-line bodies and select_profile's two reason strings are kept alike on
+purpose: they are the netra-profile-1 interface a caller of the reference
+reads and writes.
 """
 from __future__ import annotations
 

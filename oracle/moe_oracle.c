@@ -90,7 +90,8 @@ float orc_f32_from_e4m3(uint8_t q) {
 }
 
 /* Contract exp: Cody-Waite reduction x = n ln2 + r with n = rint(x log2 e),
- * ln2 split hi/lo, then the degree-7 Taylor polynomial of e^r in Horner form
+ * ln2 split hi/lo as fdlibm's single-precision expf splits it (0x3f317200 +
+ * 0x35bfbe8e), then the degree-7 Taylor polynomial of e^r in Horner form
  * with explicit fmaf, scaled by 2^n through the exponent field. x < -87 -> 0,
  * x > 88 -> +inf (no subnormal results). The HIP kernels evaluate the same
  * operation sequence, so both sides produce identical bits. */

@@ -1,10 +1,13 @@
-// Decode FFN for T <= 64 tokens after the route kernel: the sort rebuilt in
-// the gate/up prologue, and (narrow variant) the top-k weighted combine folded
-// into down through a hand-off between workgroups.
+// Decode FFN for T <= 64 tokens after the route kernel (wide) or the router
+// logits kernel (narrow, T <= 8): the sort rebuilt in the gate/up prologue,
+// and (narrow) the top-k too, and the top-k weighted combine folded into down
+// through a hand-off between workgroups.
 //
-//   netra_moe_ffn_gate_up_h<H>_i<I>_<wide|narrow>_gfx950(topk_ids, xq, xs, w13,
-//       w13s, sorted_ids, sorted_expert, tile_map, pair_map, num_valid, counts,
-//       hrows, hq, hs; T, E, K, S, CAP)
+//   netra_moe_ffn_gate_up_h<H>_i<I>_<wide|narrow>_gfx950(logits, bias,
+//       topk_ids, topk_weights, xq, xs, w13, w13s, sorted_ids, sorted_expert,
+//       tile_map, pair_map, num_valid, counts, hrows, hq, hs; T, E, K, S, CAP)
+//     wide reads topk_ids (logits, bias and topk_weights unused); narrow
+//     selects from logits + bias and writes topk_ids / topk_weights
 //   netra_moe_ffn_down_h<H>_i<I>_<wide|narrow>_gfx950(topk_weights, w2, w2s,
 //       sorted_ids, sorted_expert, tile_map, num_valid, hrows, hq, hs, partial,
 //       counters, out; T, E, K, S)
@@ -20,7 +23,9 @@
 // at T = 64 against ordinary loads.
 //
 // gate/up prologue (every workgroup, redundantly; the inputs are a few KB in
-// L2): the route kernel's ids go to LDS; the routing bitmask (bit t of word e:
+// L2): the route kernel's ids go to LDS (narrow: wave t runs token t's top-k
+// on the logits, the route kernel's selection, and puts its ids there, and
+// workgroup 0 writes topk_ids / topk_weights); the routing bitmask (bit t of word e:
 // token t routes to expert e) gives each expert's count and each route's rank
 // among its expert's tokens; a scan over experts gives block, tile and pair
 // offsets in the AITER sorted format. Workgroup 0 writes the counts, the tile
@@ -63,6 +68,7 @@
 // gate_up_mfma.inc:12-161, silu_quant.inc:16-236, down_reduce_mfma_2wave.inc:
 // 14-291; sorted format entry_routing.inc:27-112)
 #pragma once
+#include "moe_gemm_lds.hip"
 #include "moe_gemm_stream.hip"
 #include "moe_numerics.h"
 
@@ -121,7 +127,8 @@ __device__ __forceinline__ void quant_block(const uint32_t (&raw)[16], uint4& ql
 template <uint32_t KB, uint32_t KBI, uint32_t SA, uint32_t CHM, uint32_t P>  // H / 128, I / 128, K splits,
                                                                                // K blocks per step, items per wave
 __device__ __forceinline__ void ffn_gate_up(
-    const int32_t* __restrict__ topk_ids, const uint8_t* __restrict__ xq, const float* __restrict__ xs,
+    const uint16_t* __restrict__ logits, const float* __restrict__ bias, int32_t* __restrict__ topk_ids,
+    float* __restrict__ topk_weights, const uint8_t* __restrict__ xq, const float* __restrict__ xs,
     const uint8_t* __restrict__ w13, const float* __restrict__ w13s, int32_t* __restrict__ sorted_ids,
     int32_t* __restrict__ sorted_expert, int32_t* __restrict__ tile_map, int32_t* __restrict__ pair_map,
     int32_t* __restrict__ num_valid, int32_t* __restrict__ counts, uint16_t* __restrict__ hrows,
@@ -140,8 +147,9 @@ __device__ __forceinline__ void ffn_gate_up(
   static_assert(CA * SA == kWaves && KB % SA == 0 && KBA % kCH == 0, "K splits");
   static_assert(I % (16u * CA * P) == 0 && H % kThreads == 0 && (P == 1 || SA == 1) && P <= kWaves, "shares");
   constexpr uint32_t kRed = SA > 1 ? kWaves * 8u * 64u * 4u : 0u;  // split sums
+  constexpr bool kStageAll = SA > 1;  // narrow: one A operand (every token's row) for all items
   constexpr uint32_t kProl = kMaxCap * 4u + (kMaxE + 1u) * 4u;      // s_owner, s_poff
-  constexpr uint32_t kBig0 = KB * 2048u > kRed ? KB * 2048u : kRed;
+  constexpr uint32_t kBig0 = KB * 2048u > kRed || kStageAll ? KB * 2048u : kRed;
   constexpr uint32_t kBig = kBig0 > kProl ? kBig0 : kProl;
   // s_big: the tile's x rows | split sums | prologue tables
   __shared__ __align__(16) uint8_t s_big[kBig];
@@ -151,156 +159,254 @@ __device__ __forceinline__ void ffn_gate_up(
   __shared__ unsigned long long s_mask[kMaxE];
   __shared__ uint32_t s_boff[kMaxE + 1], s_toff[kMaxE + 1];
   __shared__ uint32_t s_chunk[48];
-  constexpr bool kStageAll = SA > 1;                   // narrow: T <= kNarrowT tokens' rows fit in LDS
-  constexpr uint32_t kAllPieces = kStageAll ? (kNarrowT * H / 16u + kThreads - 1u) / kThreads : 0u;
-  __shared__ uint4 s_xall[kStageAll ? kNarrowT * H / 16u : 1u];
-  __shared__ float s_xsall[kStageAll ? kNarrowT * KB : 1u];
+  __shared__ float s_rsum[kStageAll ? kRed / 4u : 1u];  // narrow: split sums (s_big holds the A operand)
   uint8_t* const s_a = s_big;
-  float* const s_red = reinterpret_cast<float*>(s_big);
+  float* const s_red = kStageAll ? s_rsum : reinterpret_cast<float*>(s_big);
   int32_t* const s_owner = reinterpret_cast<int32_t*>(s_big);
   uint32_t* const s_poff = reinterpret_cast<uint32_t*>(s_big + kMaxCap * 4u);
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = nkstream::wave_id();
   const uint32_t Ktot = K + S, Etot = E + S, routes = T * Ktot;
-  if (T > (kStageAll ? kNarrowT : kMaxT) || Ktot > kMaxKtot || Etot > kMaxE || cap_blocks > kMaxCap || K > E)
+  if (T == 0u || T > (kStageAll ? kNarrowT : kMaxT) || Ktot > kMaxKtot || Etot > kMaxE || cap_blocks > kMaxCap ||
+      K > E)
     return;  // host-checked
 
   // ---- routes into LDS, routing bitmask ------------------------------------------------------
   if (tid < Etot) s_mask[tid] = 0ull;
-  // narrow: every token's x row and scales go to LDS now, their loads in
-  // flight together with the ids', so no item waits for a gather from memory
+  uint32_t topk_id = 0;  // narrow: wave t lane s < Ktot, token t's slot s
+  float topk_wt = 0.0f;
   if constexpr (kStageAll) {
-#pragma unroll
-    for (uint32_t q = 0; q < kAllPieces; ++q) {
-      const uint32_t i = tid + q * kThreads;  // 16-byte piece of the T x H rows
-      if (i < T * (H / 16u)) s_xall[i] = reinterpret_cast<const uint4*>(xq)[i];
+    // narrow: the A operand of every item is the T token rows themselves
+    // (row t = token t, rows T .. 15 zero), copied by DMA into the tile layout
+    // of s_a (K block kb, half h: the 16-byte piece of row r at columns
+    // 128 kb + 32 c + 16 h .. + 15 sits at 2048 kb + 1024 h + 16 (16 c + r))
+    // with the scales s_xs[kb][r]; pieces past the T rows read as zeros. The
+    // copies use no registers and are in flight under the top-k; wave t
+    // selects token t's experts from the logits (the route kernel's top-k,
+    // one wave per token)
+    static_assert(KB % 4u == 0u, "scale copies of 64 floats");
+    const nk::u32x4 rx = nklds::rsrc(xq, T * H), rxs = nklds::rsrc(xs, T * KB * 4u);
+    for (uint32_t c = wave; c < 2u * KB; c += kWaves)  // copy c: K block c / 2, half c % 2
+      nklds::copy16((uint32_t)__builtin_amdgcn_readfirstlane((int)nklds::lds_offset(s_a + c * 1024u)), rx,
+                    (lane & 15u) * H + (c >> 1) * 128u + (lane >> 4) * 32u + (c & 1u) * 16u, 0u);
+    for (uint32_t c = wave; c < KB / 4u; c += kWaves) {  // s_xs[64 c + l]: K block (64 c + l) / 16, row l % 16
+      const uint32_t i = 64u * c + lane;
+      nklds::copy4((uint32_t)__builtin_amdgcn_readfirstlane((int)nklds::lds_offset(&s_xs[64u * c])), rxs,
+                   ((i & 15u) * KB + (i >> 4)) * 4u, 0u);
     }
-    for (uint32_t i = tid; i < T * KB; i += kThreads) s_xsall[i] = xs[i];
+    if (wave < T) {
+      topk_select_any(logits + (size_t)wave * Etot, bias, E, K, S, lane, topk_id, topk_wt);
+      if (lane < Ktot) s_ids[wave * Ktot + lane] = (int32_t)topk_id;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the copies have landed
+    lds_barrier();
+    // workgroup 0 publishes the selection (after the barrier: no store is in
+    // the wait above)
+    if (blockIdx.x == 0 && wave < T && lane < Ktot) {
+      topk_ids[wave * Ktot + lane] = (int32_t)topk_id;
+      topk_weights[wave * Ktot + lane] = topk_wt;
+    }
+  } else {
+    for (uint32_t r = tid; r < routes; r += kThreads) s_ids[r] = topk_ids[r];
+    lds_barrier();
   }
-  for (uint32_t r = tid; r < routes; r += kThreads) s_ids[r] = topk_ids[r];
-  lds_barrier();
   for (uint32_t r = tid; r < routes; r += kThreads) {
     const uint32_t e = (uint32_t)s_ids[r];
     if (e < Etot) atomicOr(&s_mask[e], 1ull << (r / Ktot));
   }
   lds_barrier();
 
-  // ---- counts and block / tile / pair offsets (one expert per thread) -----------------------
-  const uint32_t cnt = tid < Etot ? (uint32_t)__popcll(s_mask[tid]) : 0u;
-  const uint32_t vb = (cnt + 63u) >> 6, vt = (cnt + 15u) >> 4, vp = (vb + 1u) >> 1;
-  uint32_t ib = vb, it = vt, ip = vp;
+  // Step s of item `item` (tile expert e): 16-column item c0 + s / NA, K blocks
+  // kbw + ((s + rot) % NA) * kCH ..  Rotating the K order by the item spreads
+  // the workgroups running together over different offsets of their experts'
+  // weights (same-offset streams of 2 MiB-strided experts share HBM channels).
+  const uint32_t ca = wave % CA, sa = wave / CA;
+  const uint32_t kbw = sa * KBA;  // this wave's first K block
+  auto issue_at = [&](GateUpStep<kCH>& st, uint32_t e, uint32_t item, uint32_t s) __attribute__((always_inline)) {
+    const uint8_t* w13e = w13 + (size_t)e * 2u * I * H;
+    const float* w13se = w13s + (size_t)e * (2u * I / 128u) * KB;
+    const uint32_t c = ((item % GA) * CA + ca) * P + s / NA, rot = item % NA;
 #pragma unroll
-  for (uint32_t off = 1; off < 64; off <<= 1) {
-    const uint32_t ob = __shfl_up(ib, off), ot = __shfl_up(it, off), op = __shfl_up(ip, off);
-    if (lane >= off) { ib += ob; it += ot; ip += op; }
-  }
-  if (lane == 63u) { s_chunk[wave] = ib; s_chunk[16u + wave] = it; s_chunk[32u + wave] = ip; }
-  lds_barrier();
-  uint32_t cb = 0, ct = 0, cp = 0, nblk = 0, ntile = 0, npair = 0;
-#pragma unroll
-  for (uint32_t c = 0; c < kWaves; ++c) {
-    if (c < wave) { cb += s_chunk[c]; ct += s_chunk[16u + c]; cp += s_chunk[32u + c]; }
-    nblk += s_chunk[c];
-    ntile += s_chunk[16u + c];
-    npair += s_chunk[32u + c];
-  }
-  if (tid < Etot) { s_boff[tid] = cb + ib - vb; s_toff[tid] = ct + it - vt; s_poff[tid] = cp + ip - vp; }
-  if (tid == 0) { s_boff[Etot] = nblk; s_toff[Etot] = ntile; s_poff[Etot] = npair; }
-  if (nblk > cap_blocks) return;  // impossible for T <= 64 with the engine's capacity; uniform
-  for (uint32_t b = tid; b < cap_blocks; b += kThreads) s_owner[b] = -1;
-  lds_barrier();
-  if (tid < Etot) {
-    for (uint32_t b = s_boff[tid]; b < s_boff[tid + 1u]; ++b) s_owner[b] = (int32_t)tid;
-    if (blockIdx.x == 0) {
-      counts[tid] = (int32_t)cnt;
-      for (uint32_t i = s_toff[tid]; i < s_toff[tid + 1u]; ++i) tile_map[i] = (int32_t)(s_boff[tid] * 4u + (i - s_toff[tid]));
-      for (uint32_t i = s_poff[tid]; i < s_poff[tid + 1u]; ++i) pair_map[i] = (int32_t)(s_boff[tid] + 2u * (i - s_poff[tid]));
+    for (uint32_t i = 0; i < kCH; ++i) {
+      const uint32_t kb = kbw + ((s + rot) % NA) * kCH + i;
+      st.g[i] = nk::load_tile_operand_once(nk::tile_base(w13e, 2u * c, kb, KB), lane);
+      st.u[i] = nk::load_tile_operand_once(nk::tile_base(w13e, 2u * c + 1u, kb, KB), lane);
     }
-  }
-  if (blockIdx.x == 0 && tid == 0) {
-    num_valid[0] = (int32_t)(nblk * 64u);
-    num_valid[1] = (int32_t)routes;
-    num_valid[2] = (int32_t)ntile;
-    num_valid[3] = (int32_t)npair;
-  }
-  lds_barrier();
-  // sorted ids and the block table, a grid-stride share per workgroup
+    const uint32_t sl = lane < 2u * KB ? lane : 0u;
+    st.ws = w13se[((sl < KB ? c : I / 16u + c) >> 3) * KB + (sl < KB ? sl : sl - KB)];
+  };
+  GateUpStep<kCH> b0, b1;
   const int32_t pad = (int32_t)((Ktot << 24) | T);
-  for (uint32_t p = blockIdx.x * kThreads + tid; p < cap_blocks * 64u; p += gridDim.x * kThreads) {
-    const uint32_t b = p >> 6;
-    const int32_t e = s_owner[b];
-    int32_t v = pad;
-    if (e >= 0) {
-      const uint32_t j = (b - s_boff[e]) * 64u + (p & 63u);  // rank among expert e's tokens
-      const unsigned long long m = s_mask[e];
-      if (j < (uint32_t)__popcll(m)) {
-        const uint32_t t = nth_bit(m, j);
-        v = (int32_t)((slot_of(s_ids, t, Ktot, (uint32_t)e) << 24) | t);
+  // narrow: an expert holds at most T <= kNarrowT <= 16 routes, so it has one
+  // block, one tile and one pair, all numbered g for the g-th expert with a
+  // route. Every wave holds the experts' presence as ballots (bit l of
+  // used[c]: expert 64 c + l has a route), from which the sorted format
+  // follows without a scan; the first item's steps are issued before the
+  // sorted format is written, their weight loads in flight under it.
+  static_assert(kNarrowT <= 16u && (!kStageAll || NS <= 2u), "one tile per expert; an item's steps issued at once");
+  constexpr uint32_t kChunks = kStageAll ? kMaxE / 64u : 1u;
+  unsigned long long used[kChunks];
+  uint32_t before[kChunks + 1];
+  auto used_expert = [&](uint32_t b) __attribute__((always_inline)) {  // the b-th expert with a route (uniform)
+    uint32_t e = 0;
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks; ++c)
+      if (b >= before[c] && b < before[c + 1]) e = 64u * c + nth_bit(used[c], b - before[c]);
+    return e;
+  };
+  uint32_t ntile = 0, e_pre = 0xffffffffu;
+  if constexpr (kStageAll) {
+    before[0] = 0;
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks; ++c) {
+      used[c] = __ballot(64u * c + lane < Etot && s_mask[64u * c + lane] != 0ull);
+      before[c + 1] = before[c] + (uint32_t)__popcll(used[c]);
+    }
+    ntile = before[kChunks];
+    if (blockIdx.x / GA < ntile) {
+      e_pre = used_expert(blockIdx.x / GA);
+      issue_at(b0, e_pre, blockIdx.x, 0u);
+      if constexpr (NS == 2) issue_at(b1, e_pre, blockIdx.x, 1u);
+    }
+    if (blockIdx.x == 0) {
+      if (tid < Etot) counts[tid] = (int32_t)__popcll(s_mask[tid]);
+      if (tid < ntile) {
+        tile_map[tid] = (int32_t)(4u * tid);
+        pair_map[tid] = (int32_t)tid;
+      }
+      if (tid == 0) {
+        num_valid[0] = (int32_t)(ntile * 64u);
+        num_valid[1] = (int32_t)routes;
+        num_valid[2] = (int32_t)ntile;
+        num_valid[3] = (int32_t)ntile;
       }
     }
-    sorted_ids[p] = v;
-    if ((p & 63u) == 0u) sorted_expert[b] = e;
+    // sorted ids and the block table, a grid-stride share per workgroup (a
+    // wave's 64 entries are one block)
+    for (uint32_t p = blockIdx.x * kThreads + tid; p < cap_blocks * 64u; p += gridDim.x * kThreads) {
+      const uint32_t b = __builtin_amdgcn_readfirstlane(p >> 6);
+      int32_t v = pad, e = -1;
+      if (b < ntile) {
+        e = (int32_t)used_expert(b);
+        const unsigned long long m = s_mask[e];
+        const uint32_t j = p & 63u;  // rank among expert e's tokens
+        if (j < (uint32_t)__popcll(m)) {
+          const uint32_t t = nth_bit(m, j);
+          v = (int32_t)((slot_of(s_ids, t, Ktot, (uint32_t)e) << 24) | t);
+        }
+      }
+      sorted_ids[p] = v;
+      if ((p & 63u) == 0u) sorted_expert[b] = e;
+    }
+  } else {
+    // ---- counts and block / tile / pair offsets (one expert per thread) -----------------------
+    const uint32_t cnt = tid < Etot ? (uint32_t)__popcll(s_mask[tid]) : 0u;
+    const uint32_t vb = (cnt + 63u) >> 6, vt = (cnt + 15u) >> 4, vp = (vb + 1u) >> 1;
+    uint32_t ib = vb, it = vt, ip = vp;
+#pragma unroll
+    for (uint32_t off = 1; off < 64; off <<= 1) {
+      const uint32_t ob = __shfl_up(ib, off), ot = __shfl_up(it, off), op = __shfl_up(ip, off);
+      if (lane >= off) { ib += ob; it += ot; ip += op; }
+    }
+    if (lane == 63u) { s_chunk[wave] = ib; s_chunk[16u + wave] = it; s_chunk[32u + wave] = ip; }
+    lds_barrier();
+    uint32_t cb = 0, ct = 0, cp = 0, nblk = 0, npair = 0;
+#pragma unroll
+    for (uint32_t c = 0; c < kWaves; ++c) {
+      if (c < wave) { cb += s_chunk[c]; ct += s_chunk[16u + c]; cp += s_chunk[32u + c]; }
+      nblk += s_chunk[c];
+      ntile += s_chunk[16u + c];
+      npair += s_chunk[32u + c];
+    }
+    if (tid < Etot) { s_boff[tid] = cb + ib - vb; s_toff[tid] = ct + it - vt; s_poff[tid] = cp + ip - vp; }
+    if (tid == 0) { s_boff[Etot] = nblk; s_toff[Etot] = ntile; s_poff[Etot] = npair; }
+    if (nblk > cap_blocks) return;  // impossible for T <= 64 with the engine's capacity; uniform
+    for (uint32_t b = tid; b < cap_blocks; b += kThreads) s_owner[b] = -1;
+    lds_barrier();
+    if (tid < Etot) {
+      for (uint32_t b = s_boff[tid]; b < s_boff[tid + 1u]; ++b) s_owner[b] = (int32_t)tid;
+      if (blockIdx.x == 0) {
+        counts[tid] = (int32_t)cnt;
+        for (uint32_t i = s_toff[tid]; i < s_toff[tid + 1u]; ++i) tile_map[i] = (int32_t)(s_boff[tid] * 4u + (i - s_toff[tid]));
+        for (uint32_t i = s_poff[tid]; i < s_poff[tid + 1u]; ++i) pair_map[i] = (int32_t)(s_boff[tid] + 2u * (i - s_poff[tid]));
+      }
+    }
+    if (blockIdx.x == 0 && tid == 0) {
+      num_valid[0] = (int32_t)(nblk * 64u);
+      num_valid[1] = (int32_t)routes;
+      num_valid[2] = (int32_t)ntile;
+      num_valid[3] = (int32_t)npair;
+    }
+    lds_barrier();
+    // sorted ids and the block table, a grid-stride share per workgroup
+    for (uint32_t p = blockIdx.x * kThreads + tid; p < cap_blocks * 64u; p += gridDim.x * kThreads) {
+      const uint32_t b = p >> 6;
+      const int32_t e = s_owner[b];
+      int32_t v = pad;
+      if (e >= 0) {
+        const uint32_t j = (b - s_boff[e]) * 64u + (p & 63u);  // rank among expert e's tokens
+        const unsigned long long m = s_mask[e];
+        if (j < (uint32_t)__popcll(m)) {
+          const uint32_t t = nth_bit(m, j);
+          v = (int32_t)((slot_of(s_ids, t, Ktot, (uint32_t)e) << 24) | t);
+        }
+      }
+      sorted_ids[p] = v;
+      if ((p & 63u) == 0u) sorted_expert[b] = e;
+    }
+    lds_barrier();  // s_owner / s_poff are dead from here: s_big is the items' space
   }
-  lds_barrier();  // s_owner / s_poff are dead from here: s_big is the items' space
 
   // ---- items --------------------------------------------------------------------------------
 #pragma unroll 1
   for (uint32_t item = blockIdx.x; item < ntile * GA; item += gridDim.x) {
     const uint32_t g = item / GA, grp = item % GA;
-    // the tile's expert: the last e with s_toff[e] <= g (uniform binary search)
-    uint32_t lo = 0, hi = Etot;  // s_toff[lo] <= g < s_toff[hi]
-    while (hi - lo > 1u) {
-      const uint32_t mid = (lo + hi) >> 1;
-      if (s_toff[mid] <= g) lo = mid; else hi = mid;
+    uint32_t e, k, row0;  // the tile's expert, its sub-tile among e's rows and its sorted position
+    if constexpr (kStageAll) {
+      e = used_expert(g);
+      k = 0;
+      row0 = 64u * g;
+    } else {  // the last e with s_toff[e] <= g (uniform binary search)
+      uint32_t lo = 0, hi = Etot;  // s_toff[lo] <= g < s_toff[hi]
+      while (hi - lo > 1u) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (s_toff[mid] <= g) lo = mid; else hi = mid;
+      }
+      e = lo;
+      k = g - s_toff[e];
+      row0 = (s_boff[e] + (k >> 2)) * 64u + (k & 3u) * 16u;
     }
-    const uint32_t e = lo, k = g - s_toff[e];
-    const uint32_t row0 = (s_boff[e] + (k >> 2)) * 64u + (k & 3u) * 16u;  // sorted position of the tile
     int32_t tok = -1;  // lane l: the token of row l & 15, -1 for padding
     {
       const unsigned long long emask = s_mask[e];
       const uint32_t j = 16u * k + (lane & 15u);
       if (j < (uint32_t)__popcll(emask)) tok = (int32_t)nth_bit(emask, j);
     }
-    const uint8_t* w13e = w13 + (size_t)e * 2u * I * H;
-    const float* w13se = w13s + (size_t)e * (2u * I / 128u) * KB;
-    const uint32_t ca = wave % CA, sa = wave / CA;
     const uint32_t c0 = (grp * CA + ca) * P;  // this wave's first 16-column item within the tile's I / 16
-    const uint32_t kbw = sa * KBA;            // this wave's first K block
-    // step s: 16-column item c0 + s / NA, K blocks kbw + (s % NA) * kCH ..
-    auto issue = [&](GateUpStep<kCH>& st, uint32_t s) __attribute__((always_inline)) {
-      const uint32_t c = c0 + s / NA;
-#pragma unroll
-      for (uint32_t i = 0; i < kCH; ++i) {
-        const uint32_t kb = kbw + (s % NA) * kCH + i;
-        st.g[i] = nk::load_tile_operand_once(nk::tile_base(w13e, 2u * c, kb, KB), lane);
-        st.u[i] = nk::load_tile_operand_once(nk::tile_base(w13e, 2u * c + 1u, kb, KB), lane);
-      }
-      const uint32_t sl = lane < 2u * KB ? lane : 0u;
-      st.ws = w13se[((sl < KB ? c : I / 16u + c) >> 3) * KB + (sl < KB ? sl : sl - KB)];
-    };
-    GateUpStep<kCH> b0, b1;
-    issue(b0, 0u);
-    // stage the tile's x rows (padding rows zero) and scales
+    const uint32_t rot = item % NA;
+    auto issue = [&](GateUpStep<kCH>& st, uint32_t s) __attribute__((always_inline)) { issue_at(st, e, item, s); };
+    // steps 0 and (NS > 1) 1 issued: in the prologue (narrow, first item) or now
+    const bool pre = kStageAll && item == blockIdx.x && e == e_pre;
+    if (!pre) {
+      issue(b0, 0u);
+      if constexpr (NS == 2) issue(b1, 1u);
+    }
+    // wide: stage the tile's x rows (padding rows zero) and scales
+    if constexpr (!kStageAll) {
     constexpr uint32_t kPieces = H / kThreads, kScales = (16u * KB + kThreads - 1u) / kThreads;
     uint4 av[kPieces];
 #pragma unroll
     for (uint32_t q = 0; q < kPieces; ++q) {
       const uint32_t pc = tid + q * kThreads, row = pc / (H / 16u), kk = (pc % (H / 16u)) * 16u;
       const int32_t t = __shfl(tok, row);
-      if constexpr (kStageAll)
-        av[q] = t >= 0 ? s_xall[(uint32_t)t * (H / 16u) + kk / 16u] : make_uint4(0u, 0u, 0u, 0u);
-      else
-        av[q] = t >= 0 ? *reinterpret_cast<const uint4*>(xq + (size_t)t * H + kk) : make_uint4(0u, 0u, 0u, 0u);
+      av[q] = t >= 0 ? *reinterpret_cast<const uint4*>(xq + (size_t)t * H + kk) : make_uint4(0u, 0u, 0u, 0u);
     }
     float xv[kScales];
 #pragma unroll
     for (uint32_t q = 0; q < kScales; ++q) {
       const uint32_t i = tid + q * kThreads;
       const int32_t t = __shfl(tok, (i / KB) & 15u);
-      if constexpr (kStageAll)
-        xv[q] = (i < 16u * KB && t >= 0) ? s_xsall[(uint32_t)t * KB + i % KB] : 0.0f;
-      else
-        xv[q] = (i < 16u * KB && t >= 0) ? xs[(size_t)t * KB + i % KB] : 0.0f;
+      xv[q] = (i < 16u * KB && t >= 0) ? xs[(size_t)t * KB + i % KB] : 0.0f;
     }
 #pragma unroll
     for (uint32_t q = 0; q < kPieces; ++q) {
@@ -315,12 +421,13 @@ __device__ __forceinline__ void ffn_gate_up(
         s_xs[(i % KB) * 16u + i / KB] = xv[q];
       }
     lds_barrier();
+    }
 
     v4f ag = {0.0f, 0.0f, 0.0f, 0.0f}, au = {0.0f, 0.0f, 0.0f, 0.0f};
     auto compute = [&](const GateUpStep<kCH>& st, uint32_t s) __attribute__((always_inline)) {
 #pragma unroll
       for (uint32_t i = 0; i < kCH; ++i) {
-        const uint32_t kb = kbw + (s % NA) * kCH + i;
+        const uint32_t kb = kbw + ((s + rot) % NA) * kCH + i;
         const v8i a = nk::load_tile_operand(s_a + kb * 2048u, lane);
         const v4f dg = nk::mfma_e4m3_16x16x128(a, st.g[i]);
         const v4f du = nk::mfma_e4m3_16x16x128(a, st.u[i]);
@@ -346,6 +453,9 @@ __device__ __forceinline__ void ffn_gate_up(
     };
     if constexpr (NS == 1) {
       compute(b0, 0u);
+    } else if constexpr (NS == 2) {  // both steps in flight since the item's start
+      compute(b0, 0u);
+      compute(b1, 1u);
     } else {
 #pragma unroll 1
       for (uint32_t s = 0; s < NS; s += 2u) {
@@ -358,8 +468,7 @@ __device__ __forceinline__ void ffn_gate_up(
         compute(b1, s + 1u);
       }
     }
-    if constexpr (SA > 1) {  // add the K splits in split order
-      lds_barrier();         // every wave is done with s_a
+    if constexpr (SA > 1) {  // add the K splits in split order (s_red has LDS of its own)
 #pragma unroll
       for (uint32_t j = 0; j < 4; ++j) {
         s_red[(wave * 8u + j) * 64u + lane] = ag[j];
@@ -395,11 +504,21 @@ __device__ __forceinline__ void ffn_gate_up(
         *reinterpret_cast<uint4*>(hq + blk * 2048u + 1024u + lane * 16u) = qhi;
         if (lane < 16u) hs[blk * 16u + lane] = scale;
       }
-    } else if (sa == 0) {  // bf16 h rows (l >> 4) * 4 + j, column 16 c0 + (l & 15) of tile g (P = 1)
+    } else if (sa == 0) {  // bf16 h of tile g, column 16 c0 + (l & 15) (P = 1)
+      // lane l, j: MFMA row q = (l >> 4) * 4 + j is token q; the tile's row of
+      // a token routed to e is its rank among e's tokens, and the rows past
+      // e's count take zeros from the other rows q in order (a bijection)
       uint16_t* const hg = hrows + (size_t)g * 16u * I;
+      const unsigned long long emask = s_mask[e];
+      const uint32_t cnt = (uint32_t)__popcll(emask);
 #pragma unroll
-      for (uint32_t j = 0; j < 4; ++j)
-        hg[((lane >> 4) * 4u + j) * I + c0 * 16u + (lane & 15u)] = nk::bf16_rne(nk::silu(ag[j]) * au[j]);
+      for (uint32_t j = 0; j < 4; ++j) {
+        const uint32_t q = (lane >> 4) * 4u + j;
+        const uint32_t below = (uint32_t)__popcll(emask & ((1ull << q) - 1ull));
+        const bool routed = (emask >> q) & 1ull;  // q < T <= 8 for a set bit
+        const uint32_t r = routed ? below : cnt + q - below;
+        hg[r * I + c0 * 16u + (lane & 15u)] = routed ? nk::bf16_rne(nk::silu(ag[j]) * au[j]) : (uint16_t)0u;
+      }
     }
     lds_barrier();  // every wave is done with s_a / s_hb before the next item
   }
@@ -444,7 +563,26 @@ __device__ __forceinline__ void ffn_down(
   if (T > kMaxT || Ktot > kMaxKtot || Etot > kMaxE) return;  // host-checked
   // tiles as the sort counted them, never past the capacity (T Ktot / 16 + Etot):
   // an operation launched out of order may find another tensor's bytes here
-  const uint32_t ntile = min((uint32_t)num_valid[2], (T * Ktot + 15u) / 16u + Etot);
+  // narrow: an expert holds at most kNarrowT <= 16 rows, so tile g is the first
+  // 16 rows of block g (no tile_map hop); the first item's rows and bf16 h
+  // rows (wave w < KBI: 128-column block w, lane l row l & 15, columns
+  // 32 (l >> 4) .. + 31) load together with the tile count
+  const uint32_t cap_blocks = (T * Ktot + 63u) / 64u + Etot;
+  const uint32_t g_first = blockIdx.x / GB;
+  nkstream::TileRows tr_first;
+  uint4 h_first[kFromRows ? 4 : 1];
+  auto load_hrows = [&](uint4 (&v)[kFromRows ? 4 : 1], uint32_t g) __attribute__((always_inline)) {
+    const uint4* src = reinterpret_cast<const uint4*>(hrows + ((size_t)g * 16u + (lane & 15u)) * I + wave * 128u +
+                                                      (lane >> 4) * 32u);
+#pragma unroll
+    for (uint32_t q = 0; q < (kFromRows ? 4u : 1u); ++q) v[q] = src[q];
+  };
+  if constexpr (kFromRows) {
+    const uint32_t b = min(g_first, cap_blocks - 1u);
+    nkstream::load_rows(tr_first, sorted_ids, sorted_expert, b, b * 64u, T, Ktot, Etot, true);
+    if (wave < KBI) load_hrows(h_first, b);
+  }
+  const uint32_t ntile = min((uint32_t)num_valid[2], kFromRows ? cap_blocks : (T * Ktot + 15u) / 16u + Etot);
 
   // Combine hand-off of the held items: once every wave's partial stores have
   // completed, wave w lane l counts the arrival of held item 4w + (l >> 4),
@@ -509,7 +647,13 @@ __device__ __forceinline__ void ffn_down(
   for (uint32_t item = blockIdx.x; item < ntile * GB; item += gridDim.x) {
     const uint32_t g = item / GB, grp = item % GB;
     nkstream::TileRows tr;
-    nkstream::load_tile(tr, tile_map, sorted_ids, sorted_expert, g, T, Ktot, Etot, true);
+    const bool first = kFromRows && item == blockIdx.x && g_first < cap_blocks;  // rows loaded at the start
+    if constexpr (kFromRows) {
+      if (first) tr = tr_first;
+      else nkstream::load_rows(tr, sorted_ids, sorted_expert, g, g * 64u, T, Ktot, Etot, true);
+    } else {
+      nkstream::load_tile(tr, tile_map, sorted_ids, sorted_expert, g, T, Ktot, Etot, true);
+    }
     const uint32_t e = (uint32_t)tr.expert, row0 = tr.row0;
     const int32_t route = tr.row;  // lane l: the route of row l & 15, -1 for padding
     const int32_t tok = route >= 0 ? route / (int32_t)Ktot : -1;
@@ -518,9 +662,10 @@ __device__ __forceinline__ void ffn_down(
     const uint32_t cbw = wave % CB, sb = wave / CB;
     const uint32_t d0 = (grp * CB + cbw) * PD;  // this wave's first 32-column item within H / 32
     const uint32_t kbw = sb * KBB;
-    // step s: 32-column item d0 + s / NB, K blocks kbw + (s % NB) * kDC ..
+    // step s: 32-column item d0 + s / NB, K blocks kbw + ((s + rot) % NB) * kDC .. (rotated as above)
+    const uint32_t rot = item % NB;
     auto issue = [&](DownStep<kDC>& st, uint32_t s) __attribute__((always_inline)) {
-      const uint32_t d = d0 + s / NB, kb0 = kbw + (s % NB) * kDC;
+      const uint32_t d = d0 + s / NB, kb0 = kbw + ((s + rot) % NB) * kDC;
 #pragma unroll
       for (uint32_t i = 0; i < kDC; ++i)
 #pragma unroll
@@ -537,12 +682,17 @@ __device__ __forceinline__ void ffn_down(
       uint4 qlo, qhi;
       float scale = 0.0f;
       if constexpr (kFromRows) {  // requantise bf16 rows: lane l row l & 15, columns 32 (l >> 4) .. + 31
-        const uint4* src = reinterpret_cast<const uint4*>(hrows + ((size_t)g * 16u + (lane & 15u)) * I + wave * 128u +
-                                                          (lane >> 4) * 32u);
+        uint4 hv[4];
+        if (first) {
+#pragma unroll
+          for (uint32_t q = 0; q < 4; ++q) hv[q] = h_first[q];
+        } else {
+          load_hrows(hv, g);
+        }
         uint32_t raw[16];
 #pragma unroll
         for (uint32_t q = 0; q < 4; ++q) {
-          const uint4 v = src[q];
+          const uint4 v = hv[q];
           raw[4 * q] = v.x; raw[4 * q + 1] = v.y; raw[4 * q + 2] = v.z; raw[4 * q + 3] = v.w;
         }
         quant_block(raw, qlo, qhi, scale);
@@ -577,7 +727,7 @@ __device__ __forceinline__ void ffn_down(
     auto compute = [&](const DownStep<kDC>& st, uint32_t s) __attribute__((always_inline)) {
 #pragma unroll
       for (uint32_t i = 0; i < kDC; ++i) {
-        const uint32_t kb = kbw + (s % NB) * kDC + i;
+        const uint32_t kb = kbw + ((s + rot) % NB) * kDC + i;
         const v8i a = nk::load_tile_operand(s_h + kb * 2048u, lane);
         const float4 as4 = *reinterpret_cast<const float4*>(&s_hsc[kb * 16u + (lane >> 4) * 4u]);
         const float as[4] = {as4.x, as4.y, as4.z, as4.w};
@@ -652,13 +802,15 @@ __device__ __forceinline__ void ffn_down(
 #define NK_FFN_PAIR(HV, IV, NAME, SAV, SBV, CHG, WPEG, PG, CHD, WPED, PDV)                                               \
   NK_KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WPEG)))                      \
   void netra_moe_ffn_gate_up_h##HV##_i##IV##_##NAME##_gfx950(                                      \
-      const int32_t* __restrict__ topk_ids, const uint8_t* __restrict__ xq,                        \
+      const uint16_t* __restrict__ logits, const float* __restrict__ bias,                         \
+      int32_t* __restrict__ topk_ids, float* __restrict__ topk_weights, const uint8_t* __restrict__ xq, \
       const float* __restrict__ xs, const uint8_t* __restrict__ w13, const float* __restrict__ w13s, \
       int32_t* __restrict__ sorted_ids, int32_t* __restrict__ sorted_expert,                       \
       int32_t* __restrict__ tile_map, int32_t* __restrict__ pair_map, int32_t* __restrict__ num_valid, \
       int32_t* __restrict__ counts, uint16_t* __restrict__ hrows, uint8_t* __restrict__ hq,        \
       float* __restrict__ hs, uint32_t T, uint32_t E, uint32_t K, uint32_t S, uint32_t cap_blocks) { \
-    nkffn::ffn_gate_up<HV / 128, IV / 128, SAV, CHG, PG>(topk_ids, xq, xs, w13, w13s, sorted_ids,        \
+    nkffn::ffn_gate_up<HV / 128, IV / 128, SAV, CHG, PG>(logits, bias, topk_ids, topk_weights, xq, xs, w13,  \
+                                                     w13s, sorted_ids,                              \
                                                      sorted_expert, tile_map, pair_map, num_valid,  \
                                                      counts, hrows, hq, hs, T, E, K, S, cap_blocks); \
   }                                                                                                \

@@ -47,18 +47,24 @@ struct TileRows {
   int32_t row = -1;
 };
 
-__device__ __forceinline__ void load_tile(TileRows& tr, const int32_t* __restrict__ tile_map,
-                                          const int32_t* __restrict__ sorted_ids,
-                                          const int32_t* __restrict__ sorted_expert, uint32_t tile,
+// The tile of rows row0 .. row0 + 15 of block b.
+__device__ __forceinline__ void load_rows(TileRows& tr, const int32_t* __restrict__ sorted_ids,
+                                          const int32_t* __restrict__ sorted_expert, uint32_t b, uint32_t row0,
                                           uint32_t T, uint32_t Ktot, uint32_t Etot, bool as_route) {
-  const uint32_t m = (uint32_t)tile_map[tile];
-  const uint32_t b = m >> 2;
-  tr.row0 = b * 64u + (m & 3u) * 16u;
+  tr.row0 = row0;
   const int32_t e = sorted_expert[b];
   tr.expert = (e < 0 || (uint32_t)e >= Etot) ? 0 : e;  // out of range only for malformed routing
   const int32_t id = sorted_ids[tr.row0 + (threadIdx.x & 15u)];
   const uint32_t t = (uint32_t)id & 0xffffffu, slot = (uint32_t)id >> 24;
   tr.row = (t < T && slot < Ktot) ? (int32_t)(as_route ? t * Ktot + slot : t) : -1;
+}
+
+__device__ __forceinline__ void load_tile(TileRows& tr, const int32_t* __restrict__ tile_map,
+                                          const int32_t* __restrict__ sorted_ids,
+                                          const int32_t* __restrict__ sorted_expert, uint32_t tile,
+                                          uint32_t T, uint32_t Ktot, uint32_t Etot, bool as_route) {
+  const uint32_t m = (uint32_t)tile_map[tile];
+  load_rows(tr, sorted_ids, sorted_expert, m >> 2, (m >> 2) * 64u + (m & 3u) * 16u, T, Ktot, Etot, as_route);
 }
 
 }  // namespace nkstream

@@ -206,18 +206,24 @@ __device__ __forceinline__ float logit_f32(const uint16_t* p) {
   else return nk::bf16_f32(*p);
 }
 
+// The selection of one token (one wave): lane r < K gets slot r's expert and
+// weight, lane K (S = 1) the shared expert's; other lanes' values are unused.
 template <uint32_t P, bool kCoherent = false>  // experts per lane, P * 64 >= E
-__device__ __forceinline__ void topk_token(const uint16_t* __restrict__ lrow, const float* __restrict__ bias,
-                                           int32_t* __restrict__ ids, float* __restrict__ weights,
-                                           unsigned long long* __restrict__ mask, uint32_t t, uint32_t E,
-                                           uint32_t K, uint32_t S, uint32_t W, uint32_t lane) {
-  const uint32_t Ktot = K + S;
-  uint32_t code[P];
+__device__ __forceinline__ void topk_select(const uint16_t* __restrict__ lrow, const float* __restrict__ bias,
+                                            uint32_t E, uint32_t K, uint32_t S, uint32_t lane, uint32_t& id,
+                                            float& weight) {
+  // loads at clamped indices, all issued before the first use (a conditional
+  // load per j would wait for each in turn)
+  float lg[P], bs[P];
 #pragma unroll
   for (uint32_t j = 0; j < P; ++j) {
-    const uint32_t e = lane + 64u * j;
-    code[j] = e < E ? nk::order_bits(logit_f32<kCoherent>(lrow + e) + bias[e]) : 0u;
+    const uint32_t e = min(lane + 64u * j, E - 1u);
+    lg[j] = logit_f32<kCoherent>(lrow + e);
+    bs[j] = bias[e];
   }
+  uint32_t code[P];
+#pragma unroll
+  for (uint32_t j = 0; j < P; ++j) code[j] = lane + 64u * j < E ? nk::order_bits(lg[j] + bs[j]) : 0u;
   uint32_t my_id = 0, my_code = 0;
   for (uint32_t r = 0; r < K; ++r) {
     uint32_t best = 0, bj = 0;
@@ -246,16 +252,41 @@ __device__ __forceinline__ void topk_token(const uint16_t* __restrict__ lrow, co
   const float ex = lane < K ? nk::nexp(z - z0) : 0.0f;
   float sum = 0.0f;
   for (uint32_t r = 0; r < K; ++r) sum = sum + __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(ex), (int)r));
-  if (lane < K) {
-    ids[(size_t)t * Ktot + lane] = (int32_t)my_id;
-    weights[(size_t)t * Ktot + lane] = ex / sum;
-  }
+  id = my_id;
+  weight = ex / sum;
   if (S != 0 && lane == K) {
-    my_id = E;
-    ids[(size_t)t * Ktot + K] = (int32_t)E;
-    weights[(size_t)t * Ktot + K] = nk::bf16_f32(nk::bf16_rne(nk::sigmoid(logit_f32<kCoherent>(lrow + E))));
+    id = E;
+    weight = nk::bf16_f32(nk::bf16_rne(nk::sigmoid(logit_f32<kCoherent>(lrow + E))));
   }
-  if (mask != nullptr && lane < Ktot) atomicOr(&mask[(size_t)my_id * W + (t >> 6)], 1ull << (t & 63u));
+}
+
+// topk_select by the expert count (E <= 512), a wave-uniform dispatch.
+template <bool kCoherent = false>
+__device__ __forceinline__ void topk_select_any(const uint16_t* __restrict__ lrow, const float* __restrict__ bias,
+                                                uint32_t E, uint32_t K, uint32_t S, uint32_t lane, uint32_t& id,
+                                                float& weight) {
+  if (E <= 64u) topk_select<1, kCoherent>(lrow, bias, E, K, S, lane, id, weight);
+  else if (E <= 128u) topk_select<2, kCoherent>(lrow, bias, E, K, S, lane, id, weight);
+  else if (E <= 256u) topk_select<4, kCoherent>(lrow, bias, E, K, S, lane, id, weight);
+  else topk_select<8, kCoherent>(lrow, bias, E, K, S, lane, id, weight);
+}
+
+// One token's selection stored as topk_ids / topk_weights rows, and (mask
+// non-null) its experts' bits in the routing bitmask.
+template <bool kCoherent = false>
+__device__ __forceinline__ void topk_token(const uint16_t* __restrict__ lrow, const float* __restrict__ bias,
+                                           int32_t* __restrict__ ids, float* __restrict__ weights,
+                                           unsigned long long* __restrict__ mask, uint32_t t, uint32_t E,
+                                           uint32_t K, uint32_t S, uint32_t W, uint32_t lane) {
+  const uint32_t Ktot = K + S;
+  uint32_t id = 0;
+  float weight = 0.0f;
+  topk_select_any<kCoherent>(lrow, bias, E, K, S, lane, id, weight);
+  if (lane < Ktot) {
+    ids[(size_t)t * Ktot + lane] = (int32_t)id;
+    weights[(size_t)t * Ktot + lane] = weight;
+    if (mask != nullptr) atomicOr(&mask[(size_t)id * W + (t >> 6)], 1ull << (t & 63u));
+  }
 }
 
 NK_KERNEL __launch_bounds__(256) void netra_moe_topk_gfx950(
@@ -267,10 +298,7 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_topk_gfx950(
   const uint32_t t = blockIdx.x * 4u + (threadIdx.x >> 6);
   if (t >= T || E > 512u || K > E || K + S > 64u) return;  // wave-uniform
   const uint16_t* lrow = logits + (size_t)t * (E + S);
-  if (E <= 64u) topk_token<1>(lrow, bias, ids, weights, mask, t, E, K, S, W, lane);
-  else if (E <= 128u) topk_token<2>(lrow, bias, ids, weights, mask, t, E, K, S, W, lane);
-  else if (E <= 256u) topk_token<4>(lrow, bias, ids, weights, mask, t, E, K, S, W, lane);
-  else topk_token<8>(lrow, bias, ids, weights, mask, t, E, K, S, W, lane);
+  topk_token(lrow, bias, ids, weights, mask, t, E, K, S, W, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -305,10 +333,7 @@ __device__ __forceinline__ void route(const uint16_t* __restrict__ x, const uint
   const uint32_t t = blockIdx.y * NT + wave;
   if (wave < NT && t < T && E <= 512u && K <= E && K + S <= 64u) {  // wave-uniform
     const uint16_t* lrow = logits + (size_t)t * rows;
-    if (E <= 64u) topk_token<1, true>(lrow, bias, ids, weights, nullptr, t, E, K, S, 0u, lane);
-    else if (E <= 128u) topk_token<2, true>(lrow, bias, ids, weights, nullptr, t, E, K, S, 0u, lane);
-    else if (E <= 256u) topk_token<4, true>(lrow, bias, ids, weights, nullptr, t, E, K, S, 0u, lane);
-    else topk_token<8, true>(lrow, bias, ids, weights, nullptr, t, E, K, S, 0u, lane);
+    topk_token<true>(lrow, bias, ids, weights, nullptr, t, E, K, S, 0u, lane);
   }
   if (threadIdx.x == 0)
     __hip_atomic_store(&counters[kCounterStride * blockIdx.y], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

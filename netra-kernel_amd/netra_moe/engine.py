@@ -348,6 +348,20 @@ def _route_op(cfg: MoEConfig) -> dict:
                       "tools/benchmark/export_qwen36_shared_gate_append_capture.py:97-107,134-139"])
 
 
+def _router_logits_op(cfg: MoEConfig) -> dict:
+    """Router logits + input quant only (the narrow decode FFN runs the top-k)."""
+    T, H = cfg.T, cfg.H
+    u = lambda v: ("u32", int(v))  # noqa: E731
+    NT = router_tokens(H, T)
+    return dict(name="moe.route", symbol=f"netra_moe_router_logits_h{H}_t{NT}_gfx950",
+                grid=((cfg.router_rows + 15) // 16, (T + NT - 1) // NT, 1),
+                block=(256, 1, 1), lds=4 * NT * H, dyn=0,
+                args=["x", "router_w", "logits", "x_q", "x_scale", u(T), u(H), u(cfg.router_rows)],
+                reads=["x", "router_w"], writes=["logits", "x_q", "x_scale"],
+                refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150",
+                      "tools/benchmark/export_qwen36_router_bf16_capture.py:78"])
+
+
 def ffn_variant(cfg: MoEConfig) -> str:
     """narrow (K split over waves) for a handful of tokens, else wide."""
     return "narrow" if cfg.T <= FFN_NARROW_T else "wide"
@@ -380,24 +394,32 @@ def ffn_grid(cfg: MoEConfig, op: str) -> int:
 
 
 def _fused_decode(cfg: MoEConfig) -> list[dict]:
-    """Route (router + top-k), gate/up with the sort as its prologue, down with
-    the combine folded in (narrow) or followed by the combine kernel (wide)."""
+    """Route (router + top-k; narrow: router logits only), gate/up with the sort
+    (narrow: top-k and sort) as its prologue, down with the combine folded in
+    (narrow) or followed by the combine kernel (wide)."""
     T, H, I = cfg.T, cfg.H, cfg.I
     u = lambda v: ("u32", int(v))  # noqa: E731
     v = ffn_variant(cfg)
     lds_gu, lds_dn = ffn_lds_bytes(cfg)
     sort_out = ["sorted_ids", "sorted_expert", "tile_map", "pair_map", "num_valid", "expert_counts"]
+    # narrow: the router writes the logits only and the gate/up prologue runs
+    # the top-k (one wave per token), which takes the route kernel's hand-off
+    # off the chain; wide: the route kernel's top-k feeds gate/up
+    narrow = v == "narrow"
+    route = _router_logits_op(cfg) if narrow else _route_op(cfg)
+    topk = ["topk_ids", "topk_weights"]
     ops = [
-        _route_op(cfg),
+        route,
         dict(name="moe.gate_up", symbol=f"netra_moe_ffn_gate_up_h{H}_i{I}_{v}_gfx950",
              grid=(ffn_grid(cfg, "gate_up"), 1, 1), block=(512, 1, 1), lds=lds_gu, dyn=0,
-             args=["topk_ids", "x_q", "x_scale", "w13", "w13_scale", *sort_out, "h_rows", "h_q", "h_scale",
-                   u(T), u(cfg.E), u(cfg.K), u(cfg.S), u(cfg.cap_blocks)],
-             reads=["topk_ids", "x_q", "x_scale", "w13", "w13_scale"],
-             writes=[*sort_out, "h_rows", "h_q", "h_scale"],
+             args=["logits", "router_bias", *topk, "x_q", "x_scale", "w13", "w13_scale", *sort_out,
+                   "h_rows", "h_q", "h_scale", u(T), u(cfg.E), u(cfg.K), u(cfg.S), u(cfg.cap_blocks)],
+             reads=(["logits", "router_bias"] if narrow else ["topk_ids"]) + ["x_q", "x_scale", "w13", "w13_scale"],
+             writes=(topk if narrow else []) + [*sort_out, "h_rows", "h_q", "h_scale"],
              refs=["kernels/gfx950/templates/moe/decode/gate_up_mfma.inc:12-161",
                    "kernels/gfx950/templates/moe/decode/silu_quant.inc:16-236",
-                   "kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]),
+                   "kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]
+             + (["runtime/gfx950/routing/decode/qwen36_shared_gate_append_bridge.hip:76-112"] if narrow else [])),
         dict(name="moe.down", symbol=f"netra_moe_ffn_down_h{H}_i{I}_{v}_gfx950",
              grid=(ffn_grid(cfg, "down"), 1, 1), block=(512, 1, 1), lds=lds_dn, dyn=0,
              args=["topk_weights", "w2", "w2_scale", "sorted_ids", "sorted_expert", "tile_map", "num_valid",

@@ -797,7 +797,144 @@ __device__ __forceinline__ void ffn_down(
   }
 }
 
+// ---------------------------------------------------------------------------
+// down for a single token (T = 1), the combine in the workgroup
+// (reference: kernels/gfx950/templates/moe/decode/down_reduce_mfma_2wave.inc:14-291)
+//
+// With one token every tile g < Ktot holds one row, the token's route of slot
+// s_g to expert e_g, so a workgroup can own output columns across all the
+// routes: workgroup b computes columns [16 b, 16 b + 16) of every route's fp32
+// partial and adds them in slot order itself, with no hand-off between
+// workgroups. Wave w takes tiles w and w + 8: lane l loads h columns
+// 8 l .. 8 l + 7 of the tile's row (K block l / 16 is a 16-lane row), which is
+// requantised under the 1x128 rule of the narrow down (row max by DPP) into a
+// per-wave LDS row; the MFMA A operand is that row with rows 1 .. 15 zero.
+// Per tile p = sum over K blocks in order of w_s * (a_s * mfma) from 0 (the
+// narrow down's split order), written to partial[route] and to LDS by slot;
+// out = bf16(sum over slots in order of fmaf(weight, p, acc)) from 0.
+// Workgroup 0 also writes the tiles' requantised h (hq / hs, tile layout) for
+// inspection, as the narrow down's first column group does.
+template <uint32_t KB, uint32_t KBI>
+__device__ __forceinline__ void ffn_down_single(
+    const float* __restrict__ topk_weights, const uint8_t* __restrict__ w2, const float* __restrict__ w2s,
+    const int32_t* __restrict__ sorted_ids, const int32_t* __restrict__ sorted_expert,
+    const uint16_t* __restrict__ hrows, uint8_t* __restrict__ hq, float* __restrict__ hs,
+    float* __restrict__ partial, uint16_t* __restrict__ out, uint32_t T, uint32_t E, uint32_t K, uint32_t S) {
+  constexpr uint32_t H = 128u * KB, I = 128u * KBI;
+  static_assert(I == 512u, "lane l holds h columns 8 l .. 8 l + 7: one 512-column row per wave");
+  constexpr uint32_t kTilesPerWave = kMaxKtot / kWaves;  // 2
+  __shared__ __align__(16) uint8_t s_q[kWaves][kTilesPerWave][I];  // requantised h rows
+  __shared__ float s_p[kMaxKtot * 16u];                             // partials [slot][column]
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = nkstream::wave_id();
+  const uint32_t Ktot = K + S, Etot = E + S;
+  if (T != 1u || Ktot > kMaxKtot || Etot > kMaxE) return;  // host-checked
+  const uint32_t c16 = blockIdx.x;  // 16-column group
+  if (c16 >= H / 16u) return;
+
+  // everything a tile needs that does not depend on its expert, loaded first
+  uint32_t eg[kTilesPerWave], slot[kTilesPerWave];
+  uint4 hv[kTilesPerWave];
+#pragma unroll
+  for (uint32_t i = 0; i < kTilesPerWave; ++i) {
+    const uint32_t g = min(wave + kWaves * i, Ktot - 1u);
+    const int32_t e = sorted_expert[g];
+    eg[i] = (e < 0 || (uint32_t)e >= Etot) ? 0u : (uint32_t)e;  // out of range only for malformed routing
+    slot[i] = (uint32_t)sorted_ids[64u * g] >> 24;
+    hv[i] = *reinterpret_cast<const uint4*>(hrows + (size_t)g * 16u * I + lane * 8u);
+  }
+  // the tiles' W2 blocks (16 output columns x 128 K) and block scales
+  v8i wb[kTilesPerWave][KBI];
+  float ws[kTilesPerWave][KBI];
+#pragma unroll
+  for (uint32_t i = 0; i < kTilesPerWave; ++i) {
+    const uint8_t* w2e = w2 + (size_t)eg[i] * H * I;
+    const float* w2se = w2s + (size_t)eg[i] * (H / 128u) * KBI;
+#pragma unroll
+    for (uint32_t kb = 0; kb < KBI; ++kb) {
+      wb[i][kb] = nk::load_tile_operand_once(nk::tile_base(w2e, c16, kb, KBI), lane);
+      ws[i][kb] = w2se[(c16 >> 3) * KBI + kb];
+    }
+  }
+  // requantise the rows: amax over the 16 lanes of a K block
+  float scale[kTilesPerWave];
+#pragma unroll
+  for (uint32_t i = 0; i < kTilesPerWave; ++i) {
+    const uint4 v = hv[i];
+    const float f[8] = {nk::bf16_lo(v.x), nk::bf16_hi(v.x), nk::bf16_lo(v.y), nk::bf16_hi(v.y),
+                        nk::bf16_lo(v.z), nk::bf16_hi(v.z), nk::bf16_lo(v.w), nk::bf16_hi(v.w)};
+    float amax = nk::kAmaxFloor;
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) amax = fmaxf(amax, fabsf(f[q]));
+    uint32_t ab = __float_as_uint(amax);  // non-negative: the bit patterns order as the values
+    ab = max(ab, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)ab, 0xB1, 0xF, 0xF, false));
+    ab = max(ab, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)ab, 0x4E, 0xF, 0xF, false));
+    ab = max(ab, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)ab, 0x141, 0xF, 0xF, false));
+    ab = max(ab, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)ab, 0x140, 0xF, 0xF, false));
+    scale[i] = __uint_as_float(ab) * nk::inv_e4m3_max();
+    const float inv = 1.0f / scale[i];
+    *reinterpret_cast<uint2*>(&s_q[wave][i][lane * 8u]) =
+        make_uint2(nk::e4m3x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv),
+                   nk::e4m3x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv));
+  }
+  // p of each tile: lanes 0 .. 15 hold row 0 (the route), column l
+  const bool row0 = (lane & 15u) == 0u;
+  const float floor_scale = nk::kAmaxFloor * nk::inv_e4m3_max();  // an all-zero row's scale
+#pragma unroll
+  for (uint32_t i = 0; i < kTilesPerWave; ++i) {
+    const uint32_t g = wave + kWaves * i;
+    if (g >= Ktot) break;  // uniform
+    float p = 0.0f;
+#pragma unroll
+    for (uint32_t kb = 0; kb < KBI; ++kb) {
+      // A operand: lane 16 c holds row 0's columns 128 kb + 32 c .. + 31, other rows zero
+      const uint4* src = reinterpret_cast<const uint4*>(&s_q[wave][i][kb * 128u + 32u * (lane >> 4)]);
+      const uint4 lo = row0 ? src[0] : make_uint4(0u, 0u, 0u, 0u);
+      const uint4 hi = row0 ? src[1] : make_uint4(0u, 0u, 0u, 0u);
+      v8i a;
+      a[0] = (int)lo.x; a[1] = (int)lo.y; a[2] = (int)lo.z; a[3] = (int)lo.w;
+      a[4] = (int)hi.x; a[5] = (int)hi.y; a[6] = (int)hi.z; a[7] = (int)hi.w;
+      const v4f d = nk::mfma_e4m3_16x16x128(a, wb[i][kb]);
+      const float as = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(scale[i]), (int)(16u * kb)));
+      p = p + ws[i][kb] * (as * d[0]);
+      if (blockIdx.x == 0) {  // for inspection: the tile's requantised h in the stream path's layout
+        const size_t blk = (size_t)(4u * g) * KBI + kb;
+        *reinterpret_cast<uint4*>(hq + blk * 2048u + lane * 16u) = lo;
+        *reinterpret_cast<uint4*>(hq + blk * 2048u + 1024u + lane * 16u) = hi;
+        if (lane < 16u) hs[blk * 16u + lane] = lane == 0u ? as : floor_scale;
+      }
+    }
+    if (lane < 16u) {
+      s_p[slot[i] * 16u + lane] = p;
+      partial[(size_t)slot[i] * H + c16 * 16u + lane] = p;
+    }
+  }
+  nkstream::lds_barrier();
+  if (wave == 0 && lane < 16u) {
+    float y = 0.0f;
+    for (uint32_t s = 0; s < Ktot; ++s) y = fmaf(topk_weights[s], s_p[s * 16u + lane], y);
+    out[c16 * 16u + lane] = nk::bf16_rne(y);
+  }
+}
+
 }  // namespace nkffn
+
+#define NK_FFN_DOWN_SINGLE(HV, IV)                                                                 \
+  NK_KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))                        \
+  void netra_moe_ffn_down_h##HV##_i##IV##_single_gfx950(                                          \
+      const float* __restrict__ topk_weights, const uint8_t* __restrict__ w2,                      \
+      const float* __restrict__ w2s, const int32_t* __restrict__ sorted_ids,                       \
+      const int32_t* __restrict__ sorted_expert, const int32_t* __restrict__ tile_map,             \
+      const int32_t* __restrict__ num_valid, const uint16_t* __restrict__ hrows,                   \
+      uint8_t* __restrict__ hq, float* __restrict__ hs, float* __restrict__ partial,               \
+      uint32_t* __restrict__ counters, uint16_t* __restrict__ out, uint32_t T, uint32_t E,         \
+      uint32_t K, uint32_t S) {                                                                    \
+    (void)tile_map; (void)num_valid; (void)counters;                                               \
+    nkffn::ffn_down_single<HV / 128, IV / 128>(topk_weights, w2, w2s, sorted_ids, sorted_expert,   \
+                                               hrows, hq, hs, partial, out, T, E, K, S);           \
+  }
+// Symbol netra_moe_ffn_down_h<H>_i512_single_gfx950: the T = 1 down (H / 16 workgroups).
+NK_FFN_DOWN_SINGLE(2048, 512)
 
 #define NK_FFN_PAIR(HV, IV, NAME, SAV, SBV, CHG, WPEG, PG, CHD, WPED, PDV)                                               \
   NK_KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WPEG)))                      \

@@ -221,34 +221,52 @@ __device__ __forceinline__ void topk_select(const uint16_t* __restrict__ lrow, c
     lg[j] = logit_f32<kCoherent>(lrow + e);
     bs[j] = bias[e];
   }
-  uint32_t code[P];
+  // Key of expert e = lane + 64 j: its code in the high word, ~e in the low
+  // word (larger key: larger z, then lower expert index; 0: absent). Each
+  // lane sorts its P keys once (descending; networks checked by the 0-1
+  // principle), so a round offers every lane's head: the wave max of the
+  // heads' codes, the lowest expert among lanes offering it, and the winning
+  // lane moves to its next key.
+  uint64_t key[P];
 #pragma unroll
-  for (uint32_t j = 0; j < P; ++j) code[j] = lane + 64u * j < E ? nk::order_bits(lg[j] + bs[j]) : 0u;
+  for (uint32_t j = 0; j < P; ++j) {
+    const uint32_t e = lane + 64u * j;
+    key[j] = e < E ? ((uint64_t)nk::order_bits(lg[j] + bs[j]) << 32) | (0xffffffffu - e) : 0ull;
+  }
+  auto cx = [&](uint32_t i, uint32_t j) __attribute__((always_inline)) {  // key[i] >= key[j] after
+    const uint64_t a = key[i], b = key[j];
+    const bool sw = b > a;
+    key[i] = sw ? b : a;
+    key[j] = sw ? a : b;
+  };
+  if constexpr (P == 2) {
+    cx(0, 1);
+  } else if constexpr (P == 4) {
+    cx(0, 1); cx(2, 3); cx(0, 2); cx(1, 3); cx(1, 2);
+  } else if constexpr (P == 8) {
+    cx(0, 1); cx(2, 3); cx(4, 5); cx(6, 7); cx(0, 2); cx(1, 3); cx(4, 6); cx(5, 7); cx(1, 2); cx(5, 6);
+    cx(0, 4); cx(1, 5); cx(2, 6); cx(3, 7); cx(2, 4); cx(3, 5); cx(1, 2); cx(3, 4); cx(5, 6);
+  } else {
+    static_assert(P == 1, "P in {1, 2, 4, 8}");
+  }
   uint32_t my_id = 0, my_code = 0;
   for (uint32_t r = 0; r < K; ++r) {
-    uint32_t best = 0, bj = 0;
+    const uint32_t hc = (uint32_t)(key[0] >> 32), hl = (uint32_t)key[0];
+    const uint32_t m = nk::wave_reduce_u32<true>(hc);
+    const unsigned long long tied = __ballot(hc == m);
+    uint32_t wl;  // the winning lane
+    if (__popcll(tied) == 1) wl = (uint32_t)(__ffsll((long long)tied) - 1);
+    else wl = (0xffffffffu - nk::wave_reduce_u32<true>(hc == m ? hl : 0u)) & 63u;
+    const uint32_t win = 0xffffffffu - (uint32_t)__builtin_amdgcn_readlane((int)hl, (int)wl);
+    if (lane == wl) {
 #pragma unroll
-    for (uint32_t j = 0; j < P; ++j)
-      if (code[j] > best) { best = code[j]; bj = j; }
-    const uint32_t m = nk::wave_reduce_u32<true>(best);
-    const unsigned long long tied = __ballot(best == m);
-    uint32_t win;
-    if (__popcll(tied) == 1) {
-      const int wl = __ffsll(tied) - 1;
-      win = (uint32_t)__builtin_amdgcn_readlane((int)(lane + 64u * bj), wl);
-    } else {
-      const uint32_t k = nk::wave_reduce_u32<false>(best == m ? (bj << 6) | lane : 0xffffffffu);
-      win = (k & 63u) + 64u * (k >> 6);
-    }
-    if (lane == (win & 63u)) {
-#pragma unroll
-      for (uint32_t j = 0; j < P; ++j)
-        if (j == (win >> 6)) code[j] = 0u;
+      for (uint32_t j = 0; j + 1 < P; ++j) key[j] = key[j + 1];
+      key[P - 1] = 0ull;
     }
     if (lane == r) { my_id = win; my_code = m; }
   }
   const float z = nk::from_order_bits(my_code);
-  const float z0 = __shfl(z, 0);
+  const float z0 = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(z), 0));
   const float ex = lane < K ? nk::nexp(z - z0) : 0.0f;
   float sum = 0.0f;
   for (uint32_t r = 0; r < K; ++r) sum = sum + __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(ex), (int)r));

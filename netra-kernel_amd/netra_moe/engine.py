@@ -367,6 +367,18 @@ def ffn_variant(cfg: MoEConfig) -> str:
     return "narrow" if cfg.T <= FFN_NARROW_T else "wide"
 
 
+# (H, I) with a single-token down kernel (netra_moe_ffn_down_h<H>_i<I>_single)
+SINGLE_DOWN = {(2048, 512)}
+
+
+def down_variant(cfg: MoEConfig) -> str:
+    """single (one workgroup per 16 output columns across all routes, the
+    combine in the workgroup) for one token, else the FFN variant."""
+    if cfg.T == 1 and (cfg.H, cfg.I) in SINGLE_DOWN and cfg.Ktot <= 16:
+        return "single"
+    return ffn_variant(cfg)
+
+
 def ffn_lds_bytes(cfg: MoEConfig) -> tuple[int, int]:
     """Static LDS of netra_moe_ffn_{gate_up,down}_h<H>_i<I>_<v> (their
     __shared__ arrays, rounded up)."""
@@ -376,6 +388,8 @@ def ffn_lds_bytes(cfg: MoEConfig) -> tuple[int, int]:
     gu = max(kb * 2048, red, 1024 * 4 + 513 * 4) + 64 * kb + (8 if narrow else 16 * (128 * FFN_WIDE_P[(cfg.H, cfg.I)] + 8)) * 2
     gu += 64 * 16 * 4 + 512 * 8 + 2 * 513 * 4 + 48 * 4
     dn = max(kbi * 2048, red) + 64 * kbi + 4
+    if down_variant(cfg) == "single":
+        dn = 8 * 2 * cfg.I + 16 * 16 * 4
     return (gu + 255) // 256 * 256, (dn + 255) // 256 * 256
 
 
@@ -420,8 +434,9 @@ def _fused_decode(cfg: MoEConfig) -> list[dict]:
                    "kernels/gfx950/templates/moe/decode/silu_quant.inc:16-236",
                    "kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]
              + (["runtime/gfx950/routing/decode/qwen36_shared_gate_append_bridge.hip:76-112"] if narrow else [])),
-        dict(name="moe.down", symbol=f"netra_moe_ffn_down_h{H}_i{I}_{v}_gfx950",
-             grid=(ffn_grid(cfg, "down"), 1, 1), block=(512, 1, 1), lds=lds_dn, dyn=0,
+        dict(name="moe.down", symbol=f"netra_moe_ffn_down_h{H}_i{I}_{down_variant(cfg)}_gfx950",
+             grid=(H // 16 if down_variant(cfg) == "single" else ffn_grid(cfg, "down"), 1, 1), block=(512, 1, 1),
+             lds=lds_dn, dyn=0,
              args=["topk_weights", "w2", "w2_scale", "sorted_ids", "sorted_expert", "tile_map", "num_valid",
                    "h_rows", "h_q", "h_scale", "partial", "ffn_counters", "out",
                    u(T), u(cfg.E), u(cfg.K), u(cfg.S)],
@@ -430,6 +445,9 @@ def _fused_decode(cfg: MoEConfig) -> list[dict]:
              writes=["h_q", "h_scale", "partial", "ffn_counters", "out"],
              refs=["kernels/gfx950/templates/moe/decode/down_reduce_mfma_2wave.inc:14-291"]),
     ]
+    if down_variant(cfg) == "single":  # no hand-off: the combine counters stay untouched
+        ops[-1]["reads"].remove("ffn_counters")
+        ops[-1]["writes"].remove("ffn_counters")
     if v == "wide":  # the wide down leaves the fp32 partials to the combine kernel
         ops[-1]["writes"] = ["partial"]
         ops.append(dict(name="moe.combine", symbol="netra_moe_combine_gfx950",

@@ -568,7 +568,15 @@ __device__ __forceinline__ void ffn_down(
   // rows (wave w < KBI: 128-column block w, lane l row l & 15, columns
   // 32 (l >> 4) .. + 31) load together with the tile count
   const uint32_t cap_blocks = (T * Ktot + 63u) / 64u + Etot;
-  const uint32_t g_first = blockIdx.x / GB;
+  // Items, XCD-aware: workgroups are dealt round-robin over the 8 XCDs, so
+  // workgroup i (XCD i % 8, j = i / 8) takes column group j % GB of tile slot
+  // j / GB of its XCD (tiles round-robin over the XCDs): a tile's GB items
+  // share one L2 and fetch its h operand once. Round r adds r * grid. (A grid
+  // that is not a multiple of 8 GB keeps item = workgroup.)
+  const uint32_t off = gridDim.x % (8u * GB) == 0u
+                           ? ((blockIdx.x / 8u / GB) * 8u + blockIdx.x % 8u) * GB + (blockIdx.x / 8u) % GB
+                           : blockIdx.x;
+  const uint32_t g_first = off / GB;
   nkstream::TileRows tr_first;
   uint4 h_first[kFromRows ? 4 : 1];
   auto load_hrows = [&](uint4 (&v)[kFromRows ? 4 : 1], uint32_t g) __attribute__((always_inline)) {
@@ -577,12 +585,27 @@ __device__ __forceinline__ void ffn_down(
 #pragma unroll
     for (uint32_t q = 0; q < (kFromRows ? 4u : 1u); ++q) v[q] = src[q];
   };
+  // wide: the first item's tile_map entry loads with the tile count (its
+  // block clamped: past the count the entry may hold stale bytes), its rows
+  // and h operand (fp8 block and scales) right after
+  const uint32_t cap_tiles = (T * Ktot + 15u) / 16u + Etot;
+  uint4 q_first[2];
+  float s_first = 0.0f;
   if constexpr (kFromRows) {
     const uint32_t b = min(g_first, cap_blocks - 1u);
     nkstream::load_rows(tr_first, sorted_ids, sorted_expert, b, b * 64u, T, Ktot, Etot, true);
     if (wave < KBI) load_hrows(h_first, b);
+  } else {
+    nkstream::load_tile(tr_first, tile_map, sorted_ids, sorted_expert, min(g_first, cap_tiles - 1u), T, Ktot, Etot,
+                        true, cap_blocks - 1u);
+    if (wave < KBI) {
+      const size_t blk = (size_t)(tr_first.row0 >> 4) * KBI + wave;
+      q_first[0] = *reinterpret_cast<const uint4*>(hq + blk * 2048u + lane * 16u);
+      q_first[1] = *reinterpret_cast<const uint4*>(hq + blk * 2048u + 1024u + lane * 16u);
+      if (lane < 16u) s_first = hs[blk * 16u + lane];
+    }
   }
-  const uint32_t ntile = min((uint32_t)num_valid[2], kFromRows ? cap_blocks : (T * Ktot + 15u) / 16u + Etot);
+  const uint32_t ntile = min((uint32_t)num_valid[2], kFromRows ? cap_blocks : cap_tiles);
 
   // Combine hand-off of the held items: once every wave's partial stores have
   // completed, wave w lane l counts the arrival of held item 4w + (l >> 4),
@@ -644,15 +667,17 @@ __device__ __forceinline__ void ffn_down(
   };
 
 #pragma unroll 1
-  for (uint32_t item = blockIdx.x; item < ntile * GB; item += gridDim.x) {
+  for (uint32_t item = off; item < ntile * GB; item += gridDim.x) {
     const uint32_t g = item / GB, grp = item % GB;
     nkstream::TileRows tr;
-    const bool first = kFromRows && item == blockIdx.x && g_first < cap_blocks;  // rows loaded at the start
-    if constexpr (kFromRows) {
-      if (first) tr = tr_first;
-      else nkstream::load_rows(tr, sorted_ids, sorted_expert, g, g * 64u, T, Ktot, Etot, true);
+    // rows (and h) loaded at the start
+    const bool first = item == off && g_first < (kFromRows ? cap_blocks : cap_tiles);
+    if (first) {
+      tr = tr_first;
+    } else if constexpr (kFromRows) {
+      nkstream::load_rows(tr, sorted_ids, sorted_expert, g, g * 64u, T, Ktot, Etot, true);
     } else {
-      nkstream::load_tile(tr, tile_map, sorted_ids, sorted_expert, g, T, Ktot, Etot, true);
+      nkstream::load_tile(tr, tile_map, sorted_ids, sorted_expert, g, T, Ktot, Etot, true, cap_blocks - 1u);
     }
     const uint32_t e = (uint32_t)tr.expert, row0 = tr.row0;
     const int32_t route = tr.row;  // lane l: the route of row l & 15, -1 for padding
@@ -701,6 +726,10 @@ __device__ __forceinline__ void ffn_down(
           *reinterpret_cast<uint4*>(hq + blk * 2048u + 1024u + lane * 16u) = qhi;
           if (lane < 16u) hs[blk * 16u + lane] = scale;
         }
+      } else if (first) {
+        qlo = q_first[0];
+        qhi = q_first[1];
+        scale = s_first;
       } else {
         qlo = *reinterpret_cast<const uint4*>(hq + blk * 2048u + lane * 16u);
         qhi = *reinterpret_cast<const uint4*>(hq + blk * 2048u + 1024u + lane * 16u);

@@ -59,12 +59,16 @@ __device__ __forceinline__ void load_rows(TileRows& tr, const int32_t* __restric
   tr.row = (t < T && slot < Ktot) ? (int32_t)(as_route ? t * Ktot + slot : t) : -1;
 }
 
+// max_block bounds the block a tile_map entry names (an entry past the tile
+// count, read ahead of it, may hold stale bytes).
 __device__ __forceinline__ void load_tile(TileRows& tr, const int32_t* __restrict__ tile_map,
                                           const int32_t* __restrict__ sorted_ids,
                                           const int32_t* __restrict__ sorted_expert, uint32_t tile,
-                                          uint32_t T, uint32_t Ktot, uint32_t Etot, bool as_route) {
+                                          uint32_t T, uint32_t Ktot, uint32_t Etot, bool as_route,
+                                          uint32_t max_block = 0xffffffffu) {
   const uint32_t m = (uint32_t)tile_map[tile];
-  load_rows(tr, sorted_ids, sorted_expert, m >> 2, (m >> 2) * 64u + (m & 3u) * 16u, T, Ktot, Etot, as_route);
+  const uint32_t b = min(m >> 2, max_block);
+  load_rows(tr, sorted_ids, sorted_expert, b, b * 64u + (m & 3u) * 16u, T, Ktot, Etot, as_route);
 }
 
 }  // namespace nkstream

@@ -48,6 +48,18 @@ EXTRA_CONFIGS = {
     # more than 256 experts: the 512-expert route_select / top-k / sort variants
     "shape_e384": MoEConfig("shape_e384", T=96, H=1024, E=384, K=6, I=256, S=1,
                             router_bias="zipf1.1", seed=1104),
+    # the narrow decode FFN (1 < T <= 8: top-k in the gate/up prologue, one
+    # A operand of every token row, the combine hand-off in down) on each of
+    # its shapes; hot: every token on the same experts, 8 rows per tile
+    "narrow_t4": MoEConfig("narrow_t4", T=4, H=2048, E=256, K=8, I=512, S=1, seed=1106),
+    "narrow_t8_hot": MoEConfig("narrow_t8_hot", T=8, H=2048, E=256, K=8, I=512, S=1,
+                               router_bias="hot", seed=1107),
+    "narrow_t3_h4096": MoEConfig("narrow_t3_h4096", T=3, H=4096, E=32, K=4, I=256, S=1, seed=1108),
+    "narrow_t5_h1024_i1024": MoEConfig("narrow_t5_h1024_i1024", T=5, H=1024, E=24, K=3, I=1024, S=1,
+                                       seed=1109),
+    "narrow_t2_h512": MoEConfig("narrow_t2_h512", T=2, H=512, E=16, K=2, I=256, S=0, seed=1110),
+    # the single-token down with sixteen routes (two tiles per wave), no shared expert
+    "single_k16": MoEConfig("single_k16", T=1, H=2048, E=256, K=16, I=512, S=0, seed=1111),
 }
 CONFIGS = {**BASELINE_CONFIGS, **EXTRA_CONFIGS}
 CASES = [(name, path) for name in CONFIGS for path in ("fused", "stream", "tile")

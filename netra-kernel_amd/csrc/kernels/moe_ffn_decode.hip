@@ -359,7 +359,18 @@ __device__ __forceinline__ void ffn_gate_up(
 
   // ---- items --------------------------------------------------------------------------------
 #pragma unroll 1
-  for (uint32_t item = blockIdx.x; item < ntile * GA; item += gridDim.x) {
+  for (uint32_t base = 0; base < ntile * GA; base += gridDim.x) {
+    // round base: items base .. base + grid - 1. Wide: dealt XCD-major over
+    // the round's items (workgroup i runs on XCD i % 8), so an expert's
+    // consecutive tiles (the shared expert's four at T = 64) stream its
+    // weights concurrently through one L2; narrow: item = base + workgroup
+    uint32_t item = base + blockIdx.x;
+    if (!kStageAll && gridDim.x % 8u == 0u) {
+      if (!nklds::xcd_item(blockIdx.x, min(gridDim.x, ntile * GA - base), item)) break;
+      item += base;
+    } else if (item >= ntile * GA) {
+      break;
+    }
     const uint32_t g = item / GA, grp = item % GA;
     uint32_t e, k, row0;  // the tile's expert, its sub-tile among e's rows and its sorted position
     if constexpr (kStageAll) {

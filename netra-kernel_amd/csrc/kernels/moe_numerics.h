@@ -224,6 +224,21 @@ __device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v) {
   return pick(pick(a, b), pick(c, d));
 }
 
+// Wave-wide unsigned max with the result in every lane (every lane active):
+// the same DPP row steps, then v_permlane16_swap (rows 0 <-> 1, 2 <-> 3) and
+// v_permlane32_swap (the two halves), each followed by a max of the lane's
+// own and swapped values: no scalar round trip.
+__device__ __forceinline__ uint32_t wave_max_u32_all(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max((uint32_t)r16[0], (uint32_t)r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max((uint32_t)r32[0], (uint32_t)r32[1]);
+}
+
 // Order-preserving map of fp32 onto uint32 (larger float -> larger code);
 // -0 is first folded onto +0 so the two compare equal. Finite and infinite
 // inputs map to codes >= 0x007fffff, so 0 is free as an "absent" marker.

@@ -252,17 +252,17 @@ __device__ __forceinline__ void topk_select(const uint16_t* __restrict__ lrow, c
   uint32_t my_id = 0, my_code = 0;
   for (uint32_t r = 0; r < K; ++r) {
     const uint32_t hc = (uint32_t)(key[0] >> 32), hl = (uint32_t)key[0];
-    const uint32_t m = nk::wave_reduce_u32<true>(hc);
+    const uint32_t m = nk::wave_max_u32_all(hc);  // in every lane
     const unsigned long long tied = __ballot(hc == m);
-    uint32_t wl;  // the winning lane
-    if (__popcll(tied) == 1) wl = (uint32_t)(__ffsll((long long)tied) - 1);
-    else wl = (0xffffffffu - nk::wave_reduce_u32<true>(hc == m ? hl : 0u)) & 63u;
+    uint32_t wl = (uint32_t)(__ffsll((long long)tied) - 1);  // the winning lane (uniform)
+    if (__popcll(tied) != 1)  // several lanes offer the code: the lowest expert wins
+      wl = (0xffffffffu - (uint32_t)__builtin_amdgcn_readfirstlane((int)nk::wave_max_u32_all(hc == m ? hl : 0u))) &
+           63u;
     const uint32_t win = 0xffffffffu - (uint32_t)__builtin_amdgcn_readlane((int)hl, (int)wl);
-    if (lane == wl) {
+    const bool shift = lane == wl;
 #pragma unroll
-      for (uint32_t j = 0; j + 1 < P; ++j) key[j] = key[j + 1];
-      key[P - 1] = 0ull;
-    }
+    for (uint32_t j = 0; j + 1 < P; ++j) key[j] = shift ? key[j + 1] : key[j];
+    key[P - 1] = shift ? 0ull : key[P - 1];
     if (lane == r) { my_id = win; my_code = m; }
   }
   const float z = nk::from_order_bits(my_code);

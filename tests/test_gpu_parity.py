@@ -58,6 +58,11 @@ EXTRA_CONFIGS = {
     "narrow_t5_h1024_i1024": MoEConfig("narrow_t5_h1024_i1024", T=5, H=1024, E=24, K=3, I=1024, S=1,
                                        seed=1109),
     "narrow_t2_h512": MoEConfig("narrow_t2_h512", T=2, H=512, E=16, K=2, I=256, S=0, seed=1110),
+    # the wide decode FFN at the headline shape: full 16-row tiles (hot
+    # routing) and a ragged token count
+    "wide_t16_hot": MoEConfig("wide_t16_hot", T=16, H=2048, E=256, K=8, I=512, S=1, router_bias="hot",
+                              seed=1112),
+    "wide_t33": MoEConfig("wide_t33", T=33, H=2048, E=256, K=8, I=512, S=1, seed=1113),
     # the single-token down with sixteen routes (two tiles per wave), no shared expert
     "single_k16": MoEConfig("single_k16", T=1, H=2048, E=256, K=16, I=512, S=0, seed=1111),
 }

@@ -63,6 +63,10 @@ EXTRA_CONFIGS = {
     "wide_t16_hot": MoEConfig("wide_t16_hot", T=16, H=2048, E=256, K=8, I=512, S=1, router_bias="hot",
                               seed=1112),
     "wide_t33": MoEConfig("wide_t33", T=33, H=2048, E=256, K=8, I=512, S=1, seed=1113),
+    # every hot expert with 64 rows (four tiles each, as the shared expert):
+    # multi-tile experts throughout the wide decode FFN
+    "wide_t64_hot": MoEConfig("wide_t64_hot", T=64, H=2048, E=256, K=8, I=512, S=1, router_bias="hot",
+                              seed=1114),
     # the single-token down with sixteen routes (two tiles per wave), no shared expert
     "single_k16": MoEConfig("single_k16", T=1, H=2048, E=256, K=16, I=512, S=0, seed=1111),
 }

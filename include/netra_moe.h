@@ -14,14 +14,18 @@
 // down_reduce_mfma_2wave.inc:14-291) and the route reducer
 // (moe/prefill/route_reduce_splitk2_f16.inc:6-117):
 //
-//   netra_moe_router_h<H>_t<NT>_gfx950, H in {512,1024,2048,4096} (x bf16[T,H],
-//       w bf16[E+S,H], logits bf16[T,E+S], xq e4m3[T,H], xs f32[T,H/128],
-//       mask u64[(E+S)*W]; T, H, rows=E+S, (E+S)*W)
-//       grid (ceil(rows/16), ceil(T/NT)), block 256, NT = max(1, 2048/H) for T <= 128 else 4
-//       (NT = 2 for H = 4096),
-//       static LDS 4 * NT * H bytes
-//   netra_moe_topk_gfx950(logits, bias f32[E], ids i32[T,Ktot], weights f32[T,Ktot],
-//       mask; T, E, K, S, W)   grid ceil(T/4), block 256 (one wave per token)
+//   exact front end, H in {512,1024,2048,4096}:
+//   netra_moe_route_h<H>_t<NT>_gfx950(x bf16[T,H], w bf16[E+S,H], bias f32[E],
+//       logits bf16[T,E+S], xq e4m3[T,H], xs f32[T,H/128], ids i32[T,Ktot],
+//       weights f32[T,Ktot], counters u32[64*ceil(T/NT)] (zero before the first
+//       launch, zero again after each); T, H, rows=E+S, E, K, S)
+//       grid (ceil(rows/16), ceil(T/NT)), block 256, NT = max(1, 2048/H) for T <= 128
+//       else 4 (NT = 2 for H = 4096); router logits and input quant, then top-k by
+//       each token group's last workgroup to finish
+//   netra_moe_router_logits_h<H>_t<NT>_gfx950(x, w, logits, xq, xs; T, H, rows)
+//       the same grid without the top-k (in front of the narrow decode FFN)
+//   netra_moe_router_h2048_t1_gfx950(x, w, logits, xq, xs, mask; T, H, rows,
+//       mask_words)   the router bridge's kernel (xq and mask may be null)
 //   netra_moe_sort_gfx950(ids, mask, sorted_ids i32[CAP*64], sorted_expert i32[CAP],
 //       tile_map i32[CAPT], pair_map i32[CAP], num_valid i32[4], counts i32[E+S];
 //       T, Ktot, Etot, W, CAP)
@@ -29,10 +33,10 @@
 //       B = Etot*W + 4*Etot + 51 + CAP rounded up to even
 //   prefill ("screen") front end, H in {512,1024,2048}, EMAX in {256,512}:
 //   netra_moe_route_screen_h<H>_k<KBS>_gfx950(x, w, screen f32[Z,T,RP],
-//       wsq f32[Z,RP]; T, H, rows, RP)   grid (ceil(T/64), RP/64, Z), block 256,
-//       RP = rows rounded up to 64, Z = H/128/KBS K splits (KBS in {2,4,8,16},
-//       at most H/128); workgroups with blockIdx.x == 0 write the partial
-//       squared router-row norms wsq
+//       wsq f32[Z,RP]; T, H, E, RP)   grid (ceil(T/128), ceil(RP/128), Z), block 256,
+//       RP = E rounded up to 64 (the shared-gate row is not screened), Z = H/128/KBS
+//       K splits (KBS in {2,4,8,16}, at most H/128); workgroups with
+//       blockIdx.x == 0 write the partial squared router-row norms wsq
 //   netra_moe_route_select_h<H>_e<EMAX>_w<W>_gfx950(x, w, bias, screen, wsq, logits,
 //       ids, weights, xq, xs, route_base i32[Etot,G], route_rank i32[T*Ktot];
 //       T, H, E, K, S, RP, Z)   grid G = ceil(T/W), block 64*W, W in {4,8}
@@ -41,6 +45,22 @@
 //   netra_moe_sort_place_gfx950(ids, route_base, route_rank, counts, sorted_ids,
 //       sorted_expert, tile_map, pair_map, num_valid; T, Ktot, Etot, G, W, CAP)
 //       grid max(ceil(T*Ktot/256), ceil(Etot/4)), block 256, dynamic LDS 4*(4*Etot+3)
+//   fused decode FFN (T <= 64), (H, I) in {(512,256), (1024,1024), (2048,512), (4096,256)}:
+//   netra_moe_ffn_gate_up_h<H>_i<I>_<wide|narrow>_gfx950(logits, bias, ids, weights,
+//       xq, xs, w13, w13s, sorted_ids, sorted_expert, tile_map, pair_map, num_valid,
+//       counts, hrows bf16[CAPT*16,I], hq, hs; T, E, K, S, CAP)
+//       block 512, grid 256 (wide, or H = 4096) / 512 (narrow); the sort rebuilt in
+//       the prologue (its outputs as netra_moe_sort_gfx950's); wide (8 < T) reads
+//       ids and requantises h to hq / hs; narrow (T <= 8) runs the top-k from
+//       logits + bias itself (writing ids / weights) and writes bf16 h rows
+//   netra_moe_ffn_down_h<H>_i<I>_<wide|narrow>_gfx950(weights, w2, w2s, sorted_ids,
+//       sorted_expert, tile_map, num_valid, hrows, hq, hs, partial f32[T*Ktot,H],
+//       counters u32[64*64], out bf16[T,H]; T, E, K, S)   block 512, grid 2048 (wide)
+//       / 1024 (narrow); wide leaves the partials to netra_moe_combine_gfx950,
+//       narrow combines through the counters (zero before and after each launch)
+//   netra_moe_ffn_down_h2048_i512_single_gfx950(the same arguments)   T = 1,
+//       grid H/16, block 512: a workgroup owns 16 output columns across all
+//       routes and writes out itself (partial for inspection; counters unused)
 //   decode ("stream") GEMMs, H in {512,1024,2048,4096}, I in {256,512,1024,2048}:
 //   (every w13 below is in the gate/up-interleaved tile16x128 layout of
 //   netra_moe_pack_tiles_gate_up)

@@ -1,7 +1,11 @@
-// Routing front end, three kernels per layer call:
-//   router  bf16 router logits (+ shared-gate logit) and the 1x128 input quant
-//   topk    top-k + renormalised softmax + shared-expert append per token
-//   sort    count / scan / pad / scatter into 64-row expert blocks
+// Routing front end:
+//   route          bf16 router logits (+ shared-gate logit), the 1x128 input
+//                  quant, and top-k + renormalised softmax + shared-expert
+//                  append per token (by each token group's last workgroup)
+//   router_logits  the logits and the quant only (the narrow decode FFN runs
+//                  the top-k in its prologue); router: the same with the
+//                  routing bitmask cleared (the router bridge)
+//   sort           count / scan / pad / scatter into 64-row expert blocks
 #pragma once
 #include "moe_numerics.h"
 
@@ -26,9 +30,9 @@
 // row slice loads are issued first and overlap the staging. Workgroups of
 // column 0 also quantise their tokens from the staging registers: each 16-lane
 // group holds one 128-element block, scale = max(amax, 1e-10) * 0x3b124925,
-// q = e4m3(x * (1 / scale)). Every workgroup zeroes a slice of the routing
-// bitmask that topk fills later on the same stream. With xq and mask null
-// (the router bridge) only the logits are written.
+// q = e4m3(x * (1 / scale)). With mask non-null every workgroup zeroes a
+// slice of the routing bitmask (mask_words words in all); with xq and mask
+// null (the router bridge) only the logits are written.
 template <uint32_t NJ>
 __device__ __forceinline__ void load_slice(uint4 (&v)[NJ], const uint16_t* p) {
 #pragma unroll
@@ -170,15 +174,11 @@ NK_ROUTER_LOGITS(1024, 2)
 NK_ROUTER_LOGITS(2048, 1)
 NK_ROUTER_LOGITS(4096, 2)
 
-// Symbol netra_moe_router_h<H>_t<NT>_gfx950: NT tokens per workgroup (for
-// small T the fewest the staging allows, NT * H a multiple of 2048: each
-// wave's fmaf chains run fewer tokens and more workgroups share the weight
-// rows; 7.9 -> 6.0 us at T = 64, H = 2048).
-NK_ROUTER(512, 4)
-NK_ROUTER(1024, 2)
-NK_ROUTER(1024, 4)
+// Symbol netra_moe_router_h2048_t1_gfx950: the router bridge's kernel. (NT
+// tokens per workgroup elsewhere: for small T the fewest the staging allows,
+// NT * H a multiple of 2048, so each wave's fmaf chains run fewer tokens and
+// more workgroups share the weight rows; 7.9 -> 6.0 us at T = 64, H = 2048.)
 NK_ROUTER(2048, 1)
-NK_ROUTER(2048, 4)
 NK_ROUTER(4096, 2)
 
 // ---------------------------------------------------------------------------
@@ -289,13 +289,11 @@ __device__ __forceinline__ void topk_select_any(const uint16_t* __restrict__ lro
   else topk_select<8, kCoherent>(lrow, bias, E, K, S, lane, id, weight);
 }
 
-// One token's selection stored as topk_ids / topk_weights rows, and (mask
-// non-null) its experts' bits in the routing bitmask.
+// One token's selection stored as its topk_ids / topk_weights rows.
 template <bool kCoherent = false>
 __device__ __forceinline__ void topk_token(const uint16_t* __restrict__ lrow, const float* __restrict__ bias,
-                                           int32_t* __restrict__ ids, float* __restrict__ weights,
-                                           unsigned long long* __restrict__ mask, uint32_t t, uint32_t E,
-                                           uint32_t K, uint32_t S, uint32_t W, uint32_t lane) {
+                                           int32_t* __restrict__ ids, float* __restrict__ weights, uint32_t t,
+                                           uint32_t E, uint32_t K, uint32_t S, uint32_t lane) {
   const uint32_t Ktot = K + S;
   uint32_t id = 0;
   float weight = 0.0f;
@@ -303,20 +301,7 @@ __device__ __forceinline__ void topk_token(const uint16_t* __restrict__ lrow, co
   if (lane < Ktot) {
     ids[(size_t)t * Ktot + lane] = (int32_t)id;
     weights[(size_t)t * Ktot + lane] = weight;
-    if (mask != nullptr) atomicOr(&mask[(size_t)id * W + (t >> 6)], 1ull << (t & 63u));
   }
-}
-
-NK_KERNEL __launch_bounds__(256) void netra_moe_topk_gfx950(
-    const uint16_t* __restrict__ logits, const float* __restrict__ bias,
-    int32_t* __restrict__ ids, float* __restrict__ weights,
-    unsigned long long* __restrict__ mask, uint32_t T, uint32_t E, uint32_t K, uint32_t S,
-    uint32_t W) {
-  const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t t = blockIdx.x * 4u + (threadIdx.x >> 6);
-  if (t >= T || E > 512u || K > E || K + S > 64u) return;  // wave-uniform
-  const uint16_t* lrow = logits + (size_t)t * (E + S);
-  topk_token(lrow, bias, ids, weights, mask, t, E, K, S, W, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -351,7 +336,7 @@ __device__ __forceinline__ void route(const uint16_t* __restrict__ x, const uint
   const uint32_t t = blockIdx.y * NT + wave;
   if (wave < NT && t < T && E <= 512u && K <= E && K + S <= 64u) {  // wave-uniform
     const uint16_t* lrow = logits + (size_t)t * rows;
-    topk_token<true>(lrow, bias, ids, weights, nullptr, t, E, K, S, 0u, lane);
+    topk_token<true>(lrow, bias, ids, weights, t, E, K, S, lane);
   }
   if (threadIdx.x == 0)
     __hip_atomic_store(&counters[kCounterStride * blockIdx.y], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -264,6 +264,11 @@ __device__ __forceinline__ void route_select(
   // dependent round trips of the original order overlap.
   const uint32_t t_w = blockIdx.x * W + wave;
   const bool active = t_w < T;
+  // The split partial sums come kZBatch splits at a time, every load of a
+  // batch issued before the first add (indices clamped into range, so no load
+  // sits under a condition, which would make each one its own round trip);
+  // the adds run in split order from the first split's value.
+  constexpr uint32_t kZBatch = 4;
   uint4 xv[H / 512u];
   float aval[P], bv[P];
   if (active) {
@@ -272,25 +277,39 @@ __device__ __forceinline__ void route_select(
       xv[p] = *reinterpret_cast<const uint4*>(x + (size_t)t_w * H + 512u * p + 8u * lane);
     const float* srow = screen + (size_t)t_w * RP;  // split z at srow + z * T * RP
 #pragma unroll
-    for (uint32_t j = 0; j < P; ++j) {
-      const uint32_t e = lane + 64u * j;
-      aval[j] = 0.0f;
-      bv[j] = 0.0f;
-      if (e < E) {
-        float a = srow[e];
-        for (uint32_t z = 1; z < Z; ++z) a += srow[(size_t)z * T * RP + e];
-        aval[j] = a;
-        bv[j] = bias[e];
+    for (uint32_t j = 0; j < P; ++j) bv[j] = bias[min(lane + 64u * j, E - 1u)];
+    for (uint32_t z0 = 0; z0 < Z; z0 += kZBatch) {  // uniform; one trip for Z <= kZBatch
+      float part[kZBatch][P];
+#pragma unroll
+      for (uint32_t zz = 0; zz < kZBatch; ++zz) {
+        const float* sz = srow + (size_t)min(z0 + zz, Z - 1u) * T * RP;
+#pragma unroll
+        for (uint32_t j = 0; j < P; ++j) part[zz][j] = sz[min(lane + 64u * j, E - 1u)];
       }
+#pragma unroll
+      for (uint32_t zz = 0; zz < kZBatch; ++zz)
+        if (z0 + zz < Z) {
+#pragma unroll
+          for (uint32_t j = 0; j < P; ++j) aval[j] = z0 + zz == 0u ? part[zz][j] : aval[j] + part[zz][j];
+        }
     }
+#pragma unroll
+    for (uint32_t j = 0; j < P; ++j)
+      if (lane + 64u * j >= E) aval[j] = bv[j] = 0.0f;
   }
   for (uint32_t e = tid; e <= EMAX; e += kThreads) {
     s_hist[e] = 0u;
-    if (e < E) {
-      float q = 0.0f;
-      for (uint32_t z = 0; z < Z; ++z) q += wsq[(size_t)z * RP + e];
-      s_wn[e] = sqrtf(q) * kNormSlack;
+    float wz[8];  // every split's partial norm at once (Z <= 8 for H <= 2048; more run a second batch)
+    const uint32_t ec = min(e, E - 1u);
+    float q = 0.0f;
+    for (uint32_t z0 = 0; z0 < Z; z0 += 8u) {
+#pragma unroll
+      for (uint32_t zz = 0; zz < 8u; ++zz) wz[zz] = wsq[(size_t)min(z0 + zz, Z - 1u) * RP + ec];
+#pragma unroll
+      for (uint32_t zz = 0; zz < 8u; ++zz)
+        if (z0 + zz < Z) q += wz[zz];
     }
+    if (e < E) s_wn[e] = sqrtf(q) * kNormSlack;
   }
   __syncthreads();
   const uint32_t s = lane & 15u, g = lane >> 4;

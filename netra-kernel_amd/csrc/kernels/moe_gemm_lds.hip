@@ -50,10 +50,12 @@ constexpr uint32_t kThreads = 512;
 constexpr uint32_t kStages = 3;
 constexpr uint32_t kRowsPerBlock = 64;
 constexpr uint32_t kRows = 128;                   // two blocks
-constexpr uint32_t kABytes = 8u * 2048u;          // 8 row tiles
+constexpr uint32_t kTailTile = 8;                 // row tile of an absorbed tail (rows 128 .. 143)
+constexpr uint32_t kAllRows = kRows + 16u;
+constexpr uint32_t kABytes = 9u * 2048u;          // 8 row tiles + the tail tile
 constexpr uint32_t kBBytes = 16u * 2048u;         // 8 gate + 8 up weight tiles
 constexpr uint32_t kStageBytes = kABytes + kBBytes;
-constexpr uint32_t kCopiesPerWave = 6;            // per step: A tile (2) + gate tile (2) + up tile (2)
+constexpr uint32_t kCopiesPerWave = 7;            // per step: A tile (2) + gate tile (2) + up tile (2) [+ tail share (1)]
 constexpr uint32_t kFar = 0x80000000u;            // an offset past the activation range (T * H < 2^31): zeros
 
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
@@ -161,13 +163,13 @@ __device__ __forceinline__ void gate_up_lds(
   constexpr uint32_t H = 128u * KB;
   static_assert(2u * KB <= 64u && KB % 4u == 0, "scale copies");
   constexpr uint32_t kAsLanesPerRow = KB / 4u, kAsRowsPerCopy = 64u / kAsLanesPerRow;
+  constexpr uint32_t kAsCopies = (kAllRows + kAsRowsPerCopy - 1u) / kAsRowsPerCopy;  // 1 KiB each
+  static_assert(kAsCopies <= 9u, "scale copies: one per wave, plus one by wave 0");
   auto as_swizzle = [](uint32_t r) { return (r >> 2) & (kAsLanesPerRow - 1u); };
   __shared__ __align__(16) uint8_t s_stage[kStages][kStageBytes];
-  __shared__ __align__(16) float s_as[8u * 256u];        // a_s(row, kb) at row * KB + kb (8 wave copies)
-  __shared__ __align__(16) float s_wsv[kThreads / 64u][64];  // each wave's copy of the weight block scales
-  __shared__ int32_t s_tok[kRows];
-  __shared__ float s_amax[2][4][kRowsPerBlock];
-  __shared__ float s_scale[kRows];
+  __shared__ __align__(16) float s_as[kAsCopies * 256u];  // a_s(row, kb) at row * KB + kb (swizzled chunks)
+  __shared__ __align__(16) float s_wsv[64];               // weight block scales: lane kb gate, KB + kb up
+  __shared__ int32_t s_tok[kAllRows + 1u];
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
   const uint32_t NG = I / 128u;
@@ -177,19 +179,38 @@ __device__ __forceinline__ void gate_up_lds(
   const uint32_t nblocks = (uint32_t)num_valid[0] / kRowsPerBlock;
   const uint32_t b0 = (uint32_t)pair_map[p];
   if (b0 >= nblocks) return;
-  // the rows' sorted ids and both blocks' experts in one round trip (the
-  // prologue's dependent loads are the item's fixed cost)
-  const bool has2 = b0 + 1u < nblocks;
+  // The rows' sorted ids, the first 17 of the next block, and the experts of
+  // the blocks around the pair, in one round trip (the prologue's dependent
+  // loads are the item's fixed cost). An expert whose rows end in a last
+  // block of at most 16 rows (after an even number of full blocks) has that
+  // tail computed by the item of the pair before it, as row tile 8: the
+  // tail's own item would stream the expert's whole W13 slice again for a
+  // few rows.
+  const bool has2 = b0 + 1u < nblocks, has3 = b0 + 2u < nblocks;
   int32_t id = -1;
-  if (tid < kRows && (tid < kRowsPerBlock || has2)) id = sorted_ids[b0 * kRowsPerBlock + tid];
+  if (tid < kRows) {
+    if (tid < kRowsPerBlock || has2) id = sorted_ids[b0 * kRowsPerBlock + tid];
+  } else if (tid <= kAllRows) {
+    if (has3) id = sorted_ids[(b0 + 2u) * kRowsPerBlock + (tid - kRows)];
+  }
   const int32_t e = sorted_expert[b0];
   const int32_t e2 = has2 ? sorted_expert[b0 + 1u] : -1;
+  const int32_t e3 = has3 ? sorted_expert[b0 + 2u] : -1;
+  const int32_t e4 = b0 + 3u < nblocks ? sorted_expert[b0 + 3u] : -1;
+  const int32_t ep = b0 >= 1u ? sorted_expert[b0 - 1u] : -1;
   if (e < 0 || (uint32_t)e >= Etot) return;
   const bool two = e2 == e;
-  if (tid < kRows) {
+  if (tid <= kAllRows) {
     const uint32_t t = (uint32_t)id & 0xffffffu, slot = (uint32_t)id >> 24;
-    s_tok[tid] = (id >= 0 && (tid < kRowsPerBlock || two) && t < T && slot < Ktot) ? (int32_t)t : -1;
+    s_tok[tid] = (id >= 0 && (tid < kRowsPerBlock || tid >= kRows || two) && t < T && slot < Ktot) ? (int32_t)t : -1;
   }
+  __syncthreads();
+  // absorb: the pair's expert continues in block b0 + 2 and ends there with
+  // row 16 of it padding; skip: this single block is such a tail (the pair
+  // before it takes it), so that item and this one agree
+  const bool absorb = two && e3 == e && e4 != e && s_tok[kAllRows] < 0;
+  if (!two && ep == e && s_tok[16] < 0) return;
+  if (!absorb && tid >= kRows && tid < kAllRows) s_tok[tid] = -1;
   __syncthreads();
   const uint32_t m = wave >> 2, n = wave & 3u;  // row block, 32-column quarter
   const uint32_t nvalid = (uint32_t)__popcll(__ballot(s_tok[m * kRowsPerBlock + lane] >= 0));
@@ -204,6 +225,16 @@ __device__ __forceinline__ void gate_up_lds(
     const int32_t atok = s_tok[wave * 16u + r];
     avoff[h] = atok >= 0 ? (uint32_t)atok * H + (((lane & 7u) ^ row_swizzle(r)) * 16u) : kFar;
   }
+  // the tail tile's half w & 1 (rows 8 (w & 1) .. + 7, as an A copy): every
+  // wave copies one half, so four waves write the same bytes to the same
+  // place and each wave still issues seven copies per step with no branch in
+  // the K loop (a lane-masked copy there costs the loop its registers)
+  uint32_t tvoff;
+  {
+    const uint32_t r = 8u * (wave & 1u) + (lane >> 3);
+    const int32_t ttok = s_tok[kRows + r];
+    tvoff = ttok >= 0 ? (uint32_t)ttok * H + (((lane & 7u) ^ row_swizzle(r)) * 16u) : kFar;
+  }
   const u32x4 ra = rsrc(xq, T * H);
   const uint8_t* w13e = w13 + (size_t)e * 2u * I * H;
   // gate tile t and up tile t are adjacent (gate/up-interleaved W13), or I/16
@@ -213,39 +244,40 @@ __device__ __forceinline__ void gate_up_lds(
                         (up_tiles + 1u) * KB * 2048u);
   const uint32_t bvoff = lane * 16u;
   const uint32_t lds0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_offset(&s_stage[0][0]));
-  // copy q = 0..5 of step kb (A halves, gate halves, up halves) into its stage
+  // copy q = 0..6 of step kb (A halves, gate halves, up halves, tail share) into its stage
   auto issue_part = [&](uint32_t kb, uint32_t q) __attribute__((always_inline)) {
     const uint32_t st = lds0 + (kb % kStages) * kStageBytes;
     const uint32_t half = (q & 1u) * 1024u;
     if (q < 2u) copy16(st + wave * 2048u + half, ra, avoff[q], kb * 128u);
     else if (q < 4u) copy16(st + kABytes + wave * 2048u + half, rg, bvoff + half, kb * 2048u);
-    else copy16(st + kABytes + (8u + wave) * 2048u + half, rg, bvoff + half, (up_tiles * KB + kb) * 2048u);
-  };
-  auto issue = [&](uint32_t kb) __attribute__((always_inline)) {
-#pragma unroll
-    for (uint32_t q = 0; q < kCopiesPerWave; ++q) issue_part(kb, q);
+    else if (q < 6u) copy16(st + kABytes + (8u + wave) * 2048u + half, rg, bvoff + half, (up_tiles * KB + kb) * 2048u);
+    else copy16(st + kTailTile * 2048u + (wave & 1u) * 1024u, ra, tvoff, kb * 128u);
   };
   // The scales travel with the first step's copies (so no further round trip
-  // precedes the ring): wave w's copy moves the activation scales of rows
-  // (256 / KB) w .. + 256 / KB - 1 (KB / 4 lanes a row, zeros past the 128
-  // rows and for padding rows), and every wave copies the item's weight block
-  // scales for itself (lane kb: gate, lane KB + kb: up). Row r's 16-byte
-  // chunk c sits at slot c ^ as_swizzle(r), so the four rows 4 g + j (g =
-  // 0..3) a K step reads at once fall in four different banks.
+  // precedes the ring): copy c (wave c, and wave 0 for copy 8) moves the
+  // activation scales of rows (256 / KB) c .. + 256 / KB - 1 (KB / 4 lanes a
+  // row, zeros for padding rows), and wave 0 copies the item's weight block
+  // scales (lane kb: gate, lane KB + kb: up). Row r's 16-byte chunk c sits at
+  // slot c ^ as_swizzle(r), so the four rows 4 g + j (g = 0..3) a K step
+  // reads at once fall in four different banks.
   {
-    const uint32_t row = wave * kAsRowsPerCopy + lane / kAsLanesPerRow;
-    const int32_t stok = row < kRows ? s_tok[row] : -1;
-    const uint32_t chunk = (lane % kAsLanesPerRow) ^ as_swizzle(row);
-    const uint32_t xsoff = stok >= 0 ? (uint32_t)stok * KB * 4u + chunk * 16u : kFar;
-    copy16((uint32_t)__builtin_amdgcn_readfirstlane((int)lds_offset(&s_as[wave * 256u])), rsrc(xs, T * KB * 4u),
-           xsoff, 0u);
-    const float* wse = w13s + (size_t)e * (2u * I / 128u) * KB;
-    const uint32_t wsoff = lane < 2u * KB ? ((lane < KB ? ng : I / 128u + ng) * KB + lane % KB) * 4u : kFar;
-    copy4((uint32_t)__builtin_amdgcn_readfirstlane((int)lds_offset(&s_wsv[wave][0])),
-          rsrc(wse, (2u * I / 128u) * KB * 4u), wsoff, 0u);
+    const u32x4 rxs = rsrc(xs, T * KB * 4u);
+    auto scale_copy = [&](uint32_t c) __attribute__((always_inline)) {
+      const uint32_t row = c * kAsRowsPerCopy + lane / kAsLanesPerRow;
+      const int32_t stok = row < kAllRows ? s_tok[row] : -1;
+      const uint32_t chunk = (lane % kAsLanesPerRow) ^ as_swizzle(row);
+      const uint32_t xsoff = stok >= 0 ? (uint32_t)stok * KB * 4u + chunk * 16u : kFar;
+      copy16((uint32_t)__builtin_amdgcn_readfirstlane((int)lds_offset(&s_as[c * 256u])), rxs, xsoff, 0u);
+    };
+    if (wave < kAsCopies) scale_copy(wave);
+    if (kAsCopies > 8u && wave == 0u) scale_copy(8u);
+    if (wave == 0u) {
+      const float* wse = w13s + (size_t)e * (2u * I / 128u) * KB;
+      const uint32_t wsoff = lane < 2u * KB ? ((lane < KB ? ng : I / 128u + ng) * KB + lane % KB) * 4u : kFar;
+      copy4((uint32_t)__builtin_amdgcn_readfirstlane((int)lds_offset(&s_wsv[0])),
+            rsrc(wse, (2u * I / 128u) * KB * 4u), wsoff, 0u);
+    }
   }
-  issue(0);
-  if (KB > 1) issue(1);
   const uint32_t g = lane >> 4;
   float wsv = 0.0f;
   v4f acc[4][4];
@@ -253,22 +285,32 @@ __device__ __forceinline__ void gate_up_lds(
   for (uint32_t i = 0; i < 4; ++i)
 #pragma unroll
     for (uint32_t c = 0; c < 4; ++c) acc[i][c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  auto kloop = [&](auto ntc) __attribute__((always_inline)) {
+  // the tail tile against this wave's gate and up tiles 2 n + m (16 h columns)
+  v4f acc_t[2] = {v4f{0.0f, 0.0f, 0.0f, 0.0f}, v4f{0.0f, 0.0f, 0.0f, 0.0f}};
+  auto kloop = [&](auto ntc, auto tailc) __attribute__((always_inline)) {
     constexpr uint32_t NT = decltype(ntc)::value;
+    constexpr bool kTail = decltype(tailc)::value;
+    // copies per step: the tail share only in the tail variant
+    constexpr uint32_t kCopies = kTail ? kCopiesPerWave : kCopiesPerWave - 1u;
+#pragma unroll
+    for (uint32_t q = 0; q < kCopies; ++q) issue_part(0, q);
+    if (KB > 1)
+#pragma unroll
+      for (uint32_t q = 0; q < kCopies; ++q) issue_part(1, q);
 #pragma unroll
     for (uint32_t kb = 0; kb < KB; ++kb) {
-      if (kb + 1u < KB) wait_copies<kCopiesPerWave>(); else wait_copies<0>();
+      if (kb + 1u < KB) wait_copies<kCopies>(); else wait_copies<0>();
       barrier();
-      // the next-but-one step's copies: two before each of the first NT - 1
-      // row tiles, the rest before the last
-      constexpr uint32_t kPer = NT > 1 ? 2u : kCopiesPerWave;
+      // the next-but-one step's copies: two before each of the first row
+      // tiles, the rest before the last
+      constexpr uint32_t kPer = NT > 1 ? 2u : kCopies;
       uint32_t q = 0;
       auto some_copies = [&](uint32_t count) __attribute__((always_inline)) {
 #pragma unroll
-        for (uint32_t u = 0; u < kCopiesPerWave; ++u)
-          if (u < count && q < kCopiesPerWave && kb + 2u < KB) { issue_part(kb + 2u, q); ++q; }
+        for (uint32_t u = 0; u < kCopies; ++u)
+          if (u < count && q < kCopies && kb + 2u < KB) { issue_part(kb + 2u, q); ++q; }
       };
-      if (kb == 0) wsv = s_wsv[wave][lane];  // this wave's scale copy landed with step 0's
+      if (kb == 0) wsv = s_wsv[lane];  // the scale copy landed with step 0's copies
       if (NT > 0) {
         const uint8_t* st = s_stage[kb % kStages];
         v8i bw[4];
@@ -284,7 +326,7 @@ __device__ __forceinline__ void gate_up_lds(
           const uint32_t r0 = rt * 16u + g * 4u;  // rows r0 .. r0 + 3 share as_swizzle
           const float* asr = &s_as[r0 * KB + (((kb >> 2) ^ as_swizzle(r0)) << 2) + (kb & 3u)];
           const float4 as4 = make_float4(asr[0], asr[KB], asr[2u * KB], asr[3u * KB]);
-          some_copies(i + 1u < NT ? kPer : kCopiesPerWave);
+          some_copies(i + 1u < NT ? kPer : kCopies);
           v4f d[4];
 #pragma unroll
           for (uint32_t c = 0; c < 4; ++c) d[c] = nk::mfma_e4m3_16x16x128(af, bw[c]);
@@ -294,20 +336,45 @@ __device__ __forceinline__ void gate_up_lds(
 #pragma unroll
             for (uint32_t j = 0; j < 4; ++j) acc[i][c][j] = fmaf((c < 2 ? sg : su) * as[j], d[c][j], acc[i][c][j]);
         }
+        // The tail tile: a variant of its own (a branch inside the unrolled
+        // loop costs it its registers); an absorbing item's blocks are full.
+        if constexpr (kTail) {
+          const v8i af = lds_operand_rows(st + kTailTile * 2048u, lane);
+          const uint32_t r0 = kTailTile * 16u + g * 4u;
+          const float* asr = &s_as[r0 * KB + (((kb >> 2) ^ as_swizzle(r0)) << 2) + (kb & 3u)];
+          const float as[4] = {asr[0], asr[KB], asr[2u * KB], asr[3u * KB]};
+          const v4f dg = nk::mfma_e4m3_16x16x128(af, m == 0u ? bw[0] : bw[1]);
+          const v4f du = nk::mfma_e4m3_16x16x128(af, m == 0u ? bw[2] : bw[3]);
+#pragma unroll
+          for (uint32_t j = 0; j < 4; ++j) {
+            acc_t[0][j] = fmaf(sg * as[j], dg[j], acc_t[0][j]);
+            acc_t[1][j] = fmaf(su * as[j], du[j], acc_t[1][j]);
+          }
+        }
       } else {
-        some_copies(kCopiesPerWave);
+        some_copies(kCopies);
       }
     }
   };
-  switch (ntiles) {
-    case 0: kloop(std::integral_constant<uint32_t, 0>{}); break;
-    case 1: kloop(std::integral_constant<uint32_t, 1>{}); break;
-    case 2: kloop(std::integral_constant<uint32_t, 2>{}); break;
-    case 3: kloop(std::integral_constant<uint32_t, 3>{}); break;
-    default: kloop(std::integral_constant<uint32_t, 4>{}); break;
+  using no_tail = std::false_type;
+  if (absorb) {
+    kloop(std::integral_constant<uint32_t, 4>{}, std::true_type{});
+  } else {
+    switch (ntiles) {
+      case 0: kloop(std::integral_constant<uint32_t, 0>{}, no_tail{}); break;
+      case 1: kloop(std::integral_constant<uint32_t, 1>{}, no_tail{}); break;
+      case 2: kloop(std::integral_constant<uint32_t, 2>{}, no_tail{}); break;
+      case 3: kloop(std::integral_constant<uint32_t, 3>{}, no_tail{}); break;
+      default: kloop(std::integral_constant<uint32_t, 4>{}, no_tail{}); break;
+    }
   }
-  // Epilogue: h = bf16(silu(g) * u); amax per row over the 128-column group;
-  // FP8 bytes through LDS (stage 0, free once every wave is past the K loop).
+  // Epilogue: h = bf16(silu(g) * u); amax per row over the 128-column group
+  // (in stage KB % 3, which no wave reads after the K loop); FP8 bytes
+  // through LDS (stage 0, free once every wave is past the K loop). The tail
+  // rows' amax comes from all eight waves (16 columns each).
+  float* s_amax = reinterpret_cast<float*>(s_stage[KB % kStages]);  // [2][4][64]: row block, quarter, row
+  float* s_amax_t = s_amax + 2u * 4u * kRowsPerBlock;                // [8][16]: wave, tail row
+  float* s_scale = s_amax_t + 8u * 16u;                              // [kAllRows]
   float h[4][2][4];
 #pragma unroll
   for (uint32_t i = 0; i < 4; ++i) {
@@ -324,17 +391,36 @@ __device__ __forceinline__ void gate_up_lds(
       mx = fmaxf(mx, __shfl_xor(mx, 2u));
       mx = fmaxf(mx, __shfl_xor(mx, 4u));
       mx = fmaxf(mx, __shfl_xor(mx, 8u));
-      if ((lane & 15u) == 0) s_amax[m][n][i * 16u + g * 4u + j] = mx;
+      if ((lane & 15u) == 0) s_amax[(m * 4u + n) * kRowsPerBlock + i * 16u + g * 4u + j] = mx;
+    }
+  }
+  float ht[4];
+  if (absorb) {
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+      ht[j] = nk::bf16_round_hw(nk::silu_hw(acc_t[0][j]) * acc_t[1][j]);
+      float mx = fabsf(ht[j]);
+      mx = fmaxf(mx, __shfl_xor(mx, 1u));
+      mx = fmaxf(mx, __shfl_xor(mx, 2u));
+      mx = fmaxf(mx, __shfl_xor(mx, 4u));
+      mx = fmaxf(mx, __shfl_xor(mx, 8u));
+      if ((lane & 15u) == 0) s_amax_t[wave * 16u + g * 4u + j] = mx;
     }
   }
   __syncthreads();
-  if (tid < kRows) {
-    const uint32_t mb = tid >> 6, r = tid & 63u;
+  if (tid < kAllRows) {
+    const uint32_t r = tid & 63u;
     float mx = nk::kAmaxFloor;
+    if (tid < kRows) {
 #pragma unroll
-    for (uint32_t q = 0; q < 4; ++q) mx = fmaxf(mx, s_amax[mb][q][r]);
+      for (uint32_t q = 0; q < 4; ++q) mx = fmaxf(mx, s_amax[((tid >> 6) * 4u + q) * kRowsPerBlock + r]);
+    } else {
+#pragma unroll
+      for (uint32_t w = 0; w < 8; ++w) mx = fmaxf(mx, s_amax_t[w * 16u + r]);
+    }
     const float scale = mx * nk::inv_e4m3_max();
     s_scale[tid] = scale;
+    // rows 128 .. 143 are rows 0 .. 15 of block b0 + 2: the sorted rows are contiguous
     if (s_tok[tid] >= 0) hs[(size_t)(b0 * kRowsPerBlock + tid) * (I / 128u) + ng] = scale;
   }
   __syncthreads();
@@ -352,9 +438,18 @@ __device__ __forceinline__ void gate_up_lds(
       s_out[row * kOut + ocol + 16u] = (uint8_t)(q2 >> 8);
     }
   }
+  if (absorb) {
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+      const uint32_t row = kRows + g * 4u + j;
+      const uint32_t q1 = nk::e4m3x4(ht[j] * (1.0f / s_scale[row]), 0.0f, 0.0f, 0.0f);
+      s_out[row * kOut + (2u * n + m) * 16u + (lane & 15u)] = (uint8_t)q1;
+    }
+  }
   __syncthreads();
-  {  // 128 rows x 128 bytes: 4 threads per row, two 16-byte pieces each
-    const uint32_t row = tid >> 2, c0 = (tid & 3u) * 32u;
+  // 144 rows x 128 bytes: 4 threads per row, two 16-byte pieces each
+  for (uint32_t row = tid >> 2; row < kAllRows; row += kThreads / 4u) {
+    const uint32_t c0 = (tid & 3u) * 32u;
     if (s_tok[row] >= 0) {
       uint8_t* dst = hq + (size_t)(b0 * kRowsPerBlock + row) * I + ng * 128u + c0;
       *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(&s_out[row * kOut + c0]);

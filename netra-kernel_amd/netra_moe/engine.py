@@ -121,6 +121,15 @@ def resolve_path(cfg: MoEConfig, path: str = "auto") -> str:
     return path
 
 
+def gate_up_lds_bytes(H: int) -> int:
+    """Static LDS of netra_moe_gate_up_lds_h<H>: three stages of (9 row tiles +
+    16 weight tiles) x 2 KiB, the activation scales of 144 rows in 1 KiB
+    copies of 256 / (H / 128) rows each, the weight block scales, the row tokens."""
+    kb = H // 128
+    rows_per_copy = 256 // kb
+    return 3 * 25 * 2048 + (144 + rows_per_copy - 1) // rows_per_copy * 1024 + 64 * 4 + 145 * 4
+
+
 def xcd_grid(items: int) -> int:
     """Workgroups for an XCD-major item assignment (nktile::xcd_item): a
     multiple of 8 covering every item."""
@@ -530,7 +539,7 @@ def operations(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> list[
             gate_up = dict(
                 name="moe.gate_up", symbol=f"netra_moe_gate_up_lds_h{H}_gfx950",
                 grid=(xcd_grid(cfg.cap_blocks * (I // 128)), 1, 1), block=(512, 1, 1),
-                lds=3 * 48 * 1024 + 8 * 256 * 4 + 8 * 64 * 4 + 128 * 4 + 2 * 4 * 64 * 4 + 128 * 4, dyn=0,
+                lds=gate_up_lds_bytes(H), dyn=0,
                 args=["x_q", "x_scale", "w13", "w13_scale", *common, "pair_map", "h_q", "h_scale",
                       u(T), u(H), u(I), u(cfg.Ktot), u(cfg.Etot)],
                 reads=["x_q", "x_scale", "w13", "w13_scale", *common, "pair_map"], writes=["h_q", "h_scale"],

@@ -9,7 +9,7 @@ cannot see around inline assembly:
   assembly. A missed case reads a stale resource descriptor or offset, which
   can address memory outside every buffer.
 * the LDS-ring gate/up kernels wait for "this step's copies landed" with
-  s_waitcnt vmcnt(6): correct only while the six buffer-to-LDS copies a wave
+  s_waitcnt vmcnt(7): correct only while the seven buffer-to-LDS copies a wave
   issues per 128-K step are the only vector-memory operations in flight in
   the K loop. If the compiler ever turned the per-step weight-scale loads
   (uniform addresses, scalar loads today) into vector loads, the count would
@@ -129,8 +129,8 @@ def test_no_valu_sgpr_to_vmem_hazard_in_any_kernel():
 # vmcnt waits an LDS-ring kernel family may use inside its ring: 0 or the
 # copies of one step (kCopiesPerWave in moe_gemm_lds.hip, kCopies in
 # route_screen)
-RING_WAITS = {"netra_moe_gate_up_lds_": {0, 6}, "netra_moe_route_screen_": {0, 16}}
-KCOPIES = 6
+RING_WAITS = {"netra_moe_gate_up_lds_": {0, 6, 7}, "netra_moe_route_screen_": {0, 16}}
+KCOPIES = 7
 _VMCNT = re.compile(r"vmcnt\((\d+)\)")
 _VSTORE = re.compile(r"(global|buffer|flat)_store")
 
@@ -185,7 +185,7 @@ def ring_violations(lines: list[str], waits: set[int] | None = None) -> list[str
 
 
 def test_ring_checker_flags_a_foreign_load():
-    ring = ["buffer_load_dwordx4 v1, s[4:7], s1 offen lds", "s_waitcnt vmcnt(6)",
+    ring = ["buffer_load_dwordx4 v1, s[4:7], s1 offen lds", "s_waitcnt vmcnt(7)",
             "buffer_load_dwordx4 v2, s[4:7], s1 offen lds", "s_waitcnt vmcnt(0)",
             "global_store_dword v[0:1], v3, off"]
     assert ring_violations(ring) == []
@@ -193,10 +193,10 @@ def test_ring_checker_flags_a_foreign_load():
     assert any("inside the copy ring" in v for v in ring_violations(foreign))
     early = ring[:3] + ["global_load_dword v4, v[0:1], off"]
     assert any("before the ring drains" in v for v in ring_violations(early))
-    overlap = ring[:3] + ["global_store_dword v[0:1], v3, off", "s_waitcnt vmcnt(6)"]
+    overlap = ring[:3] + ["global_store_dword v[0:1], v3, off", "s_waitcnt vmcnt(7)"]
     assert any("behind a store" in v for v in ring_violations(overlap))
     assert ring_violations(ring[:1] + ["s_waitcnt vmcnt(5)"] + ring[2:])
-    stored = ring[:2] + ["global_store_dwordx4 v[0:1], v[4:7], off", "s_waitcnt vmcnt(6)"] + ring[2:]
+    stored = ring[:2] + ["global_store_dwordx4 v[0:1], v[4:7], off", "s_waitcnt vmcnt(7)"] + ring[2:]
     assert any("behind a store" in v for v in ring_violations(stored))
     drained = ring[:2] + ["global_store_dwordx4 v[0:1], v[4:7], off", "s_waitcnt vmcnt(0)"] + ring[2:]
     assert ring_violations(drained) == []

@@ -168,6 +168,10 @@ __device__ __forceinline__ void gate_up_lds(
   auto as_swizzle = [](uint32_t r) { return (r >> 2) & (kAsLanesPerRow - 1u); };
   __shared__ __align__(16) uint8_t s_stage[kStages][kStageBytes];
   __shared__ __align__(16) float s_as[kAsCopies * 256u];  // a_s(row, kb) at row * KB + kb (swizzled chunks)
+  // a_s(row, kb): 16 consecutive rows of one kb fall in 16 distinct banks
+  auto s_as_at = [&](uint32_t r, uint32_t kb) __attribute__((always_inline)) {
+    return s_as[r * KB + (((kb >> 2) ^ as_swizzle(r)) << 2) + (kb & 3u)];
+  };
   __shared__ __align__(16) float s_wsv[64];               // weight block scales: lane kb gate, KB + kb up
   __shared__ int32_t s_tok[kAllRows + 1u];
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
@@ -278,7 +282,6 @@ __device__ __forceinline__ void gate_up_lds(
             rsrc(wse, (2u * I / 128u) * KB * 4u), wsoff, 0u);
     }
   }
-  const uint32_t g = lane >> 4;
   float wsv = 0.0f;
   v4f acc[4][4];
 #pragma unroll
@@ -323,32 +326,29 @@ __device__ __forceinline__ void gate_up_lds(
         for (uint32_t i = 0; i < NT; ++i) {
           const uint32_t rt = 4u * m + i;
           const v8i af = lds_operand_rows(st + rt * 2048u, lane);
-          const uint32_t r0 = rt * 16u + g * 4u;  // rows r0 .. r0 + 3 share as_swizzle
-          const float* asr = &s_as[r0 * KB + (((kb >> 2) ^ as_swizzle(r0)) << 2) + (kb & 3u)];
-          const float4 as4 = make_float4(asr[0], asr[KB], asr[2u * KB], asr[3u * KB]);
+          const float as = s_as_at(rt * 16u + (lane & 15u), kb);  // this lane's token row
+          const float sgi = sg * as, sui = su * as;
           some_copies(i + 1u < NT ? kPer : kCopies);
           v4f d[4];
 #pragma unroll
-          for (uint32_t c = 0; c < 4; ++c) d[c] = nk::mfma_e4m3_16x16x128(af, bw[c]);
-          const float as[4] = {as4.x, as4.y, as4.z, as4.w};
+          for (uint32_t c = 0; c < 4; ++c) d[c] = nk::mfma_e4m3_16x16x128(bw[c], af);
 #pragma unroll
           for (uint32_t c = 0; c < 4; ++c)
 #pragma unroll
-            for (uint32_t j = 0; j < 4; ++j) acc[i][c][j] = fmaf((c < 2 ? sg : su) * as[j], d[c][j], acc[i][c][j]);
+            for (uint32_t j = 0; j < 4; ++j) acc[i][c][j] = fmaf(c < 2 ? sgi : sui, d[c][j], acc[i][c][j]);
         }
         // The tail tile: a variant of its own (a branch inside the unrolled
         // loop costs it its registers); an absorbing item's blocks are full.
         if constexpr (kTail) {
           const v8i af = lds_operand_rows(st + kTailTile * 2048u, lane);
-          const uint32_t r0 = kTailTile * 16u + g * 4u;
-          const float* asr = &s_as[r0 * KB + (((kb >> 2) ^ as_swizzle(r0)) << 2) + (kb & 3u)];
-          const float as[4] = {asr[0], asr[KB], asr[2u * KB], asr[3u * KB]};
-          const v4f dg = nk::mfma_e4m3_16x16x128(af, m == 0u ? bw[0] : bw[1]);
-          const v4f du = nk::mfma_e4m3_16x16x128(af, m == 0u ? bw[2] : bw[3]);
+          const float as = s_as_at(kTailTile * 16u + (lane & 15u), kb);
+          const float sgi = sg * as, sui = su * as;
+          const v4f dg = nk::mfma_e4m3_16x16x128(m == 0u ? bw[0] : bw[1], af);
+          const v4f du = nk::mfma_e4m3_16x16x128(m == 0u ? bw[2] : bw[3], af);
 #pragma unroll
           for (uint32_t j = 0; j < 4; ++j) {
-            acc_t[0][j] = fmaf(sg * as[j], dg[j], acc_t[0][j]);
-            acc_t[1][j] = fmaf(su * as[j], du[j], acc_t[1][j]);
+            acc_t[0][j] = fmaf(sgi, dg[j], acc_t[0][j]);
+            acc_t[1][j] = fmaf(sui, du[j], acc_t[1][j]);
           }
         }
       } else {
@@ -375,37 +375,36 @@ __device__ __forceinline__ void gate_up_lds(
   float* s_amax = reinterpret_cast<float*>(s_stage[KB % kStages]);  // [2][4][64]: row block, quarter, row
   float* s_amax_t = s_amax + 2u * 4u * kRowsPerBlock;                // [8][16]: wave, tail row
   float* s_scale = s_amax_t + 8u * 16u;                              // [kAllRows]
+  // The MFMAs take the weight tile as A: lane l holds channels 4 (l >> 4) ..
+  // + 3 of each 16-row weight tile for token row l & 15 of each row tile, so
+  // a lane's four h values of a tile are consecutive columns of one row.
   float h[4][2][4];
 #pragma unroll
   for (uint32_t i = 0; i < 4; ++i) {
+    float mx = 0.0f;
 #pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) {
-      float mx = 0.0f;
+    for (uint32_t c = 0; c < 2; ++c)
 #pragma unroll
-      for (uint32_t c = 0; c < 2; ++c) {
+      for (uint32_t j = 0; j < 4; ++j) {
         const float v = nk::bf16_round_hw(nk::silu_hw(acc[i][c][j]) * acc[i][2u + c][j]);
         h[i][c][j] = v;
         mx = fmaxf(mx, fabsf(v));
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 1u));
-      mx = fmaxf(mx, __shfl_xor(mx, 2u));
-      mx = fmaxf(mx, __shfl_xor(mx, 4u));
-      mx = fmaxf(mx, __shfl_xor(mx, 8u));
-      if ((lane & 15u) == 0) s_amax[(m * 4u + n) * kRowsPerBlock + i * 16u + g * 4u + j] = mx;
-    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16u));
+    mx = fmaxf(mx, __shfl_xor(mx, 32u));
+    if (lane < 16u) s_amax[(m * 4u + n) * kRowsPerBlock + i * 16u + lane] = mx;
   }
   float ht[4];
   if (absorb) {
+    float mx = 0.0f;
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j) {
       ht[j] = nk::bf16_round_hw(nk::silu_hw(acc_t[0][j]) * acc_t[1][j]);
-      float mx = fabsf(ht[j]);
-      mx = fmaxf(mx, __shfl_xor(mx, 1u));
-      mx = fmaxf(mx, __shfl_xor(mx, 2u));
-      mx = fmaxf(mx, __shfl_xor(mx, 4u));
-      mx = fmaxf(mx, __shfl_xor(mx, 8u));
-      if ((lane & 15u) == 0) s_amax_t[wave * 16u + g * 4u + j] = mx;
+      mx = fmaxf(mx, fabsf(ht[j]));
     }
+    mx = fmaxf(mx, __shfl_xor(mx, 16u));
+    mx = fmaxf(mx, __shfl_xor(mx, 32u));
+    if (lane < 16u) s_amax_t[wave * 16u + lane] = mx;
   }
   __syncthreads();
   if (tid < kAllRows) {
@@ -426,25 +425,21 @@ __device__ __forceinline__ void gate_up_lds(
   __syncthreads();
   constexpr uint32_t kOut = 144;  // LDS bytes per output row (128 + 16)
   uint8_t* s_out = s_stage[0];
-  const uint32_t ocol = n * 32u + (lane & 15u);
+  const uint32_t ocol = 4u * (lane >> 4);  // this lane's four columns within a 16-column tile
 #pragma unroll
   for (uint32_t i = 0; i < 4; ++i) {
+    const uint32_t row = m * kRowsPerBlock + i * 16u + (lane & 15u);
+    const float inv = 1.0f / s_scale[row];
 #pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) {
-      const uint32_t row = m * kRowsPerBlock + i * 16u + g * 4u + j;
-      const float inv = 1.0f / s_scale[row];
-      const uint32_t q2 = nk::e4m3x4(h[i][0][j] * inv, h[i][1][j] * inv, 0.0f, 0.0f);
-      s_out[row * kOut + ocol] = (uint8_t)q2;
-      s_out[row * kOut + ocol + 16u] = (uint8_t)(q2 >> 8);
-    }
+    for (uint32_t c = 0; c < 2; ++c)
+      *reinterpret_cast<uint32_t*>(&s_out[row * kOut + (2u * n + c) * 16u + ocol]) =
+          nk::e4m3x4(h[i][c][0] * inv, h[i][c][1] * inv, h[i][c][2] * inv, h[i][c][3] * inv);
   }
   if (absorb) {
-#pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) {
-      const uint32_t row = kRows + g * 4u + j;
-      const uint32_t q1 = nk::e4m3x4(ht[j] * (1.0f / s_scale[row]), 0.0f, 0.0f, 0.0f);
-      s_out[row * kOut + (2u * n + m) * 16u + (lane & 15u)] = (uint8_t)q1;
-    }
+    const uint32_t row = kRows + (lane & 15u);
+    const float inv = 1.0f / s_scale[row];
+    *reinterpret_cast<uint32_t*>(&s_out[row * kOut + (2u * n + m) * 16u + ocol]) =
+        nk::e4m3x4(ht[0] * inv, ht[1] * inv, ht[2] * inv, ht[3] * inv);
   }
   __syncthreads();
   // 144 rows x 128 bytes: 4 threads per row, two 16-byte pieces each

@@ -491,8 +491,7 @@ __device__ __forceinline__ void down_rows(
     soff[p] = live[p] ? ((uint32_t)route * H + c16 * 8u) * 2u : 0x80000000u;
   }
   auto pack2 = [&](float lo, float hi) __attribute__((always_inline)) {
-    return kSplitF16 ? ((uint32_t)f16_bits(lo) | ((uint32_t)f16_bits(hi) << 16))
-                     : ((uint32_t)nk::bf16_rne(lo) | ((uint32_t)nk::bf16_rne(hi) << 16));
+    return kSplitF16 ? ((uint32_t)f16_bits(lo) | ((uint32_t)f16_bits(hi) << 16)) : nk::bf16x2_hw(lo, hi);
   };
   // One output group through the LDS transpose: buffer v & 1, one barrier (the
   // other buffer was read before the previous barrier); `extra` moves live

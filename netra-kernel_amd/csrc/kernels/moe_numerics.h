@@ -101,6 +101,13 @@ __device__ __forceinline__ float silu_hw(float g) {
   return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
 }
 __device__ __forceinline__ float bf16_round_hw(float x) { return (float)(__bf16)x; }
+// Two floats to packed bf16 (low half first) by one v_cvt_pk_bf16_f32: the
+// bits of bf16_rne for every non-NaN input, without its NaN branch.
+__device__ __forceinline__ uint32_t bf16x2_hw(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
 __device__ __forceinline__ float sigmoid(float z) { return 1.0f / (1.0f + nexp(-z)); }
 
 // 32 contiguous FP8 bytes as one MFMA operand (two 16-byte loads).

@@ -247,12 +247,12 @@ __device__ __forceinline__ void route_select(
     uint32_t S, uint32_t RP, uint32_t Z) {
   constexpr uint32_t H = 128u * NJ;
   constexpr uint32_t P = EMAX / 64u;  // experts per lane
-  static_assert(EMAX % 64u == 0 && P <= 8u, "shape");
+  static_assert(EMAX % 64u == 0 && P <= 8u && W <= 32u, "shape");
   __shared__ float4 s_x[W][32u * NJ];        // the tokens' rows, widened to fp32
   __shared__ __align__(16) uint16_t s_cand[W][EMAX];  // also the selected slots (K * 8 <= 2 * EMAX bytes)
   __shared__ uint16_t s_exact[W][EMAX + 1];  // exact logit bits, candidate order; shared row last
   __shared__ int32_t s_ids[W][kMaxSlots];
-  __shared__ uint32_t s_hist[EMAX + 1];
+  __shared__ uint32_t s_hist[EMAX + 1];  // bit u: token u of the workgroup routes to the expert
   __shared__ float s_wn[EMAX];  // router-row norms, ||w_e|| (1 + 2^-9), from the screen's Z partial sums
   const uint32_t rows = E + S, Ktot = K + S;
   if (E > EMAX || K == 0 || K > E || Ktot > kMaxSlots || S > 1u) return;  // uniform
@@ -342,8 +342,8 @@ __device__ __forceinline__ void route_select(
       clo[j] = chi[j] = 0u;
       if (e < E) {
         const float a = aval[j], m = mx * s_wn[e], b = bv[j];
-        clo[j] = nk::order_bits(nk::bf16_f32(nk::bf16_rne(a - m)) + b);
-        chi[j] = nk::order_bits(nk::bf16_f32(nk::bf16_rne(a + m)) + b);
+        clo[j] = nk::order_bits(nk::bf16_round_hw(a - m) + b);  // bf16 RNE (hardware; a is finite)
+        chi[j] = nk::order_bits(nk::bf16_round_hw(a + m) + b);
       }
     }
     // theta <= the K-th largest zlo: the largest code with its low 16 bits
@@ -477,7 +477,7 @@ __device__ __forceinline__ void route_select(
     }
     if (lane < Ktot) {
       s_ids[tt][lane] = (int32_t)my_id;
-      atomicAdd(&s_hist[my_id], 1u);
+      atomicOr(&s_hist[my_id], 1u << tt);
     }
 
     // 4. logits row
@@ -491,18 +491,18 @@ __device__ __forceinline__ void route_select(
   }
   __syncthreads();
 
-  // 5. in-workgroup ranks and histogram
+  // 5. in-workgroup ranks and histogram from the per-expert token masks (a
+  // token routes to an expert at most once): the rank of token tk's route to
+  // e is the number of earlier tokens in e's mask
   const uint32_t t0 = blockIdx.x * W;
   for (uint32_t r = tid; r < W * Ktot; r += kThreads) {
     const uint32_t tk = r / Ktot, sl = r - tk * Ktot;
     if (t0 + tk >= T) break;
-    const int32_t e = s_ids[tk][sl];
-    uint32_t rank = 0u;
-    for (uint32_t u = 0; u < tk; ++u)
-      for (uint32_t v = 0; v < Ktot; ++v) rank += s_ids[u][v] == e ? 1u : 0u;
-    lrank[(size_t)(t0 + tk) * Ktot + sl] = (int32_t)rank;
+    const uint32_t bits = s_hist[s_ids[tk][sl]];
+    lrank[(size_t)(t0 + tk) * Ktot + sl] = __popc(bits & ((1u << tk) - 1u));
   }
-  for (uint32_t e = tid; e < rows; e += kThreads) hist[(size_t)e * gridDim.x + blockIdx.x] = (int32_t)s_hist[e];
+  for (uint32_t e = tid; e < rows; e += kThreads)
+    hist[(size_t)e * gridDim.x + blockIdx.x] = __popc(s_hist[e]);
 }
 
 }  // namespace nkroute

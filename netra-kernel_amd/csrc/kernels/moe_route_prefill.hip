@@ -108,14 +108,16 @@ __device__ __forceinline__ float exact_dot(const float4* __restrict__ xrow, cons
 // ---------------------------------------------------------------------------
 // route_screen: workgroup (tm, tn, z), 256 threads (4 waves): tokens
 // 128 tm .. +127 x rows 128 tn .. +127 over K blocks [z KBS, (z + 1) KBS)
-// (split K, so that a few hundred workgroups cover the token count). Per
-// 128-K block both 128 x 128 bf16 tiles (32 KiB each) are copied global ->
-// LDS by buffer loads with the LDS-destination bit into a two-stage ring, the
-// next block's copies in flight during this block's multiplies. A tile is
-// row-major, 256 bytes a row, with the 16-byte chunk c of row r at position
-// c ^ (r & 15): one wave copy moves four whole rows (lane l: row l >> 4,
-// position l & 15), and an operand read (one chunk of 16 rows per 16 lanes)
-// hits 16 distinct positions. Wave w multiplies rows 64 (w & 1) .. +63 by
+// (split K, so that a few hundred workgroups cover the token count). The K
+// range is walked in 64-element half blocks: both 128 x 64 bf16 tiles (16 KiB
+// each) of a half block are copied global -> LDS by buffer loads with the
+// LDS-destination bit into a ring of four stages, three half blocks ahead of
+// the multiplies (one workgroup per CU: its copies in flight are what hides
+// the memory latency). A tile is row-major, 128 bytes a row, with the 16-byte
+// chunk c of row r at position c ^ ((r >> 1) & 7): one wave copy moves eight
+// whole rows (lane l: row l >> 3, position l & 7), and an operand read (one
+// chunk of 16 rows per 16 lanes) hits 16 distinct (row parity, position)
+// pairs, i.e. all 64 banks. Wave w multiplies rows 64 (w & 1) .. +63 by
 // tokens 64 (w >> 1) .. +63 with v_mfma_f32_16x16x32_bf16, the router rows as
 // the A operand, so a lane's four results are four consecutive rows of one
 // token: one 16-byte store. Each tile element is read from LDS by two waves
@@ -132,35 +134,41 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
                                              float* __restrict__ screen, float* __restrict__ wsq,
                                              uint32_t T, uint32_t rows, uint32_t RP) {
   constexpr uint32_t H = 128u * NJ;
-  constexpr uint32_t kTile = 128u * 256u;  // bytes of one 128 x 128 bf16 tile
-  constexpr uint32_t kCopies = 16u;        // copies per wave per K block: 8 of x rows, 8 of router rows
+  constexpr uint32_t kTile = 128u * 128u;  // bytes of one 128 x 64 bf16 tile
+  constexpr uint32_t kStages = 4u;
+  constexpr uint32_t kAhead = kStages - 1u;  // half blocks in flight ahead of the one multiplied
+  constexpr uint32_t kCopies = 8u;           // copies per wave per half block: 4 of x rows, 4 of router rows
+  constexpr uint32_t NS = 2u * KBS;          // half blocks of the split
   static_assert(KBS <= NJ && NJ % KBS == 0, "splits cover K");
-  __shared__ __align__(16) uint8_t s_tile[2][2][kTile];  // [stage][x, w]
+  __shared__ __align__(16) uint8_t s_tile[kStages][2][kTile];  // [stage][x, w]
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
   const bool norms = blockIdx.x == 0;  // uniform
   const uint32_t t0 = blockIdx.x * 128u, r0 = blockIdx.y * 128u, z = blockIdx.z, kb0 = z * KBS;
-  // copy c of this wave moves tile rows 32 wave + 4 c .. + 3; lane l fetches
-  // the chunk that position l & 15 of row 32 wave + 4 c + (l >> 4) holds
+  auto swz = [](uint32_t r) { return (r >> 1) & 7u; };
+  // copy c of this wave moves tile rows 32 wave + 8 c .. + 7; lane l fetches
+  // the chunk that position l & 7 of row 32 wave + 8 c + (l >> 3) holds
   const nk::u32x4 rx = nklds::rsrc(x, T * H * 2u), rw = nklds::rsrc(w, rows * H * 2u);
-  uint32_t xoff[8], woff[8];
+  uint32_t xoff[4], woff[4];
 #pragma unroll
-  for (uint32_t c = 0; c < 8u; ++c) {
-    const uint32_t row = 32u * wave + 4u * c + (lane >> 4), chunk = (lane & 15u) ^ (row & 15u);
+  for (uint32_t c = 0; c < 4u; ++c) {
+    const uint32_t row = 32u * wave + 8u * c + (lane >> 3), chunk = (lane & 7u) ^ swz(row);
     const uint32_t t = t0 + row, r = r0 + row;
     xoff[c] = t < T ? t * H * 2u + chunk * 16u : nklds::kFar;
     woff[c] = r < rows ? r * H * 2u + chunk * 16u : nklds::kFar;
   }
   const uint32_t lds0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)nklds::lds_offset(&s_tile[0][0][0]));
-  auto issue = [&](uint32_t kb) __attribute__((always_inline)) {
-    const uint32_t st = lds0 + (kb & 1u) * 2u * kTile + (32u * wave) * 256u;
+  auto issue = [&](uint32_t hs) __attribute__((always_inline)) {  // half block hs of the split
+    const uint32_t st = lds0 + (hs % kStages) * 2u * kTile + (32u * wave) * 128u;
+    const uint32_t koff = kb0 * 256u + hs * 128u;  // bytes into each row
 #pragma unroll
-    for (uint32_t c = 0; c < 8u; ++c) nklds::copy16(st + 4u * c * 256u, rx, xoff[c], (kb0 + kb) * 256u);
+    for (uint32_t c = 0; c < 4u; ++c) nklds::copy16(st + 8u * c * 128u, rx, xoff[c], koff);
 #pragma unroll
-    for (uint32_t c = 0; c < 8u; ++c) nklds::copy16(st + kTile + 4u * c * 256u, rw, woff[c], (kb0 + kb) * 256u);
+    for (uint32_t c = 0; c < 4u; ++c) nklds::copy16(st + kTile + 8u * c * 128u, rw, woff[c], koff);
   };
-  issue(0);
-  if (KBS > 1) issue(1);
+#pragma unroll
+  for (uint32_t hs = 0; hs < kAhead; ++hs)
+    if (hs < NS) issue(hs);
   nk::v4f acc[4][4];
 #pragma unroll
   for (uint32_t i = 0; i < 4; ++i)
@@ -170,19 +178,28 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
   const uint32_t mrow = 64u * (wave & 1u), ntok = 64u * (wave >> 1);
   float nsum = 0.0f;
 #pragma unroll
-  for (uint32_t kb = 0; kb < KBS; ++kb) {
-    if (kb + 1u < KBS) nklds::wait_copies<kCopies>(); else nklds::wait_copies<0>();
-    nklds::barrier();  // every wave's copies of block kb have landed
-    const uint8_t* sx = s_tile[kb & 1u][0];
-    const uint8_t* sw = s_tile[kb & 1u][1];
+  for (uint32_t hs = 0; hs < NS; ++hs) {
+    // copies issued after half block hs's: those of the next ones up to kAhead - 1
+    if (hs + 2u < NS) nklds::wait_copies<2u * kCopies>();
+    else if (hs + 1u < NS) nklds::wait_copies<kCopies>();
+    else nklds::wait_copies<0>();
+    nklds::barrier();  // every wave's copies of half block hs have landed, and every wave is past hs - 1
+    if (hs + kAhead < NS) issue(hs + kAhead);  // into the stage half block hs - 1 used
+    const uint8_t* sx = s_tile[hs % kStages][0];
+    const uint8_t* sw = s_tile[hs % kStages][1];
 #pragma unroll
-    for (uint32_t q = 0; q < 4; ++q) {
-      const uint32_t pos = ((4u * q + g) ^ rl) * 16u;  // the chunk of elements 32 q + 8 g ..
+    for (uint32_t q = 0; q < 2; ++q) {
       uint4 a[4], b[4];
 #pragma unroll
-      for (uint32_t i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const uint4*>(sw + (mrow + 16u * i + rl) * 256u + pos);
+      for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t r = mrow + 16u * i + rl;
+        a[i] = *reinterpret_cast<const uint4*>(sw + r * 128u + ((4u * q + g) ^ swz(r)) * 16u);
+      }
 #pragma unroll
-      for (uint32_t j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const uint4*>(sx + (ntok + 16u * j + rl) * 256u + pos);
+      for (uint32_t j = 0; j < 4; ++j) {
+        const uint32_t r = ntok + 16u * j + rl;
+        b[j] = *reinterpret_cast<const uint4*>(sx + r * 128u + ((4u * q + g) ^ swz(r)) * 16u);
+      }
 #pragma unroll
       for (uint32_t i = 0; i < 4; ++i)
 #pragma unroll
@@ -191,14 +208,10 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
     if (norms) {  // thread: half (tid & 1) of row tid >> 1 of the router tile
       const uint32_t row = tid >> 1;
 #pragma unroll
-      for (uint32_t c = 0; c < 8u; ++c) {
-        const uint32_t chunk = 8u * (tid & 1u) + c;
-        nsum += sumsq8(*reinterpret_cast<const uint4*>(sw + row * 256u + ((chunk ^ (row & 15u)) * 16u)));
+      for (uint32_t c = 0; c < 4u; ++c) {
+        const uint32_t chunk = 4u * (tid & 1u) + c;
+        nsum += sumsq8(*reinterpret_cast<const uint4*>(sw + row * 128u + ((chunk ^ swz(row)) * 16u)));
       }
-    }
-    if (kb + 2u < KBS) {
-      nklds::barrier();  // every wave is done with stage kb & 1
-      issue(kb + 2u);
     }
   }
   if (norms) {

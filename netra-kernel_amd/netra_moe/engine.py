@@ -296,7 +296,7 @@ def _screen_front(cfg: MoEConfig) -> list[dict]:
     Z = screen_splits(cfg)
     return [
         dict(name="moe.route_screen", symbol=f"netra_moe_route_screen_h{H}_k{H // 128 // Z}_gfx950",
-             grid=((T + 127) // 128, (RP + 127) // 128, Z), block=(256, 1, 1), lds=2 * 2 * 128 * 256, dyn=0,
+             grid=((T + 127) // 128, (RP + 127) // 128, Z), block=(256, 1, 1), lds=4 * 2 * 128 * 128, dyn=0,
              args=["x", "router_w", "screen", "route_wsq", u(T), u(H), u(cfg.E), u(RP)],
              reads=["x", "router_w"], writes=["screen", "route_wsq"],
              refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150"]),

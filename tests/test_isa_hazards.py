@@ -129,7 +129,7 @@ def test_no_valu_sgpr_to_vmem_hazard_in_any_kernel():
 # vmcnt waits an LDS-ring kernel family may use inside its ring: 0 or the
 # copies of one step (kCopiesPerWave in moe_gemm_lds.hip, kCopies in
 # route_screen)
-RING_WAITS = {"netra_moe_gate_up_lds_": {0, 6, 7}, "netra_moe_route_screen_": {0, 16}}
+RING_WAITS = {"netra_moe_gate_up_lds_": {0, 6, 7}, "netra_moe_route_screen_": {0, 8, 16}}
 KCOPIES = 7
 _VMCNT = re.compile(r"vmcnt\((\d+)\)")
 _VSTORE = re.compile(r"(global|buffer|flat)_store")

@@ -69,6 +69,19 @@ EXTRA_CONFIGS = {
                               seed=1114),
     # the single-token down with sixteen routes (two tiles per wave), no shared expert
     "single_k16": MoEConfig("single_k16", T=1, H=2048, E=256, K=16, I=512, S=0, seed=1111),
+    # expert tails on the tile path: every token on experts 0, 1 and the shared
+    # expert, so each holds T rows; a last block of at most 16 rows after an
+    # even number of full blocks is computed by the pair before it (1 and 16
+    # rows: absorbed; 17 rows: an item of its own; 272 = 4 x 64 + 16: the
+    # second pair absorbs)
+    "tails_t129_hot": MoEConfig("tails_t129_hot", T=129, H=512, E=16, K=2, I=256, S=1, router_bias="hot",
+                                seed=1115),
+    "tails_t144_hot": MoEConfig("tails_t144_hot", T=144, H=512, E=16, K=2, I=256, S=1, router_bias="hot",
+                                seed=1116),
+    "tails_t145_hot": MoEConfig("tails_t145_hot", T=145, H=512, E=16, K=2, I=256, S=1, router_bias="hot",
+                                seed=1117),
+    "tails_t272_hot": MoEConfig("tails_t272_hot", T=272, H=512, E=16, K=2, I=256, S=1, router_bias="hot",
+                                seed=1118),
 }
 CONFIGS = {**BASELINE_CONFIGS, **EXTRA_CONFIGS}
 CASES = [(name, path) for name in CONFIGS for path in ("fused", "stream", "tile")

@@ -759,8 +759,13 @@ __device__ __forceinline__ void ffn_down(
         const int32_t r = __shfl(route, (lane >> 4) * 4u + j);
         if (r >= 0) {
           float* dst = partial + (size_t)r * H + d * 32u + (lane & 15u);
-          __hip_atomic_store(dst, acc0[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(dst + 16, acc1[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if constexpr (kHandoff) {  // read back by another workgroup of this launch
+            __hip_atomic_store(dst, acc0[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(dst + 16, acc1[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          } else {  // read by the combine kernel after this launch
+            dst[0] = acc0[j];
+            dst[16] = acc1[j];
+          }
         }
       }
     };

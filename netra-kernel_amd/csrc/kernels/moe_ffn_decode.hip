@@ -48,7 +48,7 @@
 //     (wide: hq/hs as they are; narrow: hrows requantised, item b == 0 also
 //     writing hq/hs for inspection), and wave w takes 32-column item w % CB
 //     over K split w / CB (SB = 8 / CB). Each valid row's fp32 result goes to
-//     partial[route] with agent-scope stores.
+//     partial[route] (agent-scope stores where the hand-off reads it back).
 // Items are dealt round-robin (item = workgroup, + grid, ...). Nothing waits
 // for another workgroup.
 //

@@ -14,9 +14,10 @@
 // items measured slower: its step loop could not be unrolled without spills.)
 //
 // The copies are inline assembly waited for by explicit vmcnt counts: every
-// wave issues the same six copies per step and nothing else in the K loop
-// touches vector memory, so "this wave's copies for step kb are done" is
-// vmcnt <= 6 (the next step's copies). A barrier then makes every wave's
+// wave issues the same six copies per step (seven in the tail variant below)
+// and nothing else in the K loop touches vector memory, so "this wave's
+// copies for step kb are done" is vmcnt <= 6 (7): the next step's copies. A
+// barrier then makes every wave's
 // copies visible to all, and (being after every read of the stage about to be
 // refilled) keeps refills behind reads.
 //

@@ -82,6 +82,8 @@ EXTRA_CONFIGS = {
                                 seed=1117),
     "tails_t272_hot": MoEConfig("tails_t272_hot", T=272, H=512, E=16, K=2, I=256, S=1, router_bias="hot",
                                 seed=1118),
+    "tails_t144_h1024_hot": MoEConfig("tails_t144_h1024_hot", T=144, H=1024, E=16, K=2, I=256, S=1,
+                                      router_bias="hot", seed=1120),
     # twice the largest benchmark token count: larger capacities, several
     # rounds of every prefill grid, more expert tails
     "prefill_t8192": MoEConfig("prefill_t8192", T=8192, H=2048, E=256, K=8, I=512, S=1, seed=1119),

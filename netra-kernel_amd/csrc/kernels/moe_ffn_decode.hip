@@ -59,8 +59,10 @@
 // arrival that brings it to Ktot is the last of the token's routes for that
 // group, and its workgroup reads the Ktot partial rows back at agent scope and
 // writes out[t, group] = bf16(sum over slots in order of fmaf(w_s, p_s, acc))
-// from acc = 0 (the order of netra_moe_combine_gfx950), then puts the counter
-// back to zero for the next launch. Agent-scope (sc1) stores and loads carry
+// from acc = 0 (the order of netra_moe_combine_gfx950). The arrival is one
+// wrapping atomic increment (old >= Ktot - 1 ? 0 : old + 1), so the last
+// arrival leaves the counter at zero for the next launch with no separate
+// reset that could be lost. Agent-scope (sc1) stores and loads carry
 // the hand-off: the per-XCD L2s are not coherent with each other for plain
 // accesses.
 //
@@ -631,8 +633,8 @@ __device__ __forceinline__ void ffn_down(
         const int32_t t = s_itok[i * 16u + (lane & 15u)];
         if (t >= 0) {
           uint32_t* ctr = &counters[(uint32_t)t * kMaxGroups + s_igrp[i]];
-          last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == Ktot - 1u;
-          if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          // wrapping increment: the Ktot-th arrival leaves the counter at zero
+          last = __builtin_amdgcn_atomic_inc32(ctr, Ktot - 1u, __ATOMIC_RELAXED, "agent") == Ktot - 1u;
         }
       }
       const unsigned long long m = __ballot(last);

@@ -312,9 +312,12 @@ __device__ __forceinline__ void topk_token(const uint16_t* __restrict__ lrow, co
 // arrivals on counters[kCounterStride * blockIdx.y] (an atomic per workgroup,
 // after its logit stores have completed; one counter per 256-byte line, as
 // atomics on one line serialise); the last arriver reads the logits at agent
-// scope and puts the counter back to zero for the next launch (counters start
-// at zero: the engine zeroes its workspace when it is created). No workgroup
-// waits on another, so the launch cannot deadlock whatever the residency.
+// scope. The arrival is a wrapping increment (old >= gridDim.x - 1 ? 0 :
+// old + 1, one atomic), so the last arrival itself puts the counter back to
+// zero for the next launch and no separate reset can be lost between two
+// launches (counters start at zero: the engine zeroes its workspace when it
+// is created). No workgroup waits on another, so the launch cannot deadlock
+// whatever the residency.
 constexpr uint32_t kCounterStride = 64;  // u32 words between hand-off counters
 template <uint32_t NJ, uint32_t NT>
 __device__ __forceinline__ void route(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
@@ -328,8 +331,8 @@ __device__ __forceinline__ void route(const uint16_t* __restrict__ x, const uint
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this workgroup's logit stores have completed
   __syncthreads();
   if (threadIdx.x == 0)
-    s_arrival = __hip_atomic_fetch_add(&counters[kCounterStride * blockIdx.y], 1u, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+    s_arrival = __builtin_amdgcn_atomic_inc32(&counters[kCounterStride * blockIdx.y], gridDim.x - 1u,
+                                              __ATOMIC_RELAXED, "agent");
   __syncthreads();
   if (s_arrival != gridDim.x - 1u) return;
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
@@ -338,8 +341,6 @@ __device__ __forceinline__ void route(const uint16_t* __restrict__ x, const uint
     const uint16_t* lrow = logits + (size_t)t * rows;
     topk_token<true>(lrow, bias, ids, weights, t, E, K, S, lane);
   }
-  if (threadIdx.x == 0)
-    __hip_atomic_store(&counters[kCounterStride * blockIdx.y], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 #define NK_ROUTE(HV, NT)                                                                          \

@@ -26,12 +26,13 @@ from dataclasses import dataclass
 from pathlib import Path
 
 from .config import BLOCK_M, MoEConfig
-from .contracts import HipKernelContract, Launch, canonical_json
+from .contracts import FallbackContract, HipKernelContract, Launch, _pairs, canonical_json, stable_hash
 from .profiles import profile_for
 from . import paths
 
 DTYPE_BYTES = {"bf16": 2, "f32": 4, "e4m3": 1, "i32": 4, "u32": 4, "u64": 8}
 ALIGN = 256
+OPERATION_NAME = "moe.routed_layer"
 
 
 @dataclass(frozen=True)
@@ -616,16 +617,202 @@ def _dependencies(ops: list[dict]) -> list[list[int]]:
 # launch puts them back to zero. They get bytes of their own in the workspace.
 PERSISTENT_TENSORS = frozenset({"route_counters", "ffn_counters"})
 
+COMPILER_NAME = "netra-moe-compiler"
+COMPILER_VERSION = "0.3.0"
+# The eight artefact files of a netra-engine-1 directory, in the reference
+# compiler's order (compiler/netra_compiler/engine.py:478-479).
+ARTIFACT_FILES = ("contracts.json", "graph.json", "graph_recipe.json", "memory_plan.json",
+                  "layout_plan.json", "symbols.json", "validation_plan.json", "explain.json")
+# Configuration fields an engine is guarded on, named as the reference's
+# deployment guards name them (compiler/netra_compiler/engine.py:445-468).
+ACTIVATION_QUANT, WEIGHT_QUANT = "e4m3_per_128", "e4m3_128x128"
+IR_DTYPES = {"bf16": "bf16", "f32": "fp32", "e4m3": "fp8_e4m3", "i32": "int32", "u32": "uint32", "u64": "uint64"}
+
+
+def _quantization() -> dict:
+    return {"activation": ACTIVATION_QUANT, "weight": WEIGHT_QUANT,
+            "activation_scale_block": 128, "weight_scale_block": [128, 128]}
+
+
+def op_typing(cfg: MoEConfig, op: dict, path: str) -> dict:
+    """The typed-contract fields of one operation: shape [m, n, k], dtypes
+    [input, weight, accumulator, output], layouts [activation, weight,
+    output], epilogue and numerical rules, in the reference's vocabulary
+    (compiler/netra_compiler/contracts.py:176-285, types.py:11-32)."""
+    kind = op["name"].split(".", 1)[1]
+    T, H, I = cfg.T, cfg.H, cfg.I
+    h_layout = H_LAYOUTS[path]
+    partial_dtype = "bf16" if path == "tile" else "fp32"
+    num = {"accumulation_dtype": "fp32", "nan_behavior": "ieee_preserve", "deterministic": True}
+    router = {"output_rounding": "rne_bf16_logits",
+              "reduction_order": "sixteen_slice_fmaf_chains_then_tree_8_4_2_1"}
+    topk = {"selection": "topk_lowest_index_on_ties.softmax_of_selected_exp_cw7"}
+    if kind in ("route", "route_select"):
+        typ = dict(shape=[T, cfg.router_rows, H], dtypes=["bf16", "bf16", "fp32", "fp32"],
+                   layouts=["row_major", "row_major", "topk_slots_row_major"], epilogue="identity",
+                   numerical={**num, **router, **topk})
+        if op["symbol"].startswith("netra_moe_router_logits"):
+            typ.update(dtypes=["bf16", "bf16", "fp32", "bf16"], layouts=["row_major", "row_major", "row_major"],
+                       numerical={**num, **router})
+    elif kind == "route_screen":
+        typ = dict(shape=[T, cfg.E, H], dtypes=["bf16", "bf16", "fp32", "fp32"],
+                   layouts=["row_major", "row_major", "screen_partials_ksplit"], epilogue="identity",
+                   numerical={**num, "output_rounding": "fp32_partial_per_k_split",
+                              "reduction_order": "bf16_mfma_k_split_partials"})
+    elif kind in ("sort", "sort_count", "sort_place"):
+        typ = dict(shape=[cfg.routes, cfg.Etot, 1], dtypes=["int32", "int32", "int32", "int32"],
+                   layouts=["topk_slots_row_major", "none", "sorted_m64_slot24"], epilogue="identity",
+                   numerical={**num, "accumulation_dtype": "int32", "output_rounding": "exact_integer",
+                              "reduction_order": "expert_then_token_ascending"})
+    elif kind == "gate_up":
+        typ = dict(shape=[cfg.routes, 2 * I, H], dtypes=["fp8_e4m3", "fp8_e4m3", "fp32", "fp8_e4m3"],
+                   layouts=["row_major_scale_1x128", "tile16x128_gate_up_interleaved", h_layout],
+                   epilogue="gated_silu",
+                   numerical={**num, "output_rounding": "silu_mul_rne_bf16_then_e4m3_per_128",
+                              "reduction_order": "k_block_ascending_fixed"})
+    elif kind == "down":
+        combined = path == "fused" and ffn_variant(cfg) == "narrow"
+        typ = dict(shape=[cfg.routes, H, I],
+                   dtypes=["fp8_e4m3", "fp8_e4m3", "fp32", "bf16" if combined else partial_dtype],
+                   layouts=[h_layout, "tile16x128", "row_major" if combined else "route_partials_row_major"],
+                   epilogue="identity",
+                   numerical={**num, "reduction_order": "k_block_ascending_fixed",
+                              "output_rounding": "topk_slots_ascending_fmaf_then_rne_bf16" if combined
+                              else f"route_partial_{partial_dtype}"})
+    elif kind == "combine":
+        typ = dict(shape=[T, H, cfg.Ktot], dtypes=[partial_dtype, "fp32", "fp32", "bf16"],
+                   layouts=["route_partials_row_major", "topk_slots_row_major", "row_major"], epilogue="identity",
+                   numerical={**num, "output_rounding": "rne_bf16",
+                              "reduction_order": "topk_slots_ascending_fmaf"})
+    else:
+        raise ValueError(f"no typed contract for operation {op['name']}")
+    typ["quantization"] = _quantization()
+    return typ
+
+
+def _kernarg_layout(args: list) -> tuple[list[int], int]:
+    """Byte offset of every kernel argument (pointers 8 bytes, u32 constants
+    4, each at its natural alignment) and the 8-byte-aligned kernarg size."""
+    offs, pos = [], 0
+    for a in args:
+        size = 4 if isinstance(a, tuple) else 8
+        pos = (pos + size - 1) // size * size
+        offs.append(pos)
+        pos += size
+    return offs, (pos + 7) // 8 * 8
+
+
+def model_configuration(cfg: MoEConfig) -> dict:
+    """The layer's configuration as an engine is guarded on it."""
+    return {"architecture": "routed_moe_fp8_block128", "hidden_size": cfg.H,
+            "moe_intermediate_size": cfg.I, "num_experts": cfg.E, "num_experts_per_tok": cfg.K,
+            "shared_experts": cfg.S, "quantization_method": "fp8", "quantization_format": "e4m3fn",
+            "activation_quantization": ACTIVATION_QUANT, "weight_scale_block": [128, 128],
+            "kernel_scale_dtype": "fp32", "tensor_parallel": 1, "tokens": cfg.T}
+
+
+DEPLOYMENT_GUARD_FIELDS = ("architecture", "hidden_size", "quantization_method", "quantization_format",
+                           "activation_quantization", "weight_scale_block", "kernel_scale_dtype",
+                           "tensor_parallel")
+
+
+def _compiler_record(code_sha: str) -> dict:
+    """Compiler identity: the package's Python sources, the tactic catalog and
+    the code object (what the engine's contents follow from)."""
+    from .planner import catalog
+    pkg = Path(__file__).resolve().parent
+    sources = {f.name: hashlib.sha256(f.read_bytes()).hexdigest() for f in sorted(pkg.glob("*.py"))}
+    tactics = [{"name": t.name, "path": t.path, "front": t.front, "rank": t.rank, "maturity": t.maturity}
+               for t in catalog()]
+    return {"name": COMPILER_NAME, "version": COMPILER_VERSION,
+            "source_hash": stable_hash({"version": COMPILER_VERSION, "python_sources": sources,
+                                        "tactics": tactics, "code_object_sha256": code_sha})}
+
+
+def _layout_plan() -> dict:
+    """How checkpoint weights become the bound tensors (netra_moe.prep: the
+    steps of compiler/netra_compiler/layouts.py:109-206 for this layout)."""
+    def step(src, dst, transform, params=(), scope="synthetic_checkpoint_bit_exact"):
+        return {"source_layout": src, "target_layout": dst, "transform": transform,
+                "parameters": dict(params), "validated_scope": scope}
+
+    def scale(name, tensors):
+        return {"tensor": name, "checkpoint_tensors": tensors, "checkpoint_dtype": "bf16",
+                "kernel_dtype": "fp32", "block": [128, 128], "checkpoint_layout": "row_major_block_grid",
+                "kernel_layout": "row_major_block_grid",
+                "steps": ["concatenate_output_scale_shards_axis0", "widen_bf16_to_fp32_exact", "stack_experts"]}
+    rm = "checkpoint_row_major_fp8_block128"
+    w13_src = ["mlp.experts.*.gate_proj.weight", "mlp.experts.*.up_proj.weight",
+               "mlp.shared_expert.gate_proj.weight", "mlp.shared_expert.up_proj.weight"]
+    w2_src = ["mlp.experts.*.down_proj.weight", "mlp.shared_expert.down_proj.weight"]
+    return {"format": "netra-layout-plan-1", "bindings": [
+        {"tensor": "w13", "checkpoint_layout": rm, "kernel_layout": "tile16x128_gate_up_interleaved",
+         "output_layout": None, "checkpoint_tensors": w13_src,
+         "steps": [step(rm, rm, "concatenate_output_shards", (("axis", 0),)),
+                   step(rm, "stacked_row_major_fp8_block128", "stack_experts",
+                        (("rows_gate_then_up", 1), ("shared_expert_last", 1))),
+                   step("stacked_row_major_fp8_block128", "tile16x128_gate_up_interleaved",
+                        "tile16x128_gate_up_interleaved", (("tile_m", 16), ("tile_k", 128)))],
+         "scale": scale("w13_scale", [n + "_scale_inv" for n in w13_src])},
+        {"tensor": "w2", "checkpoint_layout": rm, "kernel_layout": "tile16x128",
+         "output_layout": None, "checkpoint_tensors": w2_src,
+         "steps": [step(rm, rm, "concatenate_output_shards", (("axis", 0),)),
+                   step(rm, "stacked_row_major_fp8_block128", "stack_experts", (("shared_expert_last", 1),)),
+                   step("stacked_row_major_fp8_block128", "tile16x128", "tile16x128",
+                        (("tile_m", 16), ("tile_k", 128)))],
+         "scale": scale("w2_scale", [n + "_scale_inv" for n in w2_src])},
+    ]}
+
+
+def _graph(cfg: MoEConfig, tensors: dict, ops: list[dict]) -> dict:
+    """The layer as a netra-ir-1 graph (compiler/netra_compiler/ir.py:126-249):
+    typed tensors with roles, operations with their inputs and outputs."""
+    role = lambda n, s: "state" if n in PERSISTENT_TENSORS else s.role  # noqa: E731
+    return {
+        "format": "netra-ir-1", "name": f"netra-moe-{cfg.name}",
+        "tensors": [{"name": n, "shape": list(s.shape), "dtype": IR_DTYPES[s.dtype],
+                     "layout": "engine_internal" if s.role == "temporary" else "row_major",
+                     "role": role(n, s), "alias_of": None, "persistent": n in PERSISTENT_TENSORS}
+                    for n, s in tensors.items()],
+        "operations": [{"name": op["name"], "kind": "moe_fp8_block128", "inputs": list(op["reads"]),
+                        "outputs": list(op["writes"]), "attributes": {"kernel_symbol": op["symbol"]},
+                        "numerical": {}} for op in ops],
+        "inputs": [n for n, s in tensors.items() if s.role in ("input", "weight")],
+        "outputs": [n for n, s in tensors.items() if s.role == "output"],
+        "state": sorted(n for n in tensors if n in PERSISTENT_TENSORS),
+    }
+
+
+def _symbol_listing(hsaco: Path, code: bytes, symbols: list[str]) -> str:
+    """Text listing of the kernel symbols an engine names in its code object,
+    the source its validation plan points at for each symbol."""
+    sha = hashlib.sha256(code).hexdigest()
+    return "".join([f"# kernel symbols of {hsaco.name} (sha256 {sha}) used by this engine\n"]
+                   + [s + "\n" for s in symbols])
+
+
+def _write(directory: Path, docs: dict) -> None:
+    for fname, doc in docs.items():
+        (directory / fname).write_text(canonical_json(doc))
+
+
+def _finish_engine(engine: dict) -> dict:
+    engine["engine_id"] = "ne_" + stable_hash(engine)[:24]
+    return engine
+
 
 def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ...] = (),
                        hsaco: Path | None = None, path: str = "auto", front: str = "auto",
                        semantics: dict | None = None, allow_experimental: bool = False) -> dict:
-    """Plan the layer (netra_moe.planner), then write the engine directory:
-    engine.json, contracts.json, graph_recipe.json, memory_plan.json and
-    explain.json (every tactic considered, with its rejection reasons). When no
-    tactic serves the request the engine holds one framework-fallback operation
-    and no kernels. Returns the graph recipe (also on disk)."""
-    from .planner import layer_request, pack_workspace, plan_layer
+    """Plan the layer (netra_moe.planner), then write the netra-engine-1
+    directory the reference compiler writes (compiler/netra_compiler/engine.py:
+    373-504): engine.json, contracts.json (netra-contract-set-1), graph.json,
+    graph_recipe.json, memory_plan.json, layout_plan.json, symbols.json,
+    validation_plan.json and explain.json (every tactic considered, with its
+    rejection reasons), plus hsaco/. When no tactic serves the request the
+    engine holds one framework-fallback operation and no kernels. Returns the
+    graph recipe (also on disk)."""
+    from .planner import catalog, layer_request, pack_workspace, plan_layer
     directory = Path(directory)
     hsaco = Path(hsaco) if hsaco else paths.hsaco_path()
     if not hsaco.is_file():
@@ -633,8 +820,11 @@ def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ..
     plan = plan_layer(layer_request(cfg, semantics=semantics, path=path, front=front),
                       allow_experimental=allow_experimental)
     profile = profile_for(cfg)
+    code = hsaco.read_bytes()
+    sha = hashlib.sha256(code).hexdigest()
     explain = {"format": "netra-explain-1", "profile": profile.to_dict(),
                "operations": [plan.explain("moe.layer")]}
+    model_cfg = model_configuration(cfg)
     engine = {
         "format_version": "netra-engine-1",
         "target": "gfx950",
@@ -642,23 +832,54 @@ def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ..
         "required_rocm": {"minimum": "7.0", "code_object_version": 6},
         "name": f"netra-moe-{cfg.name}",
         "configuration": cfg.to_dict(),
-        "profiles": [{"name": profile.name, "guards": profile.to_dict()["guards"],
-                      "tensor_parallel": profile.tensor_parallel}],
-        "artifact_files": ["contracts.json", "graph_recipe.json", "memory_plan.json", "explain.json"],
+        "model_configuration_hash": stable_hash(model_cfg),
+        "checkpoint_hash": None,
+        "deployment_guards": {k: model_cfg[k] for k in DEPLOYMENT_GUARD_FIELDS},
+        "tensor_parallel": 1,
+        "profiles": [profile.to_dict()],
+        "layout_plan": "layout_plan.json", "graph_recipe": "graph_recipe.json", "memory_plan": "memory_plan.json",
+        "validation_status": "static_only_not_promoted",
+        "compiler": _compiler_record(sha),
+        "golden_artifacts": [],
+        "artifact_files": list(ARTIFACT_FILES),
     }
+    validation = {"format": "netra-validation-plan-1", "static": "pending", "cross_assembly": "not_applicable",
+                  "hardware": "not_run", "real_checkpoint_correctness": "not_run", "graph_replay": "not_run",
+                  "matched_server_ab": "not_run", "promotion_eligible": False, "candidates": [],
+                  "golden_artifacts": [],
+                  "commands": ["netra_engine_manifest_check ENGINE_DIR",
+                               "python -m pytest tests -m gpu (gfx950 device; parity against the CPU oracle)"]}
     directory.mkdir(parents=True, exist_ok=True)
     if plan.selected is None:
-        engine.update(gemm_path=None, front_end=None, workspace_bytes=0, selected_tactics=[],
-                      operations=[{"name": "moe.layer", "execution": "fallback", "fallback": plan.fallback}],
+        # the requested computation, with no tactic to run it (contracts.py:288-375)
+        fb = FallbackContract(
+            operation=OPERATION_NAME, shape=(cfg.routes, 2 * cfg.I, cfg.H),
+            dtypes=("bf16", "fp8_e4m3", "fp32", "bf16"), quantization=_pairs(_quantization()),
+            layouts=("row_major", str((semantics or {}).get("layouts", "unspecified")), "row_major"),
+            epilogue="gated_silu", numerical=_pairs({"accumulation_dtype": "fp32", "deterministic": True}),
+            fallback=plan.fallback)
+        engine.update(gemm_path=None, front_end=None, workspace_bytes=0, selected_tactics=[], kernel_symbols=[],
+                      operations=[{"index": 0, "name": "moe.layer", "kind": OPERATION_NAME,
+                                   "contract_id": fb.stable_id, "tactic": None, "maturity": None,
+                                   "execution": "fallback", "kernel_symbol": None, "launch": None,
+                                   "workspace_offset": None, "fallback": plan.fallback,
+                                   "bindings": {"inputs": ["x", "router_w", "router_bias", "w13", "w13_scale",
+                                                           "w2", "w2_scale"], "outputs": ["out"]},
+                                   "artifact_kind": None}],
                       fallbacks={"moe.layer": plan.fallback})
-        recipe = {"format": "netra-graph-recipe-1", "execution": "fallback", "gemm_path": None,
+        recipe = {"format": "netra-graph-recipe-1", "profile": profile.name, "capture_at_initialization": False,
+                  "portable_serialized_hip_graph": False, "execution": "fallback", "gemm_path": None,
                   "front_end": None, "operations": [], "tensors": {}, "bindings": {}, "dependencies": []}
-        for fname, doc in (("engine.json", engine), ("contracts.json", {"contracts": []}),
-                           ("graph_recipe.json", recipe),
-                           ("memory_plan.json", {"format": "netra-memory-plan-1", "workspace_bytes": 0,
-                                                 "alignment": ALIGN, "buffers": [], "offsets": {}}),
-                           ("explain.json", explain)):
-            (directory / fname).write_text(canonical_json(doc))
+        graph = {"format": "netra-ir-1", "name": f"netra-moe-{cfg.name}", "tensors": [], "operations": [],
+                 "inputs": [], "outputs": [], "state": []}
+        _write(directory, {
+            "contracts.json": {"format": "netra-contract-set-1", "contracts": [fb.to_dict()]},
+            "graph.json": graph, "graph_recipe.json": recipe,
+            "memory_plan.json": {"format": "netra-memory-plan-1", "workspace_bytes": 0, "alignment": ALIGN,
+                                 "buffers": [], "offsets": {}},
+            "layout_plan.json": _layout_plan(), "symbols.json": {"selected": [], "candidates": []},
+            "validation_plan.json": validation, "explain.json": explain,
+            "engine.json": _finish_engine(engine)})
         return recipe
 
     path, front = plan.selected.path, plan.selected.front
@@ -667,57 +888,84 @@ def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ..
     if unknown:
         raise ValueError(f"cannot expose unknown tensors {sorted(unknown)}")
     ops = operations(cfg, path, front)
-    code = hsaco.read_bytes()
-    sha = hashlib.sha256(code).hexdigest()
 
     # Workspace: engine-owned temporaries, interval-packed, 256-byte aligned.
     owned = {n: s.nbytes for n, s in tensors.items() if s.role == "temporary" and n not in expose}
     workspace_bytes, slots = pack_workspace(owned, ops, set(PERSISTENT_TENSORS), ALIGN)
     offsets = {sl.name: sl.offset for sl in slots}
+    deps = _dependencies(ops)
 
     bindings: dict[str, list[list[int]]] = {}
     op_records, contracts = [], []
     for oi, op in enumerate(ops):
         arguments = []
+        arg_offsets, kernarg = _kernarg_layout(op["args"])
         for ai, a in enumerate(op["args"]):
             if isinstance(a, tuple):
-                arguments.append({"kind": "u32_constant", "value": a[1]})
+                arguments.append({"kind": "u32_constant", "value": a[1], "offset": arg_offsets[ai]})
             elif a in offsets:
                 arguments.append({"kind": "pointer", "source": "workspace", "tensor": a,
-                                  "workspace_offset": offsets[a]})
+                                  "workspace_offset": offsets[a], "offset": arg_offsets[ai]})
             else:
-                arguments.append({"kind": "pointer", "source": "binding", "tensor": a})
+                arguments.append({"kind": "pointer", "source": "binding", "tensor": a, "offset": arg_offsets[ai]})
                 bindings.setdefault(a, []).append([0, oi, ai])
         launch = Launch(tuple(op["grid"]), tuple(op["block"]), op["lds"], op["dyn"])
-        kernarg = sum(4 if isinstance(a, tuple) else 8 for a in op["args"])
-        kernarg = (kernarg + 7) // 8 * 8
+        typ = op_typing(cfg, op, path)
         contract = HipKernelContract(
             operation=op["name"], family="moe.fp8_block128.gfx950_hip", symbol=op["symbol"],
             constants=(("T", cfg.T), ("H", cfg.H), ("I", cfg.I), ("E", cfg.E), ("K", cfg.K),
                        ("S", cfg.S), ("BLOCK_M", BLOCK_M), ("SCALE_BLOCK", 128)),
             semantics=layer_semantics(op["symbol"], path, front),
             launch=launch, kernarg_size=kernarg, code_object_sha256=sha,
-            source_refs=tuple(op["refs"]))
+            shape=tuple(typ["shape"]), dtypes=tuple(typ["dtypes"]), quantization=_pairs(typ["quantization"]),
+            layouts=tuple(typ["layouts"]), epilogue=typ["epilogue"], tactic=plan.selected.name,
+            numerical=_pairs(typ["numerical"]), maturity=plan.selected.maturity, fallback=plan.fallback,
+            source_refs=tuple(op["refs"]), evidence_refs=tuple(plan.selected.evidence_refs))
         contracts.append(contract.to_dict())
         op_records.append({
-            "name": op["name"], "execution": "kernel", "contract_id": contract.stable_id,
-            "tactic": plan.selected.name, "launch": launch.to_dict(), "hsaco": "hsaco/" + hsaco.name,
-            "kernel_symbol": op["symbol"], "arguments": arguments,
+            "index": oi, "name": op["name"], "kind": OPERATION_NAME, "contract_id": contract.stable_id,
+            "tactic": plan.selected.name, "maturity": plan.selected.maturity, "execution": "kernel",
+            "kernel_symbol": op["symbol"], "launch": launch.to_dict(), "workspace_offset": None,
+            "fallback": plan.fallback, "bindings": {"inputs": list(op["reads"]), "outputs": list(op["writes"])},
+            "artifact_kind": "hip_code_object", "hsaco": "hsaco/" + hsaco.name, "hsaco_sha256": sha,
+            "kernarg_size": kernarg, "arguments": arguments,
         })
 
+    selected_symbols = sorted({op["symbol"] for op in ops})
+    # kernels of the other tactics that also serve this request (explain.json's compatible candidates)
+    other: set[str] = set()
+    by_name = {t.name: t for t in catalog()}
+    for cand in plan.candidates:
+        t = by_name.get(cand["tactic"])
+        if t is None or cand["reasons"] or t is plan.selected:
+            continue
+        other.update(o["symbol"] for o in operations(cfg, t.path, t.front))
+    candidate_symbols = sorted(other - set(selected_symbols))
+    listing = f"hsaco/{hsaco.stem}.symbols.txt"
+    validation["candidates"] = [
+        {"symbol": sym, "source": listing, "artifact_kind": "hip_code_object", "hsaco": "hsaco/" + hsaco.name,
+         "hsaco_sha256": sha, "selected": sym in selected_symbols}
+        for sym in selected_symbols + candidate_symbols]
+
     engine.update(gemm_path=path, front_end=front, workspace_bytes=workspace_bytes,
-                  selected_tactics=[plan.selected.name], operations=op_records, fallbacks={})
+                  selected_tactics=[plan.selected.name], kernel_symbols=selected_symbols,
+                  operations=op_records, fallbacks={})
     recipe = {
         "format": "netra-graph-recipe-1",
+        "profile": profile.name,
+        "capture_at_initialization": True,
+        "portable_serialized_hip_graph": False,
         "execution": "kernel",
         "gemm_path": path,
         "front_end": front,
-        "operations": [op["name"] for op in ops],
+        "operations": [{"index": r["index"], "name": r["name"], "depends_on": deps[r["index"]],
+                        "execution": "kernel", "kernel_symbol": r["kernel_symbol"], "launch": r["launch"],
+                        "bindings": r["bindings"], "workspace_offset": None} for r in op_records],
         "tensors": {n: {"dtype": s.dtype, "shape": list(s.shape), "role": s.role,
                         "bytes": s.nbytes, "storage": "workspace" if n in offsets else "binding"}
                     for n, s in tensors.items()},
         "bindings": bindings,
-        "dependencies": _dependencies(ops),
+        "dependencies": deps,
     }
     memory_plan = {"format": "netra-memory-plan-1", "workspace_bytes": workspace_bytes, "alignment": ALIGN,
                    "unpacked_bytes": sum((b + ALIGN - 1) // ALIGN * ALIGN for b in owned.values()),
@@ -727,8 +975,11 @@ def compile_moe_engine(cfg: MoEConfig, directory: Path, *, expose: tuple[str, ..
     target = directory / "hsaco" / hsaco.name
     if not target.exists() or target.read_bytes() != code:
         shutil.copyfile(hsaco, target)
-    for fname, doc in (("engine.json", engine), ("contracts.json", {"contracts": contracts}),
-                       ("graph_recipe.json", recipe), ("memory_plan.json", memory_plan),
-                       ("explain.json", explain)):
-        (directory / fname).write_text(canonical_json(doc))
+    (directory / listing).write_text(_symbol_listing(hsaco, code, selected_symbols + candidate_symbols))
+    _write(directory, {
+        "contracts.json": {"format": "netra-contract-set-1", "contracts": contracts},
+        "graph.json": _graph(cfg, tensors, ops), "graph_recipe.json": recipe, "memory_plan.json": memory_plan,
+        "layout_plan.json": _layout_plan(), "symbols.json": {"selected": selected_symbols,
+                                                             "candidates": candidate_symbols},
+        "validation_plan.json": validation, "explain.json": explain, "engine.json": _finish_engine(engine)})
     return recipe

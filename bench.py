@@ -49,13 +49,17 @@ def gate_up_bytes(cfg, touched: int, path: str) -> int:
 
 
 def down_bytes(cfg, touched: int, path: str) -> int:
-    """Touched experts' W2 + scales, h in, route partial rows out (fused: the
-    combined bf16 output; its fp32 partials are hand-off traffic, not work)."""
+    """Touched experts' W2 + scales, h in, and what the kernel writes: the
+    combined bf16 output where the down kernel combines (fused narrow and
+    single-token variants), else its route partial rows (fp32 on the fused
+    wide and stream paths, bf16 on the tile path), which a combine kernel
+    reads back."""
+    from netra_moe.engine import down_variant
     w = touched * (cfg.H * cfg.I + 4 * (cfg.H // 128) * (cfg.I // 128))
     h = cfg.routes * cfg.I + 4 * cfg.routes * (cfg.I // 128)
-    if path == "fused":
+    if path == "fused" and down_variant(cfg) in ("narrow", "single"):
         return w + h + 2 * cfg.T * cfg.H
-    part = (4 if path == "stream" else 2) * cfg.routes * cfg.H  # fp32 / bf16 route partials
+    part = (2 if path == "tile" else 4) * cfg.routes * cfg.H  # bf16 / fp32 route partials
     return w + h + part
 
 

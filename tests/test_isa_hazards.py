@@ -16,7 +16,10 @@ cannot see around inline assembly:
   be off and a step would read a stage before its data arrived.
 
 Runs on the CPU over the disassembly of this repository's own build (the
-ROCm llvm tools); skipped when the code object or the tools are absent.
+ROCm llvm tools): the engine's code object and the gfx950 device code
+embedded in libnetra_moe.so (a separate compile of the kernels, which the
+allocation-free prefill entry point launches); skipped when an artefact or the
+tools are absent.
 """
 from __future__ import annotations
 
@@ -29,6 +32,8 @@ import pytest
 
 REPO = Path(__file__).resolve().parents[1]
 HSACO = REPO / "netra-kernel_amd" / "lib" / "netra_moe_gfx950.hsaco"
+LIB_SO = REPO / "netra-kernel_amd" / "lib" / "libnetra_moe.so"
+ARTEFACTS = {"hsaco": HSACO, "libnetra_moe.so": LIB_SO}
 LLVM = Path("/opt/rocm/llvm/bin")
 TARGET = "hipv4-amdgcn-amd-amdhsa--gfx950"
 WAIT_STATES = 5
@@ -87,13 +92,27 @@ def hazards(lines: list[str]) -> list[str]:
     return found
 
 
-def disassembly() -> dict[str, list[str]]:
-    bundler, objdump = LLVM / "clang-offload-bundler", LLVM / "llvm-objdump"
-    if not HSACO.exists() or not bundler.exists() or not objdump.exists():
-        pytest.skip("built code object or ROCm llvm tools not present")
+_CACHE: dict[str, dict[str, list[str]]] = {}
+
+
+def disassembly(artefact: str = "hsaco") -> dict[str, list[str]]:
+    """Per-function disassembly of the gfx950 code in one built artefact: the
+    offload bundle itself (hsaco) or the .hip_fatbin section of a shared
+    library."""
+    if artefact in _CACHE:
+        return _CACHE[artefact]
+    src = ARTEFACTS[artefact]
+    bundler, objdump, objcopy = LLVM / "clang-offload-bundler", LLVM / "llvm-objdump", LLVM / "llvm-objcopy"
+    if not src.exists() or not bundler.exists() or not objdump.exists() or not objcopy.exists():
+        pytest.skip("built artefact or ROCm llvm tools not present")
     with tempfile.TemporaryDirectory() as tmp:
+        bundle = src
+        if src.suffix == ".so":
+            bundle = Path(tmp) / "fatbin"
+            subprocess.run([str(objcopy), f"--dump-section=.hip_fatbin={bundle}", str(src), str(Path(tmp) / "so")],
+                           check=True, capture_output=True)
         out = Path(tmp) / "gfx950.co"
-        subprocess.run([str(bundler), "--unbundle", "--type=o", f"--input={HSACO}", f"--targets={TARGET}",
+        subprocess.run([str(bundler), "--unbundle", "--type=o", f"--input={bundle}", f"--targets={TARGET}",
                         f"--output={out}"], check=True, capture_output=True)
         text = subprocess.run([str(objdump), "-d", "--mcpu=gfx950", str(out)], check=True,
                               capture_output=True, text=True).stdout
@@ -106,6 +125,7 @@ def disassembly() -> dict[str, list[str]]:
             funcs[name] = []
         elif name:
             funcs[name].append(line)
+    _CACHE[artefact] = funcs
     return funcs
 
 
@@ -118,10 +138,11 @@ def test_checker_flags_the_hazard_and_accepts_wait_states():
     assert hazards(["v_add_co_u32_e64 v1, s[6:7], v2, v3", "buffer_load_dword v1, v2, s[4:7], 0 offen"])
 
 
-def test_no_valu_sgpr_to_vmem_hazard_in_any_kernel():
-    funcs = disassembly()
+@pytest.mark.parametrize("artefact", sorted(ARTEFACTS))
+def test_no_valu_sgpr_to_vmem_hazard_in_any_kernel(artefact):
+    funcs = disassembly(artefact)
     kernels = {k: v for k, v in funcs.items() if k.startswith("netra_moe_")}
-    assert kernels, "no netra_moe_ kernels in the code object"
+    assert kernels, f"no netra_moe_ kernels in {artefact}"
     report = {k: h for k, v in kernels.items() if (h := hazards(v))}
     assert not report, "\n".join(f"{k}: {h[0]}" for k, h in report.items())
 
@@ -202,10 +223,11 @@ def test_ring_checker_flags_a_foreign_load():
     assert ring_violations(drained) == []
 
 
+@pytest.mark.parametrize("artefact", sorted(ARTEFACTS))
 @pytest.mark.parametrize("prefix", sorted(RING_WAITS))
-def test_lds_ring_kernels_issue_only_their_copies(prefix):
-    funcs = disassembly()
+def test_lds_ring_kernels_issue_only_their_copies(prefix, artefact):
+    funcs = disassembly(artefact)
     ring = {k: v for k, v in funcs.items() if k.startswith(prefix)}
-    assert ring, f"no {prefix} kernels in the code object"
+    assert ring, f"no {prefix} kernels in {artefact}"
     report = {k: b for k, v in ring.items() if (b := ring_violations(v, RING_WAITS[prefix]))}
     assert not report, "\n".join(f"{k}: {b[0]}" for k, b in report.items())

@@ -150,10 +150,8 @@ __device__ __forceinline__ void ffn_gate_up(
   static_assert(I % (16u * CA * P) == 0 && H % kThreads == 0 && (P == 1 || SA == 1) && P <= kWaves, "shares");
   constexpr uint32_t kRed = SA > 1 ? kWaves * 8u * 64u * 4u : 0u;  // split sums
   constexpr bool kStageAll = SA > 1;  // narrow: one A operand (every token's row) for all items
-  constexpr uint32_t kProl = kMaxCap * 4u + (kMaxE + 1u) * 4u;      // s_owner, s_poff
-  constexpr uint32_t kBig0 = KB * 2048u > kRed || kStageAll ? KB * 2048u : kRed;
-  constexpr uint32_t kBig = kBig0 > kProl ? kBig0 : kProl;
-  // s_big: the tile's x rows | split sums | prologue tables
+  constexpr uint32_t kBig = KB * 2048u > kRed || kStageAll ? KB * 2048u : kRed;
+  // s_big: the tile's x rows | split sums
   __shared__ __align__(16) uint8_t s_big[kBig];
   __shared__ float s_xs[16 * KB];                                 // x row scales [kb][row]
   __shared__ __align__(16) uint16_t s_hb[kQuant ? 16u * kHb : 8u];  // the item's h rows (bf16)
@@ -164,8 +162,10 @@ __device__ __forceinline__ void ffn_gate_up(
   __shared__ float s_rsum[kStageAll ? kRed / 4u : 1u];  // narrow: split sums (s_big holds the A operand)
   uint8_t* const s_a = s_big;
   float* const s_red = kStageAll ? s_rsum : reinterpret_cast<float*>(s_big);
-  int32_t* const s_owner = reinterpret_cast<int32_t*>(s_big);
-  uint32_t* const s_poff = reinterpret_cast<uint32_t*>(s_big + kMaxCap * 4u);
+  // wide prologue tables (block owner, pair offsets) and the first item's expert
+  __shared__ int32_t s_owner[kStageAll ? 1u : kMaxCap];
+  __shared__ uint32_t s_poff[kStageAll ? 1u : kMaxE + 1u];
+  __shared__ uint32_t s_e0;
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = nkstream::wave_id();
   const uint32_t Ktot = K + S, Etot = E + S, routes = T * Ktot;
@@ -238,6 +238,52 @@ __device__ __forceinline__ void ffn_gate_up(
     st.ws = w13se[((sl < KB ? c : I / 16u + c) >> 3) * KB + (sl < KB ? sl : sl - KB)];
   };
   GateUpStep<kCH> b0, b1;
+  // wide: the x rows of sub-tile k of expert e, loaded into registers
+  // (stage_load: rows past e's routes zero) and then stored into s_a in the
+  // MFMA operand layout with their scales in s_xs (stage_store; the caller
+  // puts a barrier behind it). Lane l's row l & 15 is token
+  // nth_bit(mask, 16 k + (l & 15)).
+  constexpr uint32_t kPieces = kStageAll ? 1u : H / kThreads, kScales = (16u * KB + kThreads - 1u) / kThreads;
+  uint4 av[kPieces];
+  float xv[kScales];
+  auto stage_load = [&](uint32_t e, uint32_t k) __attribute__((always_inline)) {
+    if constexpr (!kStageAll) {
+      int32_t tok = -1;
+      {
+        const unsigned long long emask = s_mask[e];
+        const uint32_t j = 16u * k + (lane & 15u);
+        if (j < (uint32_t)__popcll(emask)) tok = (int32_t)nth_bit(emask, j);
+      }
+#pragma unroll
+      for (uint32_t q = 0; q < kPieces; ++q) {
+        const uint32_t pc = tid + q * kThreads, row = pc / (H / 16u), kk = (pc % (H / 16u)) * 16u;
+        const int32_t t = __shfl(tok, row);
+        av[q] = t >= 0 ? *reinterpret_cast<const uint4*>(xq + (size_t)t * H + kk) : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (uint32_t q = 0; q < kScales; ++q) {
+        const uint32_t i = tid + q * kThreads;
+        const int32_t t = __shfl(tok, (i / KB) & 15u);
+        xv[q] = (i < 16u * KB && t >= 0) ? xs[(size_t)t * KB + i % KB] : 0.0f;
+      }
+    }
+  };
+  auto stage_store = [&]() __attribute__((always_inline)) {
+    if constexpr (!kStageAll) {
+#pragma unroll
+      for (uint32_t q = 0; q < kPieces; ++q) {
+        const uint32_t pc = tid + q * kThreads, row = pc / (H / 16u), kk = (pc % (H / 16u)) * 16u;
+        const uint32_t kb = kk >> 7, k7 = kk & 127u;
+        *reinterpret_cast<uint4*>(&s_a[kb * 2048u + ((k7 >> 4) & 1u) * 1024u + ((k7 >> 5) * 16u + row) * 16u]) = av[q];
+      }
+#pragma unroll
+      for (uint32_t q = 0; q < kScales; ++q)
+        if (tid + q * kThreads < 16u * KB) {  // element i = row * KB + kb of the gather
+          const uint32_t i = tid + q * kThreads;
+          s_xs[(i % KB) * 16u + i / KB] = xv[q];
+        }
+    }
+  };
   const int32_t pad = (int32_t)((Ktot << 24) | T);
   // narrow: an expert holds at most T <= kNarrowT <= 16 routes, so it has one
   // block, one tile and one pair, all numbered g for the g-th expert with a
@@ -323,8 +369,24 @@ __device__ __forceinline__ void ffn_gate_up(
     if (tid < Etot) { s_boff[tid] = cb + ib - vb; s_toff[tid] = ct + it - vt; s_poff[tid] = cp + ip - vp; }
     if (tid == 0) { s_boff[Etot] = nblk; s_toff[Etot] = ntile; s_poff[Etot] = npair; }
     if (nblk > cap_blocks) return;  // impossible for T <= 64 with the engine's capacity; uniform
+    // This workgroup's round-0 item (the item loop's dealing) and its expert,
+    // read off the scan by the thread whose tile range holds it, so the item's
+    // first weight steps and x rows go out before the sorted outputs below.
+    uint32_t item0 = blockIdx.x;
+    bool has0 = item0 < ntile * GA;
+    if (gridDim.x % 8u == 0u) has0 = nklds::xcd_item(blockIdx.x, min(gridDim.x, ntile * GA), item0);
+    if (has0 && tid < Etot && item0 / GA - (ct + it - vt) < vt) s_e0 = tid;
     for (uint32_t b = tid; b < cap_blocks; b += kThreads) s_owner[b] = -1;
     lds_barrier();
+    if (has0) {  // uniform
+      // x row loads, then the weight steps, then the rows' LDS stores: the
+      // stores wait only for the (older) row loads
+      const uint32_t e = __builtin_amdgcn_readfirstlane((int)s_e0);
+      stage_load(e, item0 / GA - s_toff[e]);
+      issue_at(b0, e, item0, 0u);
+      if constexpr (NS == 2) issue_at(b1, e, item0, 1u);
+      stage_store();
+    }
     if (tid < Etot) {
       for (uint32_t b = s_boff[tid]; b < s_boff[tid + 1u]; ++b) s_owner[b] = (int32_t)tid;
       if (blockIdx.x == 0) {
@@ -356,7 +418,7 @@ __device__ __forceinline__ void ffn_gate_up(
       sorted_ids[p] = v;
       if ((p & 63u) == 0u) sorted_expert[b] = e;
     }
-    lds_barrier();  // s_owner / s_poff are dead from here: s_big is the items' space
+    lds_barrier();  // the staged x rows and scales are visible to every wave
   }
 
   // ---- items --------------------------------------------------------------------------------
@@ -389,51 +451,20 @@ __device__ __forceinline__ void ffn_gate_up(
       k = g - s_toff[e];
       row0 = (s_boff[e] + (k >> 2)) * 64u + (k & 3u) * 16u;
     }
-    int32_t tok = -1;  // lane l: the token of row l & 15, -1 for padding
-    {
-      const unsigned long long emask = s_mask[e];
-      const uint32_t j = 16u * k + (lane & 15u);
-      if (j < (uint32_t)__popcll(emask)) tok = (int32_t)nth_bit(emask, j);
-    }
     const uint32_t c0 = (grp * CA + ca) * P;  // this wave's first 16-column item within the tile's I / 16
     const uint32_t rot = item % NA;
     auto issue = [&](GateUpStep<kCH>& st, uint32_t s) __attribute__((always_inline)) { issue_at(st, e, item, s); };
-    // steps 0 and (NS > 1) 1 issued: in the prologue (narrow, first item) or now
-    const bool pre = kStageAll && item == blockIdx.x && e == e_pre;
+    // steps 0 and (NS > 1) 1 issued: in the prologue (narrow: the first
+    // item; wide: round 0, x rows staged too) or now
+    const bool pre = kStageAll ? item == blockIdx.x && e == e_pre : base == 0u;
     if (!pre) {
       issue(b0, 0u);
       if constexpr (NS == 2) issue(b1, 1u);
     }
-    // wide: stage the tile's x rows (padding rows zero) and scales
-    if constexpr (!kStageAll) {
-    constexpr uint32_t kPieces = H / kThreads, kScales = (16u * KB + kThreads - 1u) / kThreads;
-    uint4 av[kPieces];
-#pragma unroll
-    for (uint32_t q = 0; q < kPieces; ++q) {
-      const uint32_t pc = tid + q * kThreads, row = pc / (H / 16u), kk = (pc % (H / 16u)) * 16u;
-      const int32_t t = __shfl(tok, row);
-      av[q] = t >= 0 ? *reinterpret_cast<const uint4*>(xq + (size_t)t * H + kk) : make_uint4(0u, 0u, 0u, 0u);
-    }
-    float xv[kScales];
-#pragma unroll
-    for (uint32_t q = 0; q < kScales; ++q) {
-      const uint32_t i = tid + q * kThreads;
-      const int32_t t = __shfl(tok, (i / KB) & 15u);
-      xv[q] = (i < 16u * KB && t >= 0) ? xs[(size_t)t * KB + i % KB] : 0.0f;
-    }
-#pragma unroll
-    for (uint32_t q = 0; q < kPieces; ++q) {
-      const uint32_t pc = tid + q * kThreads, row = pc / (H / 16u), kk = (pc % (H / 16u)) * 16u;
-      const uint32_t kb = kk >> 7, k7 = kk & 127u;
-      *reinterpret_cast<uint4*>(&s_a[kb * 2048u + ((k7 >> 4) & 1u) * 1024u + ((k7 >> 5) * 16u + row) * 16u]) = av[q];
-    }
-#pragma unroll
-    for (uint32_t q = 0; q < kScales; ++q)
-      if (tid + q * kThreads < 16u * KB) {  // element i = row * KB + kb of the gather
-        const uint32_t i = tid + q * kThreads;
-        s_xs[(i % KB) * 16u + i / KB] = xv[q];
-      }
-    lds_barrier();
+    if (!kStageAll && !pre) {  // wide: stage the tile's x rows and scales
+      stage_load(e, k);
+      stage_store();
+      lds_barrier();
     }
 
     v4f ag = {0.0f, 0.0f, 0.0f, 0.0f}, au = {0.0f, 0.0f, 0.0f, 0.0f};

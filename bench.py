@@ -10,8 +10,11 @@ the queue kept full, 22.2 against 27.5 us per call at T = 1 and 135.8 against
 140.3 us at T = 64. The headline workload is BASELINE config 1 (decode, T=64,
 H=2048, 256 routed experts + 1 shared, top-8, I=512). Two copies of the expert
 weights alternate between steps so weights stream from HBM rather than the
-256 MB last-level cache. The same weights serve the T=1, T=512 (Zipf-skewed)
-and T=4096 configs, reported under "secondary".
+256 MB last-level cache (T=1, whose call touches only 9 experts, rotates 12
+address-distinct copies). The same weights serve the T=1, T=512 (Zipf-skewed)
+and T=4096 configs, reported under "secondary", each with its two GEMMs timed
+back to back on both rooflines (T=4096: a `roofline` object for gate/up against
+dense FP8).
 
 Prints ONE JSON line. Extra objects:
   roofline      the dominant kernel (gate/up) on its binding roofline (HBM),
@@ -61,6 +64,22 @@ def down_bytes(cfg, touched: int, path: str) -> int:
         return w + h + 2 * cfg.T * cfg.H
     part = (2 if path == "tile" else 4) * cfg.routes * cfg.H  # bf16 / fp32 route partials
     return w + h + part
+
+
+def gate_up_flops(cfg) -> int:
+    """Algorithmic FLOPs of one gate/up launch: 2 * 2I * H per route row."""
+    return 2 * cfg.routes * 2 * cfg.I * cfg.H
+
+
+def down_flops(cfg) -> int:
+    return 2 * cfg.routes * cfg.H * cfg.I
+
+
+# Weight copies a config rotates through, so that its weights come from HBM
+# and not from the 256 MB last-level cache: one T = 1 call touches 9 experts
+# (28.3 MB), so 12 copies (340 MB between reuses of a copy); the larger
+# configs touch 240 MB or more per call and alternate the 2 base copies.
+COLD_COPIES = {"decode_t1": 12}
 
 
 def time_layer(layers, steps: int, warmup: int, torch):
@@ -314,11 +333,25 @@ def main() -> int:
              for i in range(2)]
     torch.cuda.synchronize()
 
+    def copies_for(c):
+        """The weight sets a config rotates through: the 2 base copies, or for
+        configs that touch few experts per call, byte-identical clones of them
+        at other addresses (caches key on addresses; routing does not depend
+        on the expert weights)."""
+        n = COLD_COPIES.get(c.name, len(wsets))
+        out = []
+        for i in range(n):
+            base = wsets[i % len(wsets)]
+            out.append(base if i < len(wsets) else
+                       {k: v.clone() for k, v in base.items() if k in ("w13", "w13_scale", "w2", "w2_scale")})
+        return out
+
     def run_config(c, steps, warmup, with_kernels):
         act = W.synthetic_activations(c, "cpu")
+        sets = copies_for(c)
         layers = []
-        for ws in wsets:
-            w = {"router_w": act["router_w"].to(dev), "router_bias": act["router_bias"].to(dev), **ws}
+        for ws in sets:
+            w = {"router_w": act["router_w"].to(dev).clone(), "router_bias": act["router_bias"].to(dev), **ws}
             lay = MoELayer(c, w, expose=("topk_ids",), graph=args.launch == "graph")
             lay.x.copy_(act["x"].to(dev))
             layers.append(lay)
@@ -330,34 +363,36 @@ def main() -> int:
         res = {"T": c.T, "gemm_path": resolve_path(c), "ms_per_step": ms, "wall_ms_per_step": wall_ms,
                "tokens_per_s": c.T / (ms / 1e3), "tflops": flops / (ms / 1e3) / 1e12,
                "gbps": nbytes / (ms / 1e3) / 1e9, "touched_experts": touched,
-               "algorithmic_bytes": nbytes, "flops": flops}
+               "algorithmic_bytes": nbytes, "flops": flops, "weight_copies_rotated": len(sets)}
         res["hbm_frac"] = res["gbps"] / HBM_PEAK_GBPS
         res["mfma_frac"] = res["tflops"] / FP8_PEAK_TFLOPS
         kern = None
         if with_kernels:
             dl = []
-            for ws in wsets:
-                w = {"router_w": act["router_w"].to(dev), "router_bias": act["router_bias"].to(dev), **ws}
+            for ws in sets:
+                w = {"router_w": act["router_w"].to(dev).clone(), "router_bias": act["router_bias"].to(dev), **ws}
                 lay = MoELayer(c, w, graph=False)
                 lay.x.copy_(act["x"].to(dev))
                 dl.append(lay)
             kern = {op: ms * 1e3 for op, ms in time_operations(dl, max(50, steps // 2), torch).items()}  # us
             for lay in dl:
                 lay.close()
-            if c is cfg:  # the GEMMs' own durations, for the rooflines
-                from netra_moe.engine import tensor_table
-                inter = tuple(n for n, sp in tensor_table(c).items() if sp.role == "temporary")
-                xl = []
-                for ws in wsets:
-                    w = {"router_w": act["router_w"].to(dev), "router_bias": act["router_bias"].to(dev), **ws}
-                    lay = MoELayer(c, w, graph=False, expose=inter)
-                    lay.x.copy_(act["x"].to(dev))
-                    xl.append(lay)
-                kern["isolated"] = {op: time_isolated(xl, op, max(50, steps // 2), torch) * 1e3 for op in ISOLATED_OPS}
-                for lay in xl:
-                    lay.close()
+            # the GEMMs' own durations, for the rooflines
+            from netra_moe.engine import tensor_table
+            inter = tuple(n for n, sp in tensor_table(c).items() if sp.role == "temporary")
+            xl = []
+            for ws in sets:
+                w = {"router_w": act["router_w"].to(dev).clone(), "router_bias": act["router_bias"].to(dev), **ws}
+                lay = MoELayer(c, w, graph=False, expose=inter)
+                lay.x.copy_(act["x"].to(dev))
+                xl.append(lay)
+            kern["isolated"] = {op: time_isolated(xl, op, max(50, steps // 2), torch) * 1e3 for op in ISOLATED_OPS}
+            for lay in xl:
+                lay.close()
         for lay in layers:
             lay.close()
+        del sets
+        torch.cuda.empty_cache()
         return res, kern, act
 
     log(f"[bench] {cfg.name}: warmup {args.warmup}, steps {args.steps}")
@@ -376,13 +411,39 @@ def main() -> int:
             "box_copy_gbps": copy_gbps}
     roof["frac"] = roof["achieved"] / roof["peak"]
 
+    def gemm_rooflines(c, touched, iso):
+        """The two GEMMs of config c, timed back to back (HIP events on their
+        stream), on both rooflines: algorithmic FLOPs against dense FP8 and
+        algorithmic bytes against HBM."""
+        p = resolve_path(c)
+        syms = {op["name"]: op["symbol"] for op in operations(c, p)}
+        out = {}
+        for op, fl, by in (("gate_up", gate_up_flops(c), gate_up_bytes(c, touched, p)),
+                           ("down", down_flops(c), down_bytes(c, touched, p))):
+            us = iso[op]
+            out[op] = {"kernel": syms[f"moe.{op}"], "avg_us": us, "flops": fl, "bytes": by,
+                       "tflops": fl / (us * 1e-6) / 1e12, "gbps": by / (us * 1e-6) / 1e9}
+            out[op]["mfma_frac"] = out[op]["tflops"] / FP8_PEAK_TFLOPS
+            out[op]["hbm_frac"] = out[op]["gbps"] / HBM_PEAK_GBPS
+        return out
+
     secondary = {}
     for name in [s for s in args.secondary.split(",") if s]:
         c = BASELINE_CONFIGS[name]
         log(f"[bench] secondary {name}")
         # at least 50 timed steps and 10 warm-up steps, whatever --steps says
         res, kern_c, _ = run_config(c, max(50, args.steps), max(10, args.warmup), True)
+        iso_c = kern_c.pop("isolated")
         res["kernels_us"] = kern_c
+        res["gemms"] = gemm_rooflines(c, res["touched_experts"], iso_c)
+        if c.name == "prefill_t4096":  # the north star's MFMA bar: the dominant GEMM on dense FP8
+            g = res["gemms"]["gate_up"]
+            res["roofline"] = {"kernel": g["kernel"], "bound": "mfma", "achieved": g["tflops"],
+                               "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": g["mfma_frac"],
+                               "avg_us": g["avg_us"], "algorithmic_flops_per_launch": g["flops"],
+                               "hbm": {"achieved": g["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                                       "frac": g["hbm_frac"], "algorithmic_bytes_per_launch": g["bytes"]},
+                               "traffic": None}
         secondary[name] = res
 
     cpu = None
@@ -415,7 +476,8 @@ def main() -> int:
         "warmup": args.warmup, "ms_per_step": main_res["ms_per_step"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp8_e4m3", "data": "synthetic (seeded)",
         "config": {"workload": cfg.name, "T": cfg.T, "H": cfg.H, "E": cfg.E, "K": cfg.K, "S": cfg.S,
-                   "I": cfg.I, "block_m": 64, "weight_copies_rotated": 2, "launch": args.launch},
+                   "I": cfg.I, "block_m": 64, "weight_copies_rotated": main_res["weight_copies_rotated"],
+                   "launch": args.launch},
         "layer": main_res, "kernels_us": kern, "roofline": roof, "other_kernels": other,
         "cpu_baseline": cpu, "secondary": secondary,
     }

@@ -181,6 +181,109 @@ def cpu_baseline(cfg, act_cpu, w_host, threads: int, min_seconds: float):
                       f"fp64-accumulated C oracle, OpenMP), median of {len(runs)} runs, {med * 1e3:.1f} ms each"}
 
 
+# The reference's published isolated HIP-event medians for its per-operation
+# bridges on MI350X (docs/notes/gfx950-qwen36-fp8-kernels.md lines 78, 261,
+# 301, 563, 643), at the shapes they were quoted for. (Its SiLU-quant and
+# shared-gate notes also give kernel-trace figures: 2.742 us, line 80, and a
+# serving-trace median of 3.160 us, line 263.)
+REFERENCE_BRIDGE_US = {"router_m1": 6.24, "router_m16": 6.32, "shared_gate_m1": 5.96,
+                       "silu_mul_quant_m1": 2.78, "gate_up_m1": 8.96, "down_reduce_m1": 10.28}
+
+
+def bridge_timings(torch, dev, launches: int = 200, copies: int = 12) -> dict:
+    """Per-launch HIP-event medians of libnetra_bridges.so at the reference's
+    shapes (hidden 2048, 256 routed + 1 shared expert, top-8 + 1, intermediate
+    512; weights in the AITER 16x16 shuffle the reference's kernels read).
+    "hot" repeats one argument set, the reference's method; "cold" rotates
+    `copies` address-distinct copies of the weights the launch streams, so they
+    come from HBM and not the last-level cache."""
+    import ctypes
+
+    from netra_moe import bridges as B
+
+    H, E, I, K = 2048, 256, 512, 9
+    g = torch.Generator(device=dev).manual_seed(5)
+
+    def fp8(*shape):
+        return (torch.randn(shape, generator=g, device=dev) * 0.5).to(torch.float8_e4m3fn).view(torch.uint8)
+
+    def f32(*shape, scale=1e-3):
+        return torch.rand(shape, generator=g, device=dev) * scale + scale
+
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    w13, w13s = fp8(E + 1, 2 * I, H), f32(E + 1, 2 * I // 128, H // 128)
+    w2, w2s = fp8(E + 1, H, I), f32(E + 1, H // 128, I // 128)
+    router = (torch.randn((E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    shared_w = (torch.randn((1, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    x = torch.randn((16, H), generator=g, device=dev).to(torch.bfloat16)
+    xq, xs = fp8(16, H), f32(16, H // 128, scale=1e-2)
+    ids = torch.stack([torch.randperm(E, generator=g, device=dev)[:K - 1] for _ in range(16)]).to(torch.int32)
+    ids9 = torch.cat([ids, torch.full((16, 1), E, dtype=torch.int32, device=dev)], 1).contiguous()
+    wts9 = torch.softmax(torch.rand((16, K), generator=g, device=dev), 1).contiguous()
+    wts8 = wts9[:, :K - 1].contiguous()
+    logits = torch.empty((16, E), dtype=torch.bfloat16, device=dev)
+    out_ids = torch.empty((16, K), dtype=torch.int32, device=dev)
+    out_w = torch.empty((16, K), dtype=torch.float32, device=dev)
+    gu = torch.randn((K * 16, 2 * I), generator=g, device=dev)
+    hq, hs = torch.empty((K * 16, I), dtype=torch.uint8, device=dev), torch.empty((K * 16, I // 128), device=dev)
+    hq.copy_(fp8(K * 16, I))
+    out = torch.empty((16, H), dtype=torch.bfloat16, device=dev)
+    hot_w = [(w13, w13s, w2, w2s)]
+    cold_w = hot_w + [(w13.clone(), w13s.clone(), w2.clone(), w2s.clone()) for _ in range(copies - 1)]
+    torch.cuda.synchronize()
+
+    def batch_us(fn, sets):
+        """Per-launch GPU time of `launches` back-to-back launches, queued behind
+        a GPU sleep so the host's launch latency is not timed (an event pair
+        around every launch costs ~6 us on its own at this size)."""
+        for i in range(10):
+            fn(sets[i % len(sets)])
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(50_000_000)
+        a.record()
+        for i in range(launches):
+            fn(sets[i % len(sets)])
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / launches
+
+    cases = {
+        "router_m1": ("netra_qwen36_router_bf16", lambda w: B.launch("netra_qwen36_router_bf16", P(logits), P(x),
+                                                                     P(router), 1, stream), False),
+        "router_m16": ("netra_qwen36_router_bf16", lambda w: B.launch("netra_qwen36_router_bf16", P(logits), P(x),
+                                                                      P(router), 16, stream), False),
+        "shared_gate_m1": ("netra_qwen36_shared_gate_append",
+                           lambda w: B.launch("netra_qwen36_shared_gate_append", P(out_ids), P(out_w), P(x),
+                                              P(shared_w), P(ids), P(wts8), 1, stream), False),
+        "silu_mul_quant_m1": ("netra_qwen36_moe_silu_mul_quant",
+                              lambda w: B.launch("netra_qwen36_moe_silu_mul_quant", P(gu), P(hq), P(hs), K, stream),
+                              False),
+        "gate_up_m1": ("netra_qwen36_moe_gate_up",
+                       lambda w: B.launch("netra_qwen36_moe_gate_up", P(xq), P(xs), P(w[0]), P(w[1]), P(ids9), P(gu),
+                                          1, stream), True),
+        "down_reduce_m1": ("netra_qwen36_moe_down_reduce",
+                           lambda w: B.launch("netra_qwen36_moe_down_reduce", P(hq), P(hs), P(w[2]), P(w[3]),
+                                              P(wts9), P(ids9), P(out), 1, stream), True),
+    }
+    res = {}
+    for name, (fam, fn, streams_weights) in cases.items():
+        B.check(fam, B.load(fam))
+        r = {"hot_us": batch_us(fn, hot_w), "reference_mi350x_us": REFERENCE_BRIDGE_US[name]}
+        if streams_weights:
+            r["cold_us"] = batch_us(fn, cold_w)
+        B.check(fam, B.unload(fam))
+        res[name] = r
+    res["method"] = (f"HIP events around {launches} back-to-back launches (after 10 warm-up launches), queued "
+                     f"behind a GPU sleep so no host gap is timed, per launch (kernel plus the gap to the next); "
+                     f"hot: one argument set (the reference's method); cold: {copies} address-distinct weight "
+                     f"copies rotated. Kernel-only durations: profiles/bridges_kernel_stats.md")
+    del cold_w
+    torch.cuda.empty_cache()
+    return res
+
+
 COPY_BYTES = 1 << 30
 PMC_REPS = 6
 
@@ -298,6 +401,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc passes that measure the dominant kernel's HBM bytes")
+    ap.add_argument("--no-bridges", action="store_true", help="skip timing the per-operation bridges")
+    ap.add_argument("--bridges-only", action="store_true",
+                    help="time only the per-operation bridges (one JSON line), e.g. under a kernel trace")
     ap.add_argument("--launch", choices=("eager", "graph"), default="eager",
                     help="dispatch each layer call's kernels directly, or replay the engine's HIP graph")
     ap.add_argument("--pmc-workload", action="store_true", help=argparse.SUPPRESS)
@@ -309,6 +415,12 @@ def main() -> int:
         return 2
     if args.pmc_workload:
         return pmc_workload(args.config)
+    if args.bridges_only:
+        import torch
+        dev = torch.device("cuda", 0)
+        torch.cuda.set_device(dev)
+        print(json.dumps({"bridges": bridge_timings(torch, dev)}), flush=True)
+        return 0
 
     import numpy as np
     import torch
@@ -446,6 +558,11 @@ def main() -> int:
                                "traffic": None}
         secondary[name] = res
 
+    bridges = None
+    if not args.no_bridges:
+        log("[bench] per-operation bridges")
+        bridges = bridge_timings(torch, dev)
+
     cpu = None
     if not args.no_cpu_baseline:
         # the GPU box grants one GPU's share of its host: 16 threads at most,
@@ -479,7 +596,7 @@ def main() -> int:
                    "I": cfg.I, "block_m": 64, "weight_copies_rotated": main_res["weight_copies_rotated"],
                    "launch": args.launch},
         "layer": main_res, "kernels_us": kern, "roofline": roof, "other_kernels": other,
-        "cpu_baseline": cpu, "secondary": secondary,
+        "cpu_baseline": cpu, "secondary": secondary, "bridges": bridges,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -247,7 +247,7 @@ extern "C" int netra_qwen36_moe_silu_mul_quant_launch(const float* input_f32, vo
   const float* in = input_f32;
   uint32_t n = static_cast<uint32_t>(rows), I = kInter;
   void* args[] = {&in, &output_fp8, &output_scale_f32, &n, &I};
-  const int rc = dispatch(f, 0, dim3(n), dim3(64), args, stream);
+  const int rc = dispatch(f, 0, dim3(n), dim3(256), args, stream);  // four waves per row
   return rc ? rc : ok(f);
 }
 

@@ -162,39 +162,32 @@ __device__ __forceinline__ void gate_up_route(const uint8_t* __restrict__ xq, co
 // qwen36_moe_silu_mul_quant_bridge.h:14-29; rule harness/gfx950/fp8/moe/
 // decode/qwen36_moe_silu_mul_quant_fp8_gfx950.hip:41-94).
 //
-// One wave per row of [g (I values) | u (I values)]: h = bf16(silu(g) * u)
-// with the contract exp, amax per 128 columns (floor 1e-10),
-// scale = amax * 0x3b124925, q = e4m3(h * (1 / scale)). Lane l holds eight
-// consecutive columns of each 512-column chunk.
+// Four waves per row of [g (I values) | u (I values)]: h = bf16(silu(g) * u)
+// with the contract exp, amax per 128 columns (floor 1e-10), scale = amax *
+// 0x3b124925, q = e4m3(h * (1 / scale)). Wave w takes 128-column blocks w,
+// w + 4, ..; lane l two consecutive columns of a block, so a block's amax is
+// one wave reduction and each lane evaluates two SiLUs (the per-value
+// arithmetic does not depend on the mapping).
+constexpr uint32_t kSiluWaves = 4;
 __device__ __forceinline__ void silu_mul_quant(const float* __restrict__ in, uint8_t* __restrict__ q,
                                                float* __restrict__ s, uint32_t rows, uint32_t I) {
-  const uint32_t row = blockIdx.x, lane = threadIdx.x;
+  const uint32_t row = blockIdx.x, lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   if (row >= rows) return;
   const float* g = in + (size_t)row * 2u * I;
   const float* u = g + I;
-  for (uint32_t n0 = lane * 8u; n0 < I; n0 += 512u) {
-    const float4 g0 = *reinterpret_cast<const float4*>(g + n0), g1 = *reinterpret_cast<const float4*>(g + n0 + 4u);
-    const float4 u0 = *reinterpret_cast<const float4*>(u + n0), u1 = *reinterpret_cast<const float4*>(u + n0 + 4u);
-    const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-    const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-    float h[8];
-    float amax = nk::kAmaxFloor;
+  for (uint32_t blk = wave; blk < I / 128u; blk += kSiluWaves) {
+    const uint32_t n0 = blk * 128u + lane * 2u;
+    const float2 gv = *reinterpret_cast<const float2*>(g + n0), uv = *reinterpret_cast<const float2*>(u + n0);
+    const float h0 = nk::bf16_f32(nk::bf16_rne(nk::silu(gv.x) * uv.x));
+    const float h1 = nk::bf16_f32(nk::bf16_rne(nk::silu(gv.y) * uv.y));
+    float amax = fmaxf(nk::kAmaxFloor, fmaxf(fabsf(h0), fabsf(h1)));
 #pragma unroll
-    for (uint32_t i = 0; i < 8; ++i) {
-      h[i] = nk::bf16_f32(nk::bf16_rne(nk::silu(gv[i]) * uv[i]));
-      amax = fmaxf(amax, fabsf(h[i]));
-    }
-    amax = fmaxf(amax, __shfl_xor(amax, 1u));
-    amax = fmaxf(amax, __shfl_xor(amax, 2u));
-    amax = fmaxf(amax, __shfl_xor(amax, 4u));
-    amax = fmaxf(amax, __shfl_xor(amax, 8u));
+    for (uint32_t m = 1; m < 64u; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
     const float scale = amax * nk::inv_e4m3_max();
     const float inv = 1.0f / scale;
-    uint2 qv;
-    qv.x = nk::e4m3x4(h[0] * inv, h[1] * inv, h[2] * inv, h[3] * inv);
-    qv.y = nk::e4m3x4(h[4] * inv, h[5] * inv, h[6] * inv, h[7] * inv);
-    *reinterpret_cast<uint2*>(q + (size_t)row * I + n0) = qv;
-    if ((lane & 15u) == 0u) s[(size_t)row * (I / 128u) + (n0 >> 7)] = scale;
+    const uint32_t qq = nk::e4m3x4(h0 * inv, h1 * inv, 0.0f, 0.0f);
+    *reinterpret_cast<uint16_t*>(q + (size_t)row * I + n0) = (uint16_t)(qq & 0xffffu);
+    if (lane == 0u) s[(size_t)row * (I / 128u) + blk] = scale;
   }
 }
 
@@ -350,7 +343,7 @@ NK_SHARED_GATE_APPEND(2048)
   }
 NK_GATE_UP_ROUTE(2048)
 
-NK_KERNEL __launch_bounds__(64) void netra_moe_silu_mul_quant_gfx950(const float* __restrict__ in,
+NK_KERNEL __launch_bounds__(256) void netra_moe_silu_mul_quant_gfx950(const float* __restrict__ in,
                                                                      uint8_t* __restrict__ q,
                                                                      float* __restrict__ s, uint32_t rows,
                                                                      uint32_t I) {

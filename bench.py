@@ -97,26 +97,39 @@ def time_layer(layers, steps: int, warmup: int, torch):
     return start.elapsed_time(end) / steps, wall * 1e3 / steps
 
 
+# GPU sleep queued ahead of timed launches, in GPU clock cycles per eight
+# launches: longer than the host takes to launch them.
+QUEUE_AHEAD_CYCLES = 2_500_000
+
+
 def time_operations(layers, steps: int, torch) -> dict[str, float]:
-    """Average duration (ms) of every operation of a layer call, from HIP events
-    recorded between the operations of whole eager layer calls on the stream
-    they are launched on (torch's current stream). Operations always run in
-    order: their inputs are the previous operations' outputs, and the packed
-    workspace lets a later operation's tensors reuse an earlier one's bytes,
-    so an operation launched on its own would read stale data."""
+    """Marginal GPU time (ms) of every operation of a layer call: the average
+    time of `steps` back-to-back eager calls truncated after operation k,
+    minus the same for the calls truncated before it, so the figures add up
+    to the eager call's time. A truncated call is a valid layer prefix (an
+    operation reads only the layer's inputs and the outputs of earlier
+    operations of the same call). The launches are queued behind a GPU sleep,
+    so the host's launch rate, which exceeds the duration of the short
+    routing kernels, is not timed; and no event is recorded between two
+    operations (an event between kernels costs GPU time of its own, largest
+    after kernels that leave much written data in the L2 caches)."""
     names = layers[0].op_names
     for lay in layers:
         lay.forward()
     torch.cuda.synchronize()
-    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(steps)]
-    for i in range(steps):
-        lay = layers[i % len(layers)]
-        marks[i][0].record()
-        for j, op in enumerate(names):
-            lay.run_operation(op)
-            marks[i][j + 1].record()
-    torch.cuda.synchronize()
-    return {op: sum(m[j].elapsed_time(m[j + 1]) for m in marks) / steps for j, op in enumerate(names)}
+    prefix = [0.0]
+    for k in range(1, len(names) + 1):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(QUEUE_AHEAD_CYCLES * max(1, steps * k // 8))
+        start.record()
+        for i in range(steps):
+            lay = layers[i % len(layers)]
+            for op in names[:k]:
+                lay.run_operation(op)
+        end.record()
+        torch.cuda.synchronize()
+        prefix.append(start.elapsed_time(end) / steps)
+    return {op: prefix[j + 1] - prefix[j] for j, op in enumerate(names)}
 
 
 # Operations that are pure functions of other operations' outputs (nothing
@@ -138,6 +151,7 @@ def time_isolated(layers, op: str, steps: int, torch) -> float:
     for i in range(4):
         layers[i % len(layers)].run_operation(op)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(QUEUE_AHEAD_CYCLES * max(1, steps // 8))  # queue the launches ahead of the GPU
     start.record()
     for i in range(steps):
         layers[i % len(layers)].run_operation(op)

@@ -33,18 +33,19 @@
 //       B = Etot*W + 4*Etot + 51 + CAP rounded up to even
 //   prefill ("screen") front end, H in {512,1024,2048}, EMAX in {256,512}:
 //   netra_moe_route_screen_h<H>_k<KBS>_gfx950(x, w, screen f32[Z,T,RP],
-//       wsq f32[Z,RP]; T, H, E, RP)   grid (ceil(T/128), ceil(RP/128), Z), block 256,
+//       wsq f32[Z,RP], slices i32[Etot*8]; Etot*8, T, H, E, RP)
+//       grid (ceil(T/128), ceil(RP/128), Z), block 256,
 //       RP = E rounded up to 64 (the shared-gate row is not screened), Z = H/128/KBS
 //       K splits (KBS in {2,4,8,16}, at most H/128); workgroups with
-//       blockIdx.x == 0 write the partial squared router-row norms wsq
+//       blockIdx.x == 0 write the partial squared router-row norms wsq, and
+//       workgroup (0,0,0) clears slices
 //   netra_moe_route_select_h<H>_e<EMAX>_w<W>_gfx950(x, w, bias, screen, wsq, logits,
-//       ids, weights, xq, xs, route_base i32[Etot,G], route_rank i32[T*Ktot];
-//       T, H, E, K, S, RP, Z)   grid G = ceil(T/W), block 64*W, W in {4,8}
-//       (one token per wave)
-//   netra_moe_sort_count_gfx950(route_base, counts; G, Etot)   grid Etot, block 256
-//   netra_moe_sort_place_gfx950(ids, route_base, route_rank, counts, sorted_ids,
+//       ids, weights, xq, xs, hist i32[Etot,G], bucket i32[Etot,G,W], slices i32[Etot,8];
+//       T, H, E, K, S, RP, Z, G)   grid G = ceil(T/W), block 64*W, W in {4,8}
+//       (one token per wave); slices must hold zeros (route_screen clears them)
+//   netra_moe_sort_route_gfx950(hist, bucket, slices, counts, sorted_ids,
 //       sorted_expert, tile_map, pair_map, num_valid; T, Ktot, Etot, G, W, CAP)
-//       grid max(ceil(T*Ktot/256), ceil(Etot/4)), block 256, dynamic LDS 4*(4*Etot+3)
+//       grid exactly Etot, block 256, dynamic LDS 4*(4*Etot+3)
 //   fused decode FFN (T <= 64), (H, I) in {(512,256), (1024,1024), (2048,512), (4096,256)}:
 //   netra_moe_ffn_gate_up_h<H>_i<I>_<wide|narrow>_gfx950(logits, bias, ids, weights,
 //       xq, xs, w13, w13s, sorted_ids, sorted_expert, tile_map, pair_map, num_valid,

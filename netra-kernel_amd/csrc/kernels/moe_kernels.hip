@@ -4,7 +4,7 @@
 // Layer pipeline, one engine operation per kernel, fixed grids with
 // device-side early exit so a whole layer call is one capturable HIP graph:
 //   front end, exact:  router (logits + input quant) -> topk -> sort
-//   front end, screen: route_screen -> route_select -> sort_count -> sort_place
+//   front end, screen: route_screen -> route_select -> sort_route
 //   then gate_up_{stream|lds|tile} -> down_{stream|tile} -> combine
 // Every kernel takes plain pointers followed by u32 shape constants, in the
 // order documented in include/netra_moe.h. moe_bridge_kernels.hip adds the

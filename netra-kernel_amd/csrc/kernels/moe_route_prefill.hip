@@ -1,4 +1,4 @@
-// Routing front end for large token counts (prefill, T > 256), four kernels:
+// Routing front end for large token counts (prefill, T > 256), three kernels:
 //   route_screen  bf16-MFMA router GEMM over all tokens and router rows, K
 //                 split for small T: partial sums of the approximate logit a,
 //                 and partial squared norms of the router rows
@@ -6,13 +6,13 @@
 //                 the bound m = 2^-10 ||x|| ||w|| on |L - a| (Cauchy-Schwarz),
 //                 exact contract logits of the candidates and the shared-gate
 //                 row, top-k + weights + shared-expert append, input quant,
-//                 logits out; per workgroup expert histogram and the
-//                 in-workgroup rank of every route
-//   sort_count    per expert (one workgroup each): prefix sums of its
-//                 histogram row over the route_select workgroups, and its total
-//   sort_place    expert layout (64-row blocks, padding, tile and pair lists)
-//                 rebuilt by every workgroup from the totals; sorted ids =
-//                 block base + prefix + in-workgroup rank
+//                 logits out; per workgroup: expert histogram, every route's
+//                 sorted-id entry in an (expert, workgroup) bucket, and the
+//                 expert totals added into slice counters
+//   sort_route    one workgroup per expert: the expert layout (64-row blocks,
+//                 padding, tile and pair lists) from the totals, the expert's
+//                 prefix over the route_select workgroups, and its routes
+//                 copied from the buckets into their sorted rows
 // The results equal those of the exact front end (moe_router.hip): top-k ids,
 // weights, counts and the sorted layout are the same bits. Logits of the
 // experts that were not candidates are the screen's values rounded to bf16.
@@ -33,6 +33,11 @@ constexpr uint32_t kMaxSlots = 64;  // K + S <= 64 (and the K selected slots fit
 // 2^-10 leaves a factor > 3, and the norms are rounded up by (1 + 2^-9).
 constexpr float kScreenMargin = 0.0009765625f;
 constexpr float kNormSlack = 1.001953125f;
+// route_select adds each expert's per-workgroup count into one of kSlices
+// counters of that expert (slice = workgroup index mod kSlices), which spreads
+// the atomic adds of many workgroups over more addresses; sort_route sums the
+// slices. route_screen clears them (route_select runs after it).
+constexpr uint32_t kSlices = 8;
 
 __device__ __forceinline__ nk::v4f mfma_bf16(uint4 a, uint4 b, nk::v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
@@ -67,11 +72,11 @@ __device__ __forceinline__ void quant8(uint4 v, uint8_t* __restrict__ q_dst, flo
   amax = fmaxf(amax, __shfl_xor(amax, 8u));
   const float scale = amax * nk::inv_e4m3_max();
   const float inv = 1.0f / scale;
-  uint2 q;
-  q.x = nk::e4m3x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv);
-  q.y = nk::e4m3x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv);
-  *reinterpret_cast<uint2*>(q_dst) = q;
-  if (first_lane) *s_dst = scale;
+  const nk::u32x2 q = {nk::e4m3x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv),
+                       nk::e4m3x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv)};
+  // non-temporal: written here, read by the gate/up GEMM two kernels later
+  __builtin_nontemporal_store(q, reinterpret_cast<nk::u32x2*>(q_dst));
+  if (first_lane) __builtin_nontemporal_store(scale, s_dst);
 }
 
 // Exact contract logit of one (token, router row) pair by a 16-lane group:
@@ -127,11 +132,13 @@ __device__ __forceinline__ float exact_dot(const float4* __restrict__ xrow, cons
 // stride RP; the select kernel adds the splits in z order. The engine screens
 // the E expert rows only (rows = E): the shared-gate row's logit is always
 // computed exactly by route_select. The workgroups of the first token tile
-// also write the rows' partial squared norms wsq[z][e]. Needs T H < 2^30 (the
-// buffer offsets are 32-bit).
+// also write the rows' partial squared norms wsq[z][e]. Workgroup (0, 0, 0)
+// clears route_select's slice counters cslice[0 .. nslice). Needs T H < 2^30
+// (the buffer offsets are 32-bit).
 template <uint32_t NJ, uint32_t KBS>  // H / 128, K blocks per split
 __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                              float* __restrict__ screen, float* __restrict__ wsq,
+                                             int32_t* __restrict__ cslice, uint32_t nslice,
                                              uint32_t T, uint32_t rows, uint32_t RP) {
   constexpr uint32_t H = 128u * NJ;
   constexpr uint32_t kTile = 128u * 128u;  // bytes of one 128 x 64 bf16 tile
@@ -145,6 +152,8 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
   const bool norms = blockIdx.x == 0;  // uniform
   const uint32_t t0 = blockIdx.x * 128u, r0 = blockIdx.y * 128u, z = blockIdx.z, kb0 = z * KBS;
+  if (norms && blockIdx.y == 0 && z == 0)
+    for (uint32_t i = tid; i < nslice; i += 256u) cslice[i] = 0;
   auto swz = [](uint32_t r) { return (r >> 1) & 7u; };
   // copy c of this wave moves tile rows 32 wave + 8 c .. + 7; lane l fetches
   // the chunk that position l & 7 of row 32 wave + 8 c + (l >> 3) holds
@@ -225,9 +234,8 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j) {
       const uint32_t t = t0 + ntok + 16u * j + rl;
-      if (t < T && e0 < RP)
-        *reinterpret_cast<float4*>(screen + ((size_t)z * T + t) * RP + e0) =
-            make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      if (t < T && e0 < RP)  // non-temporal: read once, by route_select
+        __builtin_nontemporal_store(acc[i][j], reinterpret_cast<nk::v4f*>(screen + ((size_t)z * T + t) * RP + e0));
     }
   }
 }
@@ -246,18 +254,20 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
 //  3. top-K over the candidates' exact z (descending, ties to the lower expert
 //     index), weights, shared expert append (as the exact top-k kernel);
 //  4. logits row;
-//  5. per workgroup g: in-workgroup rank of every route among the workgroup's
-//     routes to the same expert (token order), and the per-expert histogram
-//     hist[e][g] (expert-major, so each expert's counts are contiguous for
-//     the sort's per-expert scan).
+//  5. per workgroup g (of G): the per-expert histogram hist[e][g]
+//     (expert-major, so each expert's counts are contiguous for the sort's
+//     per-expert scan); the sorted-id entry (slot << 24) | token of every
+//     route, at bucket[e][g][rank], rank = the route's position among the
+//     workgroup's routes to e in token order; and the nonzero counts added
+//     into cslice[e][g mod kSlices].
 template <uint32_t NJ, uint32_t EMAX, uint32_t W>
 __device__ __forceinline__ void route_select(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
     const float* __restrict__ screen, const float* __restrict__ wsq, uint16_t* __restrict__ logits,
     int32_t* __restrict__ ids,
     float* __restrict__ weights, uint8_t* __restrict__ xq, float* __restrict__ xs,
-    int32_t* __restrict__ hist, int32_t* __restrict__ lrank, uint32_t T, uint32_t E, uint32_t K,
-    uint32_t S, uint32_t RP, uint32_t Z) {
+    int32_t* __restrict__ hist, int32_t* __restrict__ bucket, int32_t* __restrict__ cslice, uint32_t T,
+    uint32_t E, uint32_t K, uint32_t S, uint32_t RP, uint32_t Z, uint32_t G) {
   constexpr uint32_t H = 128u * NJ;
   constexpr uint32_t P = EMAX / 64u;  // experts per lane
   static_assert(EMAX % 64u == 0 && P <= 8u && W <= 32u, "shape");
@@ -498,24 +508,31 @@ __device__ __forceinline__ void route_select(
 #pragma unroll
     for (uint32_t j = 0; j < P; ++j) {
       const uint32_t e = lane + 64u * j;
-      if (e < E) lrow[e] = pos[j] != 0xffffffffu ? s_exact[tt][pos[j]] : nk::bf16_rne(aval[j]);
+      if (e < E)  // non-temporal: no later kernel of the layer reads the logits
+        __builtin_nontemporal_store(pos[j] != 0xffffffffu ? s_exact[tt][pos[j]] : nk::bf16_rne(aval[j]), lrow + e);
     }
-    if (S != 0u && lane == 0) lrow[E] = s_exact[tt][n];
+    if (S != 0u && lane == 0) __builtin_nontemporal_store(s_exact[tt][n], lrow + E);
   }
   __syncthreads();
 
-  // 5. in-workgroup ranks and histogram from the per-expert token masks (a
-  // token routes to an expert at most once): the rank of token tk's route to
-  // e is the number of earlier tokens in e's mask
+  // 5. buckets and histogram from the per-expert token masks (a token routes
+  // to an expert at most once): the rank of token tk's route to e is the
+  // number of earlier tokens in e's mask
   const uint32_t t0 = blockIdx.x * W;
   for (uint32_t r = tid; r < W * Ktot; r += kThreads) {
     const uint32_t tk = r / Ktot, sl = r - tk * Ktot;
     if (t0 + tk >= T) break;
-    const uint32_t bits = s_hist[s_ids[tk][sl]];
-    lrank[(size_t)(t0 + tk) * Ktot + sl] = __popc(bits & ((1u << tk) - 1u));
+    const uint32_t e = (uint32_t)s_ids[tk][sl];
+    const uint32_t rank = __popc(s_hist[e] & ((1u << tk) - 1u));
+    bucket[((size_t)e * G + blockIdx.x) * W + rank] = (int32_t)((sl << 24) | (t0 + tk));
   }
-  for (uint32_t e = tid; e < rows; e += kThreads)
-    hist[(size_t)e * gridDim.x + blockIdx.x] = __popc(s_hist[e]);
+  for (uint32_t e = tid; e < rows; e += kThreads) {
+    const uint32_t c = __popc(s_hist[e]);
+    hist[(size_t)e * G + blockIdx.x] = (int32_t)c;
+    if (c != 0u)
+      __hip_atomic_fetch_add(&cslice[e * kSlices + (blockIdx.x & (kSlices - 1u))], (int32_t)c, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 }  // namespace nkroute
@@ -523,9 +540,10 @@ __device__ __forceinline__ void route_select(
 #define NK_ROUTE_SCREEN(HV, KBS)                                                                  \
   NK_KERNEL __launch_bounds__(256) void netra_moe_route_screen_h##HV##_k##KBS##_gfx950(           \
       const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, float* __restrict__ screen,  \
-      float* __restrict__ wsq, uint32_t T, uint32_t H, uint32_t rows, uint32_t RP) {              \
+      float* __restrict__ wsq, int32_t* __restrict__ cslice, uint32_t nslice, uint32_t T,         \
+      uint32_t H, uint32_t rows, uint32_t RP) {                                                   \
     (void)H;                                                                                      \
-    nkroute::route_screen<HV / 128, KBS>(x, w, screen, wsq, T, rows, RP);                         \
+    nkroute::route_screen<HV / 128, KBS>(x, w, screen, wsq, cslice, nslice, T, rows, RP);         \
   }
 NK_ROUTE_SCREEN(512, 2)
 NK_ROUTE_SCREEN(512, 4)
@@ -544,11 +562,12 @@ NK_ROUTE_SCREEN(2048, 16)
       const float* __restrict__ bias, const float* __restrict__ screen,                           \
       const float* __restrict__ wsq, uint16_t* __restrict__ logits, int32_t* __restrict__ ids,    \
       float* __restrict__ weights, uint8_t* __restrict__ xq, float* __restrict__ xs,              \
-      int32_t* __restrict__ hist, int32_t* __restrict__ lrank, uint32_t T, uint32_t H, uint32_t E, \
-      uint32_t K, uint32_t S, uint32_t RP, uint32_t Z) {                                          \
+      int32_t* __restrict__ hist, int32_t* __restrict__ bucket, int32_t* __restrict__ cslice,     \
+      uint32_t T, uint32_t H, uint32_t E, uint32_t K, uint32_t S, uint32_t RP, uint32_t Z,        \
+      uint32_t G) {                                                                               \
     (void)H;                                                                                      \
     nkroute::route_select<HV / 128, EMAXV, WV>(x, w, bias, screen, wsq, logits, ids, weights,     \
-                                               xq, xs, hist, lrank, T, E, K, S, RP, Z);           \
+                                               xq, xs, hist, bucket, cslice, T, E, K, S, RP, Z, G); \
   }
 #define NK_ROUTE_SELECT_W(HV, EMAXV) NK_ROUTE_SELECT(HV, EMAXV, 4) NK_ROUTE_SELECT(HV, EMAXV, 8)
 NK_ROUTE_SELECT_W(512, 256)
@@ -559,84 +578,64 @@ NK_ROUTE_SELECT_W(1024, 512)
 NK_ROUTE_SELECT_W(2048, 512)
 
 // ---------------------------------------------------------------------------
-// sort_count: workgroup e (256 threads) turns expert e's histogram row
-// hist[e][0 .. G) (G route_select workgroups) into exclusive prefix sums in
-// place, i.e. the rows of expert e that precede each workgroup's routes, and
-// writes counts[e], the expert's total.
-NK_KERNEL __launch_bounds__(256) void netra_moe_sort_count_gfx950(
-    int32_t* __restrict__ hist, int32_t* __restrict__ counts, uint32_t G, uint32_t Etot) {
-  __shared__ uint32_t s_wave[4];
-  const uint32_t e = blockIdx.x;
-  if (e >= Etot) return;
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  int32_t* row = hist + (size_t)e * G;
-  uint32_t carry = 0u;
-  for (uint32_t g0 = 0; g0 < G; g0 += 256u) {  // uniform trip count
-    const uint32_t g = g0 + tid;
-    const uint32_t v = g < G ? (uint32_t)row[g] : 0u;
-    uint32_t inc = v;
-#pragma unroll
-    for (uint32_t off = 1; off < 64u; off <<= 1) {
-      const uint32_t o = __shfl_up(inc, off);
-      if (lane >= off) inc += o;
-    }
-    if (lane == 63u) s_wave[wave] = inc;
-    __syncthreads();
-    uint32_t before = carry, total = 0u;
-#pragma unroll
-    for (uint32_t w = 0; w < 4u; ++w) {
-      const uint32_t x = s_wave[w];
-      before += w < wave ? x : 0u;
-      total += x;
-    }
-    if (g < G) row[g] = (int32_t)(before + inc - v);
-    carry += total;
-    __syncthreads();  // s_wave is rewritten by the next round
-  }
-  if (tid == 0) counts[e] = (int32_t)carry;
-}
-
-// sort_place: every workgroup rebuilds the expert layout from counts (experts
-// in order get ceil(count / 64) blocks, ceil(count / 16) 16-row tiles and
-// ceil(blocks / 2) block pairs: an exclusive scan over the experts, each
-// thread summing a contiguous run of them), then
-//  - scatters its 256 routes: route r = (t, s) of expert e lands at row
-//    block_off[e] * 64 + base[e][t / W] + lrank[r], written as (s << 24) | t;
-//  - one expert per wave (e = 4 blockIdx.x + wave, + 4 gridDim.x, ...):
-//    sorted_expert of its blocks, its tile_map and pair_map entries, and its
-//    padding rows (Ktot << 24) | T after its routes;
-//  - a grid-stride share of the unused blocks: sorted_expert -1, every row
-//    padding;
-//  - workgroup 0: num_valid = {padded rows, routes, tiles, pairs}.
-// Grid max(ceil(T * Ktot / 256), ceil(Etot / 4)) x 256 threads; dynamic LDS
-// 4 * (4 * Etot + 3) bytes.
-NK_KERNEL __launch_bounds__(256) void netra_moe_sort_place_gfx950(
-    const int32_t* __restrict__ ids, const int32_t* __restrict__ base, const int32_t* __restrict__ lrank,
-    const int32_t* __restrict__ counts, int32_t* __restrict__ sorted_ids,
-    int32_t* __restrict__ sorted_expert, int32_t* __restrict__ tile_map, int32_t* __restrict__ pair_map,
-    int32_t* __restrict__ num_valid, uint32_t T, uint32_t Ktot, uint32_t Etot, uint32_t G, uint32_t W,
-    uint32_t cap_blocks) {
+// sort_route: workgroup me (256 threads) of a grid of exactly Etot, one per
+// expert:
+//  a. every expert's total = the sum of its kSlices slice counters, and the
+//     expert layout from the totals (every workgroup computes the same one):
+//     experts in order get ceil(count / 64) 64-row blocks, ceil(count / 16)
+//     16-row tiles and ceil(blocks / 2) block pairs, an exclusive scan over
+//     the experts with each thread summing a contiguous run of them;
+//  b. expert me's histogram row hist[me][0 .. G) (W <= 8) as an exclusive scan, 256
+//     route_select workgroups a round: workgroup g's bucket entries
+//     bucket[me][g][0 .. hist[me][g]) are copied to rows
+//     block_off[me] * 64 + prefix(g) + 0, 1, ...; counts[me] = the row total;
+//  c. expert me's sorted_expert blocks, tile_map and pair_map entries, and
+//     its padding rows (Ktot << 24) | T after its routes;
+//  d. a grid-stride share of the unused blocks: sorted_expert -1, every row
+//     padding; workgroup 0 writes num_valid = {padded rows, routes, tiles,
+//     pairs}.
+// Dynamic LDS 4 * (4 * Etot + 3) bytes.
+NK_KERNEL __launch_bounds__(256) void netra_moe_sort_route_gfx950(
+    const int32_t* __restrict__ hist, const int32_t* __restrict__ bucket, const int32_t* __restrict__ cslice,
+    int32_t* __restrict__ counts, int32_t* __restrict__ sorted_ids, int32_t* __restrict__ sorted_expert,
+    int32_t* __restrict__ tile_map, int32_t* __restrict__ pair_map, int32_t* __restrict__ num_valid,
+    uint32_t T, uint32_t Ktot, uint32_t Etot, uint32_t G, uint32_t W, uint32_t cap_blocks) {
   extern __shared__ uint32_t lds[];
   uint32_t* cnt = lds;                        // [Etot]
   uint32_t* block_off = cnt + Etot;           // [Etot + 1]
   uint32_t* tile_off = block_off + Etot + 1;  // [Etot + 1]
   uint32_t* pair_off = tile_off + Etot + 1;   // [Etot + 1]
   __shared__ uint32_t s_wave[3][4];
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  if (Etot == 0u || Etot > 1024u) return;
-  const uint32_t routes = T * Ktot;
-  const uint32_t r = blockIdx.x * 256u + tid;
-  int32_t my_e = -1, my_rank = 0;  // this thread's route, loaded ahead of the scan
-  if (r < routes) {
-    my_e = ids[r];
-    my_rank = lrank[r];
+  __shared__ uint32_t s_row[2][4];
+  using nkroute::kSlices;
+  static_assert(kSlices == 8u, "two 16-byte loads per expert");
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, me = blockIdx.x;
+  if (Etot == 0u || Etot > 1024u || me >= Etot || W == 0u || W > 8u) return;
+  // the first round of expert me's histogram row and the slice counters of
+  // experts tid, tid + 256, ..., all requested before the first wait
+  const int32_t* row = hist + (size_t)me * G;
+  const uint32_t v0 = tid < G ? (uint32_t)row[tid] : 0u;
+  uint32_t cv[4];
+#pragma unroll
+  for (uint32_t i = 0; i < 4u; ++i) {
+    const uint32_t e = tid + 256u * i;
+    cv[i] = 0u;
+    if (e < Etot) {
+      const int4 a = *reinterpret_cast<const int4*>(cslice + e * kSlices);
+      const int4 b = *reinterpret_cast<const int4*>(cslice + e * kSlices + 4u);
+      cv[i] = (uint32_t)(a.x + a.y + a.z + a.w + b.x + b.y + b.z + b.w);
+    }
   }
+#pragma unroll
+  for (uint32_t i = 0; i < 4u; ++i)
+    if (tid + 256u * i < Etot) cnt[tid + 256u * i] = cv[i];
+  __syncthreads();
+  // a. layout
   const uint32_t ept = (Etot + 255u) / 256u, e0 = tid * ept;
   uint32_t sb = 0u, st = 0u, sp = 0u;
   for (uint32_t i = 0; i < ept; ++i) {
     const uint32_t e = e0 + i;
-    const uint32_t c = e < Etot ? (uint32_t)counts[e] : 0u;
-    if (e < Etot) cnt[e] = c;
+    const uint32_t c = e < Etot ? cnt[e] : 0u;
     const uint32_t vb = (c + 63u) >> 6;
     sb += vb;
     st += (c + 15u) >> 4;
@@ -672,32 +671,64 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_sort_place_gfx950(
   }
   if (tid == 0) { block_off[Etot] = tb; tile_off[Etot] = tt; pair_off[Etot] = tp; }
   __syncthreads();
+  const uint32_t routes = T * Ktot, cap_rows = cap_blocks * 64u;
   const uint32_t cap_tiles = (routes + 15u) / 16u + Etot;
-  if (tb > cap_blocks || tt > cap_tiles) {  // impossible for route_select histograms; write nothing
-    if (blockIdx.x == 0 && tid == 0) { num_valid[0] = 0; num_valid[1] = -1; num_valid[2] = 0; num_valid[3] = 0; }
+  if (tb > cap_blocks || tt > cap_tiles) {  // impossible for route_select's counts; write nothing
+    if (me == 0 && tid == 0) { num_valid[0] = 0; num_valid[1] = -1; num_valid[2] = 0; num_valid[3] = 0; }
     return;
   }
+  // b. expert me's routes, in route_select workgroup order (= token order)
+  const uint32_t rbase = block_off[me] * 64u;
+  uint32_t carry = 0u;
+  for (uint32_t g0 = 0; g0 < G; g0 += 256u) {  // uniform trip count
+    const uint32_t g = g0 + tid;
+    const uint32_t v = g0 == 0u ? v0 : (g < G ? (uint32_t)row[g] : 0u);
+    uint32_t inc = v;
+#pragma unroll
+    for (uint32_t off = 1; off < 64u; off <<= 1) {
+      const uint32_t o = __shfl_up(inc, off);
+      if (lane >= off) inc += o;
+    }
+    // alternate buffers: a round's reads of s_row[par] finish before the
+    // barrier of the next round, ahead of the writes of the round after it
+    const uint32_t par = (g0 >> 8) & 1u;
+    if (lane == 63u) s_row[par][wave] = inc;
+    __syncthreads();
+    uint32_t before = carry, total = 0u;
+#pragma unroll
+    for (uint32_t w = 0; w < 4u; ++w) {
+      const uint32_t x = s_row[par][w];
+      before += w < wave ? x : 0u;
+      total += x;
+    }
+    if (v != 0u) {  // the whole bucket (W <= 8 entries) in one or two 16-byte loads
+      const int32_t* src = bucket + ((size_t)me * G + g) * W;
+      const uint32_t dst = rbase + before + inc - v;
+      const int4 q0 = *reinterpret_cast<const int4*>(src);
+      const int4 q1 = W > 4u ? *reinterpret_cast<const int4*>(src + 4) : make_int4(0, 0, 0, 0);
+      const int32_t ent[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+      for (uint32_t i = 0; i < 8u; ++i)
+        if (i < v && dst + i < cap_rows) sorted_ids[dst + i] = ent[i];
+    }
+    carry += total;
+  }
+  if (tid == 0) counts[me] = (int32_t)carry;
+  // c. expert me's blocks, tiles, pairs and padding rows
   const int32_t pad = (int32_t)((Ktot << 24) | T);
-  if (r < routes && (uint32_t)my_e < Etot) {
-    const uint32_t t = r / Ktot, s = r - t * Ktot, g = t / W;
-    const uint32_t pos = block_off[my_e] * 64u + (g < G ? (uint32_t)base[(size_t)my_e * G + g] : 0u) +
-                         (uint32_t)my_rank;
-    if (pos < cap_blocks * 64u) sorted_ids[pos] = (int32_t)((s << 24) | t);
-  }
-  for (uint32_t e = blockIdx.x * 4u + wave; e < Etot; e += gridDim.x * 4u) {  // one expert per wave
-    const uint32_t b0 = block_off[e], b1 = block_off[e + 1u];
-    for (uint32_t b = b0 + lane; b < b1; b += 64u) sorted_expert[b] = (int32_t)e;
-    const uint32_t i0 = tile_off[e], i1 = tile_off[e + 1u];
-    for (uint32_t i = i0 + lane; i < i1; i += 64u) tile_map[i] = (int32_t)(b0 * 4u + (i - i0));
-    const uint32_t p0 = pair_off[e], p1 = pair_off[e + 1u];
-    for (uint32_t i = p0 + lane; i < p1; i += 64u) pair_map[i] = (int32_t)(b0 + 2u * (i - p0));
-    const uint32_t row = b0 * 64u + cnt[e] + lane;  // at most 63 rows after the expert's routes
-    if (row < b1 * 64u) sorted_ids[row] = pad;
-  }
-  const uint32_t stride = gridDim.x * 256u;
-  for (uint32_t p = tb * 64u + blockIdx.x * 256u + tid; p < cap_blocks * 64u; p += stride) sorted_ids[p] = pad;
-  for (uint32_t b = tb + blockIdx.x * 256u + tid; b < cap_blocks; b += stride) sorted_expert[b] = -1;
-  if (blockIdx.x == 0 && tid == 0) {
+  const uint32_t b0 = block_off[me], b1 = block_off[me + 1u];
+  for (uint32_t b = b0 + tid; b < b1; b += 256u) sorted_expert[b] = (int32_t)me;
+  const uint32_t i0 = tile_off[me], i1 = tile_off[me + 1u];
+  for (uint32_t i = i0 + tid; i < i1; i += 256u) tile_map[i] = (int32_t)(b0 * 4u + (i - i0));
+  const uint32_t p0 = pair_off[me], p1 = pair_off[me + 1u];
+  for (uint32_t i = p0 + tid; i < p1; i += 256u) pair_map[i] = (int32_t)(b0 + 2u * (i - p0));
+  const uint32_t prow = b0 * 64u + cnt[me] + tid;  // at most 63 rows after the expert's routes
+  if (tid < 64u && prow < b1 * 64u) sorted_ids[prow] = pad;
+  // d. unused blocks
+  const uint32_t stride = Etot * 256u;
+  for (uint32_t p = tb * 64u + me * 256u + tid; p < cap_rows; p += stride) sorted_ids[p] = pad;
+  for (uint32_t b = tb + me * 256u + tid; b < cap_blocks; b += stride) sorted_expert[b] = -1;
+  if (me == 0 && tid == 0) {
     num_valid[0] = (int32_t)(tb * 64u);
     num_valid[1] = (int32_t)routes;
     num_valid[2] = (int32_t)tt;

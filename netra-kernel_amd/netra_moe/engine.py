@@ -160,6 +160,7 @@ def resolve_front(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> st
     return front
 
 
+ROUTE_SLICES = 8                     # expert-total counters per expert (route_select's atomic adds, nkroute::kSlices)
 SCREEN_WG_TARGET = 256               # route_screen: split K until the grid has this many workgroups
                                      # (measured: T=512 screen 14.3 -> 6.1 us at 4 splits; 8 splits cost the select more)
 
@@ -238,8 +239,11 @@ def tensor_table(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> dic
     else:
         specs += [TensorSpec("screen", "f32", (screen_splits(cfg), T, screen_row_pad(cfg)), "temporary"),
                   TensorSpec("route_wsq", "f32", (screen_splits(cfg), screen_row_pad(cfg)), "temporary"),
-                  TensorSpec("route_base", "i32", (cfg.Etot, screen_groups(cfg)), "temporary"),
-                  TensorSpec("route_rank", "i32", (T * cfg.Ktot,), "temporary")]
+                  # per route_select workgroup: expert histogram, sorted-id buckets
+                  TensorSpec("route_hist", "i32", (cfg.Etot, screen_groups(cfg)), "temporary"),
+                  TensorSpec("route_bucket", "i32", (cfg.Etot, screen_groups(cfg), screen_tokens(cfg)), "temporary"),
+                  # expert totals in ROUTE_SLICES atomic counters each (cleared by route_screen)
+                  TensorSpec("route_slices", "i32", (cfg.Etot, ROUTE_SLICES), "temporary")]
     if path in ("stream", "fused"):
         specs += [TensorSpec("h_q", "e4m3", (cfg.cap_rows, I), "temporary"),
                   TensorSpec("h_scale", "f32", (cfg.cap_rows // 16, I // 128, 16), "temporary")]
@@ -251,7 +255,7 @@ def tensor_table(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> dic
 
 
 EXACT_FRONT_OPS = ("route", "sort")
-SCREEN_FRONT_OPS = ("route_screen", "route_select", "sort_count", "sort_place")
+SCREEN_FRONT_OPS = ("route_screen", "route_select", "sort_route")
 PATH_OPS = {"stream": ("gate_up", "down", "combine"), "tile": ("gate_up", "down", "combine")}
 
 
@@ -298,32 +302,29 @@ def _screen_front(cfg: MoEConfig) -> list[dict]:
     return [
         dict(name="moe.route_screen", symbol=f"netra_moe_route_screen_h{H}_k{H // 128 // Z}_gfx950",
              grid=((T + 127) // 128, (RP + 127) // 128, Z), block=(256, 1, 1), lds=4 * 2 * 128 * 128, dyn=0,
-             args=["x", "router_w", "screen", "route_wsq", u(T), u(H), u(cfg.E), u(RP)],
-             reads=["x", "router_w"], writes=["screen", "route_wsq"],
+             args=["x", "router_w", "screen", "route_wsq", "route_slices", u(cfg.Etot * ROUTE_SLICES),
+                   u(T), u(H), u(cfg.E), u(RP)],
+             reads=["x", "router_w"], writes=["screen", "route_wsq", "route_slices"],
              refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150"]),
         dict(name="moe.route_select",
              symbol=f"netra_moe_route_select_h{H}_e{screen_emax(cfg)}_w{Wt}_gfx950",
              grid=(G, 1, 1), block=(64 * Wt, 1, 1),
              lds=Wt * (H * 4 + 2 * (2 * screen_emax(cfg) + 1) + 64 * 4) + 8 * screen_emax(cfg) + 4, dyn=0,
              args=["x", "router_w", "router_bias", "screen", "route_wsq", "logits", "topk_ids", "topk_weights", "x_q",
-                   "x_scale", "route_base", "route_rank", u(T), u(H), u(cfg.E), u(cfg.K), u(cfg.S), u(RP), u(Z)],
-             reads=["x", "router_w", "router_bias", "screen", "route_wsq"],
-             writes=["logits", "topk_ids", "topk_weights", "x_q", "x_scale", "route_base", "route_rank"],
+                   "x_scale", "route_hist", "route_bucket", "route_slices",
+                   u(T), u(H), u(cfg.E), u(cfg.K), u(cfg.S), u(RP), u(Z), u(G)],
+             reads=["x", "router_w", "router_bias", "screen", "route_wsq", "route_slices"],
+             writes=["logits", "topk_ids", "topk_weights", "x_q", "x_scale", "route_hist", "route_bucket",
+                     "route_slices"],
              refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150",
                    "runtime/gfx950/routing/decode/qwen36_shared_gate_append_bridge.hip:76-112"]),
-        dict(name="moe.sort_count", symbol="netra_moe_sort_count_gfx950",
-             grid=(cfg.Etot, 1, 1), block=(256, 1, 1), lds=4 * 4, dyn=0,
-             args=["route_base", "expert_counts", u(G), u(cfg.Etot)],
-             reads=["route_base"], writes=["route_base", "expert_counts"],
-             refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]),
-        dict(name="moe.sort_place", symbol="netra_moe_sort_place_gfx950",
-             grid=(max((T * cfg.Ktot + 255) // 256, (cfg.Etot + 3) // 4), 1, 1), block=(256, 1, 1), lds=4 * 12,
-             dyn=4 * (4 * cfg.Etot + 3),
-             args=["topk_ids", "route_base", "route_rank", "expert_counts", "sorted_ids", "sorted_expert",
+        dict(name="moe.sort_route", symbol="netra_moe_sort_route_gfx950",
+             grid=(cfg.Etot, 1, 1), block=(256, 1, 1), lds=4 * 20, dyn=4 * (4 * cfg.Etot + 3),
+             args=["route_hist", "route_bucket", "route_slices", "expert_counts", "sorted_ids", "sorted_expert",
                    "tile_map", "pair_map", "num_valid",
                    u(T), u(cfg.Ktot), u(cfg.Etot), u(G), u(Wt), u(cfg.cap_blocks)],
-             reads=["topk_ids", "route_base", "route_rank", "expert_counts"],
-             writes=["sorted_ids", "sorted_expert", "tile_map", "pair_map", "num_valid"],
+             reads=["route_hist", "route_bucket", "route_slices"],
+             writes=["expert_counts", "sorted_ids", "sorted_expert", "tile_map", "pair_map", "num_valid"],
              refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112",
                    "manifests/gfx950/models/qwen36-35b-c64-fp8.json:43-49"]),
     ]
@@ -659,7 +660,7 @@ def op_typing(cfg: MoEConfig, op: dict, path: str) -> dict:
                    layouts=["row_major", "row_major", "screen_partials_ksplit"], epilogue="identity",
                    numerical={**num, "output_rounding": "fp32_partial_per_k_split",
                               "reduction_order": "bf16_mfma_k_split_partials"})
-    elif kind in ("sort", "sort_count", "sort_place"):
+    elif kind in ("sort", "sort_route"):
         typ = dict(shape=[cfg.routes, cfg.Etot, 1], dtypes=["int32", "int32", "int32", "int32"],
                    layouts=["topk_slots_row_major", "none", "sorted_m64_slot24"], epilogue="identity",
                    numerical={**num, "accumulation_dtype": "int32", "output_rounding": "exact_integer",

@@ -162,17 +162,16 @@ def test_prefill_engines_use_the_screen_front_end(tmp_path):
     doc = json.loads((tmp_path / "p" / "engine.json").read_text())
     assert doc["front_end"] == "screen" and doc["gemm_path"] == "tile"
     assert [op["name"] for op in doc["operations"]] == [f"moe.{n}" for n in op_names(cfg)]
-    assert op_names(cfg) == ("route_screen", "route_select", "sort_count", "sort_place", "gate_up", "down", "combine")
+    assert op_names(cfg) == ("route_screen", "route_select", "sort_route", "gate_up", "down", "combine")
     assert nm.manifest_check(tmp_path / "p")[0] == nm.Status.OK
     screen, select = doc["operations"][0], doc["operations"][1]
     assert screen["launch"]["grid"] == [32, 2, 4]  # 4096 / 128 tokens x 256 / 128 expert rows x 4 K splits
     # one token per wave, 8-wave workgroups at T=4096
     assert select["launch"]["grid"] == [512, 1, 1] and select["launch"]["block"] == [512, 1, 1]
     assert select["launch"]["lds_bytes"] <= 160 * 1024
-    count, place = doc["operations"][2], doc["operations"][3]
-    assert count["launch"]["grid"] == [257, 1, 1]  # one workgroup per expert (256 routed + shared)
-    assert place["launch"]["grid"] == [144, 1, 1]  # 4096 * 9 routes / 256
-    gate_up = doc["operations"][4]
+    sort = doc["operations"][2]
+    assert sort["launch"]["grid"] == [257, 1, 1]  # one workgroup per expert (256 routed + shared)
+    gate_up = doc["operations"][3]
     assert gate_up["kernel_symbol"] == "netra_moe_gate_up_lds_h2048_gfx950"
     assert gate_up["launch"]["block"] == [512, 1, 1] and gate_up["launch"]["lds_bytes"] <= 160 * 1024
 

@@ -2,7 +2,7 @@
 //   route_screen  bf16-MFMA router GEMM over all tokens and router rows, K
 //                 split for small T: partial sums of the approximate logit a,
 //                 and partial squared norms of the router rows
-//   route_select  one wave per token: certified candidate set from a and
+//   route_select  one to four waves per token: certified candidate set from a and
 //                 the bound m = 2^-10 ||x|| ||w|| on |L - a| (Cauchy-Schwarz),
 //                 exact contract logits of the candidates and the shared-gate
 //                 row, top-k + weights + shared-expert append, input quant,
@@ -241,26 +241,33 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
 }
 
 // ---------------------------------------------------------------------------
-// route_select: workgroup of W waves for W tokens, one token per wave (the
-// engine picks W so that the grid covers the chip: 4 for T <= 1024, else 8).
-//  0. the token row is staged in LDS, quantised (1x128) and its norm taken;
+// route_select: workgroup of W waves, WPT of them per token (a token's group),
+// so TW = W / WPT tokens per workgroup. The engine picks WPT so that small T
+// still gives the chip a few thousand waves: a token's exact dot products,
+// row staging and quant are then shared by its group's waves.
+//  0. wave v of a group stages its share of the token row (512-element
+//     chunks v, v + WPT, ...) in LDS widened to fp32, quantises it (1x128),
+//     sums its squares, and reads the screen sums of its share of the experts
+//     (lane l: experts l + 64 j for j = v, v + WPT, ...);
 //  1. bounds zlo/zhi of z = f32(bf16(L)) + bias from L in [a - m, a + m],
-//     m = 2^-10 ||x|| ||w_e|| (norms rounded up; bf16
-//     rounding and the bias add are monotone); theta <= K-th largest zlo;
-//     candidates = {e : zhi_e >= theta} contain the true top-K, since every
-//     other expert lies strictly below K experts;
-//  2. exact logits of the candidates and of the shared-gate row, one per
-//     16-lane group at a time (the token row staged in LDS);
-//  3. top-K over the candidates' exact z (descending, ties to the lower expert
-//     index), weights, shared expert append (as the exact top-k kernel);
-//  4. logits row;
+//     m = 2^-10 ||x|| ||w_e|| (norms rounded up; bf16 rounding and the bias
+//     add are monotone); theta <= K-th largest zlo; candidates =
+//     {e : zhi_e >= theta} contain the true top-K, since every other expert
+//     lies strictly below K experts. With WPT > 1 the codes meet in LDS and
+//     every wave of the group runs the same search and candidate list;
+//  2. exact logits of the candidates and of the shared-gate row, job q by
+//     16-lane group q mod 4 WPT of the group (the token row staged in LDS);
+//  3. the group's first wave: top-K over the candidates' exact z
+//     (descending, ties to the lower expert index), weights, shared expert
+//     append (as the exact top-k kernel);
+//  4. logits row, each wave its share of the experts;
 //  5. per workgroup g (of G): the per-expert histogram hist[e][g]
 //     (expert-major, so each expert's counts are contiguous for the sort's
 //     per-expert scan); the sorted-id entry (slot << 24) | token of every
 //     route, at bucket[e][g][rank], rank = the route's position among the
 //     workgroup's routes to e in token order; and the nonzero counts added
 //     into cslice[e][g mod kSlices].
-template <uint32_t NJ, uint32_t EMAX, uint32_t W>
+template <uint32_t NJ, uint32_t EMAX, uint32_t W, uint32_t WPT>
 __device__ __forceinline__ void route_select(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
     const float* __restrict__ screen, const float* __restrict__ wsq, uint16_t* __restrict__ logits,
@@ -269,56 +276,66 @@ __device__ __forceinline__ void route_select(
     int32_t* __restrict__ hist, int32_t* __restrict__ bucket, int32_t* __restrict__ cslice, uint32_t T,
     uint32_t E, uint32_t K, uint32_t S, uint32_t RP, uint32_t Z, uint32_t G) {
   constexpr uint32_t H = 128u * NJ;
-  constexpr uint32_t P = EMAX / 64u;  // experts per lane
-  static_assert(EMAX % 64u == 0 && P <= 8u && W <= 32u, "shape");
-  __shared__ float4 s_x[W][32u * NJ];        // the tokens' rows, widened to fp32
-  __shared__ __align__(16) uint16_t s_cand[W][EMAX];  // also the selected slots (K * 8 <= 2 * EMAX bytes)
-  __shared__ uint16_t s_exact[W][EMAX + 1];  // exact logit bits, candidate order; shared row last
-  __shared__ int32_t s_ids[W][kMaxSlots];
+  constexpr uint32_t P = EMAX / 64u;         // experts per lane over the whole row
+  constexpr uint32_t PW = P / WPT;           // experts per lane of one wave's share
+  constexpr uint32_t TW = W / WPT;           // tokens per workgroup
+  constexpr uint32_t NX = NJ / (4u * WPT);   // 512-element chunks of the row per wave
+  constexpr bool kShared = WPT > 1u;         // several waves per token
+  static_assert(EMAX % 64u == 0 && P <= 8u && W <= 32u && W % WPT == 0 && P % WPT == 0 &&
+                NJ % (4u * WPT) == 0, "shape");
+  __shared__ float4 s_x[TW][32u * NJ];        // the tokens' rows, widened to fp32
+  __shared__ __align__(16) uint16_t s_cand[TW][EMAX];  // also the selected slots (K * 8 <= 2 * EMAX bytes)
+  __shared__ uint16_t s_exact[TW][EMAX + 1];  // exact logit bits, candidate order; shared row last
+  __shared__ int32_t s_ids[TW][kMaxSlots];
   __shared__ uint32_t s_hist[EMAX + 1];  // bit u: token u of the workgroup routes to the expert
   __shared__ float s_wn[EMAX];  // router-row norms, ||w_e|| (1 + 2^-9), from the screen's Z partial sums
+  // several waves per token: the codes of every expert, and the row's partial squared norms
+  __shared__ uint32_t s_lo[kShared ? TW : 1u][kShared ? EMAX : 1u];
+  __shared__ uint32_t s_hi[kShared ? TW : 1u][kShared ? EMAX : 1u];
+  __shared__ float s_xx[TW][WPT];
   const uint32_t rows = E + S, Ktot = K + S;
   if (E > EMAX || K == 0 || K > E || Ktot > kMaxSlots || S > 1u) return;  // uniform
   constexpr uint32_t kThreads = 64u * W;
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
-  // This wave's token (one per wave): its row, screen sums and biases are
-  // requested before the workgroup's norm set-up below, so the three
-  // dependent round trips of the original order overlap.
-  const uint32_t t_w = blockIdx.x * W + wave;
-  const bool active = t_w < T;
-  // The split partial sums come kZBatch splits at a time, every load of a
-  // batch issued before the first add (indices clamped into range, so no load
-  // sits under a condition, which would make each one its own round trip);
-  // the adds run in split order from the first split's value.
-  constexpr uint32_t kZBatch = 4;
-  uint4 xv[H / 512u];
-  float aval[P], bv[P];
+  const uint32_t tt = wave / WPT, v = wave % WPT;  // the wave's token in the workgroup, its place in the group
+  const uint32_t t = blockIdx.x * TW + tt;
+  const bool active = t < T;  // uniform per group; inactive waves still take every barrier
+  // This wave's row chunks, screen sums and biases are requested before the
+  // workgroup's norm set-up below, so the dependent round trips overlap. The
+  // split partial sums come kZBatch splits at a time (all of them, Z <= 8,
+  // when a wave reads one or two experts a lane), every load of a batch
+  // issued before the first add (indices clamped into range, so no load sits
+  // under a condition, which would make each one its own round trip); the
+  // adds run in split order from the first split's value.
+  constexpr uint32_t kZBatch = PW <= 2u ? 8u : 4u;
+  uint4 xv[NX];
+  float aval[PW], bv[PW];
   if (active) {
 #pragma unroll
-    for (uint32_t p = 0; p < H / 512u; ++p)
-      xv[p] = *reinterpret_cast<const uint4*>(x + (size_t)t_w * H + 512u * p + 8u * lane);
-    const float* srow = screen + (size_t)t_w * RP;  // split z at srow + z * T * RP
+    for (uint32_t p = 0; p < NX; ++p)
+      xv[p] = *reinterpret_cast<const uint4*>(x + (size_t)t * H + 512u * (v + WPT * p) + 8u * lane);
+    const float* srow = screen + (size_t)t * RP;  // split z at srow + z * T * RP
 #pragma unroll
-    for (uint32_t j = 0; j < P; ++j) bv[j] = bias[min(lane + 64u * j, E - 1u)];
+    for (uint32_t jj = 0; jj < PW; ++jj) bv[jj] = bias[min(lane + 64u * (v + WPT * jj), E - 1u)];
     for (uint32_t z0 = 0; z0 < Z; z0 += kZBatch) {  // uniform; one trip for Z <= kZBatch
-      float part[kZBatch][P];
+      float part[kZBatch][PW];
 #pragma unroll
       for (uint32_t zz = 0; zz < kZBatch; ++zz) {
         const float* sz = srow + (size_t)min(z0 + zz, Z - 1u) * T * RP;
 #pragma unroll
-        for (uint32_t j = 0; j < P; ++j) part[zz][j] = sz[min(lane + 64u * j, E - 1u)];
+        for (uint32_t jj = 0; jj < PW; ++jj) part[zz][jj] = sz[min(lane + 64u * (v + WPT * jj), E - 1u)];
       }
 #pragma unroll
       for (uint32_t zz = 0; zz < kZBatch; ++zz)
         if (z0 + zz < Z) {
 #pragma unroll
-          for (uint32_t j = 0; j < P; ++j) aval[j] = z0 + zz == 0u ? part[zz][j] : aval[j] + part[zz][j];
+          for (uint32_t jj = 0; jj < PW; ++jj) aval[jj] = z0 + zz == 0u ? part[zz][jj] : aval[jj] + part[zz][jj];
         }
     }
 #pragma unroll
-    for (uint32_t j = 0; j < P; ++j)
-      if (lane + 64u * j >= E) aval[j] = bv[j] = 0.0f;
+    for (uint32_t jj = 0; jj < PW; ++jj)
+      if (lane + 64u * (v + WPT * jj) >= E) aval[jj] = bv[jj] = 0.0f;
   }
   for (uint32_t e = tid; e <= EMAX; e += kThreads) {
     s_hist[e] = 0u;
@@ -334,39 +351,61 @@ __device__ __forceinline__ void route_select(
     }
     if (e < E) s_wn[e] = sqrtf(q) * kNormSlack;
   }
-  __syncthreads();
   const uint32_t s = lane & 15u, g = lane >> 4;
 
-#pragma unroll 1
-  for (uint32_t tt = wave; tt < W; tt += W) {  // one token per wave
-    const uint32_t t = blockIdx.x * W + tt;
-    if (t >= T) break;  // uniform per wave; later tokens are past T too
-    // 0. token row -> LDS, its 1x128 quant and its norm
-    float xx = 0.0f;
+  // 0. this wave's chunks of the token row -> LDS, their 1x128 quant and squares
+  float xx = 0.0f;
+  if (active) {
 #pragma unroll
-    for (uint32_t p = 0; p < H / 512u; ++p) {
-      const uint32_t i0 = 512u * p + 8u * lane;
-      const uint4 v = xv[p];
+    for (uint32_t p = 0; p < NX; ++p) {
+      const uint32_t i0 = 512u * (v + WPT * p) + 8u * lane;
+      const uint4 u = xv[p];
       const uint32_t jx = i0 >> 7, sx = (i0 >> 3) & 15u;  // exact_dot's order: 32 j + s, then 32 j + 16 + s
-      s_x[tt][32u * jx + sx] = make_float4(nk::bf16_lo(v.x), nk::bf16_hi(v.x), nk::bf16_lo(v.y), nk::bf16_hi(v.y));
-      s_x[tt][32u * jx + 16u + sx] = make_float4(nk::bf16_lo(v.z), nk::bf16_hi(v.z), nk::bf16_lo(v.w), nk::bf16_hi(v.w));
-      quant8(v, xq + (size_t)t * H + i0, xs + (size_t)t * NJ + (i0 >> 7), s == 0);
-      xx += sumsq8(v);
+      s_x[tt][32u * jx + sx] = make_float4(nk::bf16_lo(u.x), nk::bf16_hi(u.x), nk::bf16_lo(u.y), nk::bf16_hi(u.y));
+      s_x[tt][32u * jx + 16u + sx] = make_float4(nk::bf16_lo(u.z), nk::bf16_hi(u.z), nk::bf16_lo(u.w), nk::bf16_hi(u.w));
+      quant8(u, xq + (size_t)t * H + i0, xs + (size_t)t * NJ + (i0 >> 7), s == 0);
+      xx += sumsq8(u);
     }
 #pragma unroll
     for (uint32_t off = 1; off < 64u; off <<= 1) xx += __shfl_xor(xx, off);
-    const float mx = kScreenMargin * sqrtf(xx) * kNormSlack;
+    if (kShared && lane == 0) s_xx[tt][v] = xx;
+  }
+  __syncthreads();  // s_wn, s_hist, every chunk of the rows and their squares
 
-    // 1. certified candidates
-    uint32_t clo[P], chi[P];
+  // 1. certified candidates
+  uint32_t clo[P], chi[P], pos[P], n = 0u;
+  if (active) {
+    if constexpr (kShared) {
+      xx = s_xx[tt][0];
 #pragma unroll
-    for (uint32_t j = 0; j < P; ++j) {
-      const uint32_t e = lane + 64u * j;
-      clo[j] = chi[j] = 0u;
+      for (uint32_t u = 1; u < WPT; ++u) xx += s_xx[tt][u];
+    }
+    const float mx = kScreenMargin * sqrtf(xx) * kNormSlack;
+#pragma unroll
+    for (uint32_t jj = 0; jj < PW; ++jj) {
+      const uint32_t j = v + WPT * jj, e = lane + 64u * j;
+      uint32_t lo = 0u, hi = 0u;
       if (e < E) {
-        const float a = aval[j], m = mx * s_wn[e], b = bv[j];
-        clo[j] = nk::order_bits(nk::bf16_round_hw(a - m) + b);  // bf16 RNE (hardware; a is finite)
-        chi[j] = nk::order_bits(nk::bf16_round_hw(a + m) + b);
+        const float a = aval[jj], m = mx * s_wn[e], b = bv[jj];
+        lo = nk::order_bits(nk::bf16_round_hw(a - m) + b);  // bf16 RNE (hardware; a is finite)
+        hi = nk::order_bits(nk::bf16_round_hw(a + m) + b);
+      }
+      if constexpr (kShared) {
+        s_lo[tt][e] = lo;
+        s_hi[tt][e] = hi;
+      } else {
+        clo[j] = lo;
+        chi[j] = hi;
+      }
+    }
+  }
+  if constexpr (kShared) __syncthreads();  // every expert's codes
+  if (active) {
+    if constexpr (kShared) {
+#pragma unroll
+      for (uint32_t j = 0; j < P; ++j) {
+        clo[j] = s_lo[tt][lane + 64u * j];
+        chi[j] = s_hi[tt][lane + 64u * j];
       }
     }
     // theta <= the K-th largest zlo: the largest code with its low 16 bits
@@ -384,23 +423,29 @@ __device__ __forceinline__ void route_select(
       for (uint32_t j = 0; j < P; ++j) cnt += (uint32_t)__popcll(__ballot(clo[j] >= cand));
       if (cnt >= K) theta = cand;
     }
-    uint32_t n = 0u, pos[P];
 #pragma unroll
     for (uint32_t j = 0; j < P; ++j) {
       const uint32_t e = lane + 64u * j;
       const bool pred = e < E && chi[j] >= theta;
       const unsigned long long bal = __ballot(pred);
       pos[j] = pred ? n + lane_rank(bal) : 0xffffffffu;
-      if (pred) s_cand[tt][pos[j]] = (uint16_t)e;
+      // each wave writes the list entries of its own share of the experts
+      if (pred && (!kShared || j % WPT == v)) s_cand[tt][pos[j]] = (uint16_t)e;
       n += (uint32_t)__popcll(bal);
     }
+  }
 
-    // 2. exact logits: jobs 0..n-1 are the candidates, job n the shared-gate row
+  // 2. exact logits: jobs 0..n-1 are the candidates, job n the shared-gate row
+  if constexpr (kShared) {
+    __syncthreads();  // the whole candidate list
+  } else {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's row and list are in LDS
     __builtin_amdgcn_wave_barrier();
+  }
+  if (active) {
     const uint32_t jobs = n + S;
 #pragma unroll 1
-    for (uint32_t q = g; q < jobs; q += 4u) {
+    for (uint32_t q = 4u * v + g; q < jobs; q += 4u * WPT) {
       // Re-read the token row from LDS for every job: kept in registers
       // across jobs it costs 128 VGPRs and halves the resident waves.
       asm volatile("" ::: "memory");
@@ -411,10 +456,15 @@ __device__ __forceinline__ void route_select(
       const float l = exact_dot<NJ>(s_x[tt], wv, s);
       if (s == 0) s_exact[tt][q] = nk::bf16_rne(l);
     }
-    // (the exact values are read back by this wave only)
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  }
+  if constexpr (kShared) {
+    __syncthreads();  // every exact logit of the group
+  } else {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the exact values are read back by this wave only
     __builtin_amdgcn_wave_barrier();
+  }
 
+  if (active && v == 0u) {
     // 3. top-K over the candidates' exact z (descending, ties to the lower id)
     uint32_t my_id = 0u, my_code = 0u;
     if (n <= 64u) {  // one candidate per lane: slot = rank among the candidates
@@ -502,29 +552,31 @@ __device__ __forceinline__ void route_select(
       s_ids[tt][lane] = (int32_t)my_id;
       atomicOr(&s_hist[my_id], 1u << tt);
     }
-
-    // 4. logits row
+  }
+  if (active) {
+    // 4. logits row, this wave's share of the experts (non-temporal: no later
+    // kernel of the layer reads the logits)
     uint16_t* lrow = logits + (size_t)t * rows;
 #pragma unroll
-    for (uint32_t j = 0; j < P; ++j) {
-      const uint32_t e = lane + 64u * j;
-      if (e < E)  // non-temporal: no later kernel of the layer reads the logits
-        __builtin_nontemporal_store(pos[j] != 0xffffffffu ? s_exact[tt][pos[j]] : nk::bf16_rne(aval[j]), lrow + e);
+    for (uint32_t jj = 0; jj < PW; ++jj) {
+      const uint32_t j = v + WPT * jj, e = lane + 64u * j;
+      if (e < E)
+        __builtin_nontemporal_store(pos[j] != 0xffffffffu ? s_exact[tt][pos[j]] : nk::bf16_rne(aval[jj]), lrow + e);
     }
-    if (S != 0u && lane == 0) __builtin_nontemporal_store(s_exact[tt][n], lrow + E);
+    if (S != 0u && v == 0u && lane == 0) __builtin_nontemporal_store(s_exact[tt][n], lrow + E);
   }
   __syncthreads();
 
   // 5. buckets and histogram from the per-expert token masks (a token routes
   // to an expert at most once): the rank of token tk's route to e is the
   // number of earlier tokens in e's mask
-  const uint32_t t0 = blockIdx.x * W;
-  for (uint32_t r = tid; r < W * Ktot; r += kThreads) {
+  const uint32_t t0 = blockIdx.x * TW;
+  for (uint32_t r = tid; r < TW * Ktot; r += kThreads) {
     const uint32_t tk = r / Ktot, sl = r - tk * Ktot;
     if (t0 + tk >= T) break;
     const uint32_t e = (uint32_t)s_ids[tk][sl];
     const uint32_t rank = __popc(s_hist[e] & ((1u << tk) - 1u));
-    bucket[((size_t)e * G + blockIdx.x) * W + rank] = (int32_t)((sl << 24) | (t0 + tk));
+    bucket[((size_t)e * G + blockIdx.x) * TW + rank] = (int32_t)((sl << 24) | (t0 + tk));
   }
   for (uint32_t e = tid; e < rows; e += kThreads) {
     const uint32_t c = __popc(s_hist[e]);
@@ -555,9 +607,9 @@ NK_ROUTE_SCREEN(2048, 4)
 NK_ROUTE_SCREEN(2048, 8)
 NK_ROUTE_SCREEN(2048, 16)
 
-#define NK_ROUTE_SELECT(HV, EMAXV, WV)                                                            \
+#define NK_ROUTE_SELECT(HV, EMAXV, WV, PV)                                                        \
   NK_KERNEL __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(4)))                     \
-  void netra_moe_route_select_h##HV##_e##EMAXV##_w##WV##_gfx950(                                 \
+  void netra_moe_route_select_h##HV##_e##EMAXV##_w##WV##x##PV##_gfx950(                           \
       const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,                             \
       const float* __restrict__ bias, const float* __restrict__ screen,                           \
       const float* __restrict__ wsq, uint16_t* __restrict__ logits, int32_t* __restrict__ ids,    \
@@ -566,16 +618,23 @@ NK_ROUTE_SCREEN(2048, 16)
       uint32_t T, uint32_t H, uint32_t E, uint32_t K, uint32_t S, uint32_t RP, uint32_t Z,        \
       uint32_t G) {                                                                               \
     (void)H;                                                                                      \
-    nkroute::route_select<HV / 128, EMAXV, WV>(x, w, bias, screen, wsq, logits, ids, weights,     \
-                                               xq, xs, hist, bucket, cslice, T, E, K, S, RP, Z, G); \
+    nkroute::route_select<HV / 128, EMAXV, WV, PV>(x, w, bias, screen, wsq, logits, ids, weights, \
+                                                   xq, xs, hist, bucket, cslice, T, E, K, S, RP, Z, G); \
   }
-#define NK_ROUTE_SELECT_W(HV, EMAXV) NK_ROUTE_SELECT(HV, EMAXV, 4) NK_ROUTE_SELECT(HV, EMAXV, 8)
-NK_ROUTE_SELECT_W(512, 256)
-NK_ROUTE_SELECT_W(1024, 256)
-NK_ROUTE_SELECT_W(2048, 256)
-NK_ROUTE_SELECT_W(512, 512)
-NK_ROUTE_SELECT_W(1024, 512)
-NK_ROUTE_SELECT_W(2048, 512)
+// w<W>x<WPT>: W waves a workgroup, WPT of them per token (WPT <= H / 512)
+#define NK_ROUTE_SELECT_1(HV, EMAXV) NK_ROUTE_SELECT(HV, EMAXV, 4, 1) NK_ROUTE_SELECT(HV, EMAXV, 8, 1)
+NK_ROUTE_SELECT_1(512, 256)
+NK_ROUTE_SELECT_1(1024, 256)
+NK_ROUTE_SELECT_1(2048, 256)
+NK_ROUTE_SELECT_1(512, 512)
+NK_ROUTE_SELECT_1(1024, 512)
+NK_ROUTE_SELECT_1(2048, 512)
+NK_ROUTE_SELECT(1024, 256, 8, 2)
+NK_ROUTE_SELECT(1024, 512, 8, 2)
+NK_ROUTE_SELECT(2048, 256, 8, 2)
+NK_ROUTE_SELECT(2048, 512, 8, 2)
+NK_ROUTE_SELECT(2048, 256, 8, 4)
+NK_ROUTE_SELECT(2048, 512, 8, 4)
 
 // ---------------------------------------------------------------------------
 // sort_route: workgroup me (256 threads) of a grid of exactly Etot, one per
@@ -611,10 +670,14 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_sort_route_gfx950(
   static_assert(kSlices == 8u, "two 16-byte loads per expert");
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, me = blockIdx.x;
   if (Etot == 0u || Etot > 1024u || me >= Etot || W == 0u || W > 8u) return;
-  // the first round of expert me's histogram row and the slice counters of
-  // experts tid, tid + 256, ..., all requested before the first wait
+  // the first kRounds rounds of expert me's histogram row and the slice
+  // counters of experts tid, tid + 256, ..., all requested before the first
+  // wait
+  constexpr uint32_t kRounds = 4;
   const int32_t* row = hist + (size_t)me * G;
-  const uint32_t v0 = tid < G ? (uint32_t)row[tid] : 0u;
+  uint32_t vpre[kRounds];
+#pragma unroll
+  for (uint32_t i = 0; i < kRounds; ++i) vpre[i] = tid + 256u * i < G ? (uint32_t)row[tid + 256u * i] : 0u;
   uint32_t cv[4];
 #pragma unroll
   for (uint32_t i = 0; i < 4u; ++i) {
@@ -682,7 +745,21 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_sort_route_gfx950(
   uint32_t carry = 0u;
   for (uint32_t g0 = 0; g0 < G; g0 += 256u) {  // uniform trip count
     const uint32_t g = g0 + tid;
-    const uint32_t v = g0 == 0u ? v0 : (g < G ? (uint32_t)row[g] : 0u);
+    uint32_t v = 0u;
+    if (g0 < 256u * kRounds) {
+#pragma unroll
+      for (uint32_t i = 0; i < kRounds; ++i)
+        if (g0 == 256u * i) v = vpre[i];
+    } else if (g < G) {
+      v = (uint32_t)row[g];
+    }
+    // the round's bucket entries, requested before the scan's barrier
+    const int32_t* src = bucket + ((size_t)me * G + g) * W;
+    int4 q0 = make_int4(0, 0, 0, 0), q1 = make_int4(0, 0, 0, 0);
+    if (v != 0u) {  // the whole bucket (W <= 8 entries) in one or two 16-byte loads
+      q0 = *reinterpret_cast<const int4*>(src);
+      if (W > 4u) q1 = *reinterpret_cast<const int4*>(src + 4);
+    }
     uint32_t inc = v;
 #pragma unroll
     for (uint32_t off = 1; off < 64u; off <<= 1) {
@@ -701,11 +778,8 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_sort_route_gfx950(
       before += w < wave ? x : 0u;
       total += x;
     }
-    if (v != 0u) {  // the whole bucket (W <= 8 entries) in one or two 16-byte loads
-      const int32_t* src = bucket + ((size_t)me * G + g) * W;
+    if (v != 0u) {
       const uint32_t dst = rbase + before + inc - v;
-      const int4 q0 = *reinterpret_cast<const int4*>(src);
-      const int4 q1 = W > 4u ? *reinterpret_cast<const int4*>(src + 4) : make_int4(0, 0, 0, 0);
       const int32_t ent[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
       for (uint32_t i = 0; i < 8u; ++i)

@@ -140,7 +140,7 @@ def xcd_grid(items: int) -> int:
 FRONTS = ("exact", "screen")
 SCREEN_H = (512, 1024, 2048)          # netra_moe_route_screen_h<H>_gfx950 / route_select_h<H>_e<EMAX>
 SCREEN_EMAX = (256, 512)              # expert capacities of the route_select kernels
-SCREEN_SELECT_WAVES = (4, 8)          # route_select_h<H>_e<EMAX>_w<W>: W waves, one token each
+SCREEN_SELECT_SHAPES = ((4, 1), (8, 1), (8, 2), (8, 4))  # route_select_h<H>_e<EMAX>_w<W>x<WPT>: W waves, WPT per token
 
 
 def resolve_front(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> str:
@@ -188,10 +188,32 @@ def screen_emax(cfg: MoEConfig) -> int:
     return next(e for e in SCREEN_EMAX if cfg.E <= e)
 
 
-def screen_tokens(cfg: MoEConfig) -> int:
-    """Tokens (= waves) per route_select workgroup: small workgroups while
-    they are needed to spread T tokens over the chip's 256 CUs."""
+SCREEN_WAVE_TARGET = 2048            # route_select: waves per token until T * WPT reaches this many
+
+
+def screen_waves_per_token(cfg: MoEConfig) -> int:
+    """Waves per token of route_select (WPT of netra_moe_route_select_h<H>_e<EMAX>_w<W>x<WPT>):
+    1, 2 or 4 (at most H / 512, the row's 512-element chunks), the most that
+    keeps T * WPT within SCREEN_WAVE_TARGET, so small T still spreads a few
+    thousand waves over the chip (each token's exact dot products, row staging
+    and quant split over its waves)."""
+    wpt = 1
+    while wpt < 4 and 2 * wpt <= cfg.H // 512 and cfg.T * 2 * wpt <= SCREEN_WAVE_TARGET:
+        wpt *= 2
+    return wpt
+
+
+def screen_waves(cfg: MoEConfig) -> int:
+    """Waves per route_select workgroup: 8 when tokens share waves, else 4 for
+    T <= 1024 (small workgroups spread T tokens over the chip's 256 CUs), else 8."""
+    if screen_waves_per_token(cfg) > 1:
+        return 8
     return 4 if cfg.T <= 1024 else 8
+
+
+def screen_tokens(cfg: MoEConfig) -> int:
+    """Tokens per route_select workgroup."""
+    return screen_waves(cfg) // screen_waves_per_token(cfg)
 
 
 def screen_groups(cfg: MoEConfig) -> int:
@@ -297,6 +319,7 @@ def _screen_front(cfg: MoEConfig) -> list[dict]:
     u = lambda v: ("u32", int(v))  # noqa: E731
     G = screen_groups(cfg)
     Wt = screen_tokens(cfg)
+    Wv, WPT = screen_waves(cfg), screen_waves_per_token(cfg)
     RP = screen_row_pad(cfg)
     Z = screen_splits(cfg)
     return [
@@ -307,9 +330,10 @@ def _screen_front(cfg: MoEConfig) -> list[dict]:
              reads=["x", "router_w"], writes=["screen", "route_wsq", "route_slices"],
              refs=["kernels/gfx950/templates/routing/bf16_gemv.inc:16-150"]),
         dict(name="moe.route_select",
-             symbol=f"netra_moe_route_select_h{H}_e{screen_emax(cfg)}_w{Wt}_gfx950",
-             grid=(G, 1, 1), block=(64 * Wt, 1, 1),
-             lds=Wt * (H * 4 + 2 * (2 * screen_emax(cfg) + 1) + 64 * 4) + 8 * screen_emax(cfg) + 4, dyn=0,
+             symbol=f"netra_moe_route_select_h{H}_e{screen_emax(cfg)}_w{Wv}x{WPT}_gfx950",
+             grid=(G, 1, 1), block=(64 * Wv, 1, 1),
+             lds=Wt * (H * 4 + 2 * (2 * screen_emax(cfg) + 1) + 64 * 4 + 4 * WPT
+                       + (8 * screen_emax(cfg) if WPT > 1 else 0)) + 8 * screen_emax(cfg) + 4, dyn=0,
              args=["x", "router_w", "router_bias", "screen", "route_wsq", "logits", "topk_ids", "topk_weights", "x_q",
                    "x_scale", "route_hist", "route_bucket", "route_slices",
                    u(T), u(H), u(cfg.E), u(cfg.K), u(cfg.S), u(RP), u(Z), u(G)],

@@ -40,12 +40,12 @@
 //       blockIdx.x == 0 write the partial squared router-row norms wsq, and
 //       workgroup (0,0,0) clears slices
 //   netra_moe_route_select_h<H>_e<EMAX>_w<W>x<V>_gfx950(x, w, bias, screen, wsq, logits,
-//       ids, weights, xq, xs, hist i32[Etot,G], bucket i32[Etot,G,W/V], slices i32[Etot,8];
+//       ids, weights, xq, xs, hist i32[G,Etot+1], bucket i32[G,(W/V)*Ktot], slices i32[Etot,8];
 //       T, H, E, K, S, RP, Z, G)   grid G = ceil(T/(W/V)), block 64*W,
 //       (W, V) in {(4,1), (8,1), (8,2), (8,4)}, V <= H/512 waves per token;
 //       slices must hold zeros (route_screen clears them)
 //   netra_moe_sort_route_gfx950(hist, bucket, slices, counts, sorted_ids,
-//       sorted_expert, tile_map, pair_map, num_valid; T, Ktot, Etot, G, W/V, CAP)
+//       sorted_expert, tile_map, pair_map, num_valid; T, Ktot, Etot, S, G, W/V, CAP)
 //       grid exactly Etot, block 256, dynamic LDS 4*(4*Etot+3)
 //   fused decode FFN (T <= 64), (H, I) in {(512,256), (1024,1024), (2048,512), (4096,256)}:
 //   netra_moe_ffn_gate_up_h<H>_i<I>_<wide|narrow>_gfx950(logits, bias, ids, weights,

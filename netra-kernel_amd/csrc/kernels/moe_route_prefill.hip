@@ -6,13 +6,13 @@
 //                 the bound m = 2^-10 ||x|| ||w|| on |L - a| (Cauchy-Schwarz),
 //                 exact contract logits of the candidates and the shared-gate
 //                 row, top-k + weights + shared-expert append, input quant,
-//                 logits out; per workgroup: expert histogram, every route's
-//                 sorted-id entry in an (expert, workgroup) bucket, and the
-//                 expert totals added into slice counters
+//                 logits out; per workgroup: its routes' sorted-id entries
+//                 grouped by expert with the groups' offsets, and the expert
+//                 totals added into slice counters
 //   sort_route    one workgroup per expert: the expert layout (64-row blocks,
 //                 padding, tile and pair lists) from the totals, the expert's
 //                 prefix over the route_select workgroups, and its routes
-//                 copied from the buckets into their sorted rows
+//                 copied from the workgroups' lists into their sorted rows
 // The results equal those of the exact front end (moe_router.hip): top-k ids,
 // weights, counts and the sorted layout are the same bits. Logits of the
 // experts that were not candidates are the screen's values rounded to bf16.
@@ -261,12 +261,11 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
 //     (descending, ties to the lower expert index), weights, shared expert
 //     append (as the exact top-k kernel);
 //  4. logits row, each wave its share of the experts;
-//  5. per workgroup g (of G): the per-expert histogram hist[e][g]
-//     (expert-major, so each expert's counts are contiguous for the sort's
-//     per-expert scan); the sorted-id entry (slot << 24) | token of every
-//     route, at bucket[e][g][rank], rank = the route's position among the
-//     workgroup's routes to e in token order; and the nonzero counts added
-//     into cslice[e][g mod kSlices].
+//  5. per workgroup g: its routes' sorted-id entries (slot << 24) | token
+//     as one list bucket[g][..] grouped by expert (token order within an
+//     expert), the list's expert offsets hist[g][0 .. E + S] (an exclusive
+//     scan of the per-expert counts, last entry the total), and the nonzero
+//     counts added into cslice[e][g mod kSlices].
 template <uint32_t NJ, uint32_t EMAX, uint32_t W, uint32_t WPT>
 __device__ __forceinline__ void route_select(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
@@ -567,24 +566,58 @@ __device__ __forceinline__ void route_select(
   }
   __syncthreads();
 
-  // 5. buckets and histogram from the per-expert token masks (a token routes
-  // to an expert at most once): the rank of token tk's route to e is the
-  // number of earlier tokens in e's mask
+  // 5. the workgroup's routes as one list grouped by expert, in token order
+  // within an expert: route (tk, sl) to e lands at pre[e] + rank, pre[e] =
+  // the workgroup's routes to experts below e (an exclusive scan of the
+  // per-expert counts, each thread a contiguous run of experts), rank = the
+  // earlier tokens in e's mask (a token routes to an expert at most once).
+  // hist[g][0 .. rows] = pre (pre[rows] = the workgroup's route count), so
+  // workgroup g's entries of expert e are bucket[g][pre[e] .. pre[e + 1]):
+  // every store of this step goes to the workgroup's own rows.
+  constexpr uint32_t kPer = (EMAX + 1u + kThreads - 1u) / kThreads;
+  __shared__ uint32_t s_pre[EMAX + 2];
+  __shared__ uint32_t s_wsum[W];
+  uint32_t cnt[kPer], sum = 0u;
+#pragma unroll
+  for (uint32_t i = 0; i < kPer; ++i) {
+    const uint32_t e = tid * kPer + i;
+    cnt[i] = e < rows ? (uint32_t)__popc(s_hist[e]) : 0u;
+    sum += cnt[i];
+  }
+  uint32_t inc = sum;
+#pragma unroll
+  for (uint32_t off = 1; off < 64u; off <<= 1) {
+    const uint32_t o = __shfl_up(inc, off);
+    if (lane >= off) inc += o;
+  }
+  if (lane == 63u) s_wsum[wave] = inc;
+  __syncthreads();
+  uint32_t run = inc - sum;
+  for (uint32_t u = 0; u < wave; ++u) run += s_wsum[u];
+  int32_t* hrow = hist + (size_t)blockIdx.x * (rows + 1u);
+#pragma unroll
+  for (uint32_t i = 0; i < kPer; ++i) {
+    const uint32_t e = tid * kPer + i;
+    if (e <= rows) {
+      s_pre[e] = run;
+      hrow[e] = (int32_t)run;
+    }
+    if (e < rows && cnt[i] != 0u)
+      __hip_atomic_fetch_add(&cslice[e * kSlices + (blockIdx.x & (kSlices - 1u))], (int32_t)cnt[i],
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    run += cnt[i];
+  }
+  __syncthreads();
   const uint32_t t0 = blockIdx.x * TW;
+  int32_t* brow = bucket + (size_t)blockIdx.x * (TW * Ktot);
   for (uint32_t r = tid; r < TW * Ktot; r += kThreads) {
     const uint32_t tk = r / Ktot, sl = r - tk * Ktot;
     if (t0 + tk >= T) break;
     const uint32_t e = (uint32_t)s_ids[tk][sl];
     const uint32_t rank = __popc(s_hist[e] & ((1u << tk) - 1u));
-    bucket[((size_t)e * G + blockIdx.x) * TW + rank] = (int32_t)((sl << 24) | (t0 + tk));
+    brow[s_pre[e] + rank] = (int32_t)((sl << 24) | (t0 + tk));
   }
-  for (uint32_t e = tid; e < rows; e += kThreads) {
-    const uint32_t c = __popc(s_hist[e]);
-    hist[(size_t)e * G + blockIdx.x] = (int32_t)c;
-    if (c != 0u)
-      __hip_atomic_fetch_add(&cslice[e * kSlices + (blockIdx.x & (kSlices - 1u))], (int32_t)c, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-  }
+  (void)G;
 }
 
 }  // namespace nkroute
@@ -644,10 +677,12 @@ NK_ROUTE_SELECT(2048, 512, 8, 4)
 //     experts in order get ceil(count / 64) 64-row blocks, ceil(count / 16)
 //     16-row tiles and ceil(blocks / 2) block pairs, an exclusive scan over
 //     the experts with each thread summing a contiguous run of them;
-//  b. expert me's histogram row hist[me][0 .. G) (W <= 8) as an exclusive scan, 256
-//     route_select workgroups a round: workgroup g's bucket entries
-//     bucket[me][g][0 .. hist[me][g]) are copied to rows
-//     block_off[me] * 64 + prefix(g) + 0, 1, ...; counts[me] = the row total;
+//  b. (the shared expert: every token in order) expert me's count in each
+//     route_select workgroup g (of G, W tokens
+//     each, W <= 8), v_g = hist[g][me + 1] - hist[g][me], as an exclusive
+//     scan over g, 256 workgroups a round: workgroup g's entries
+//     bucket[g][hist[g][me] ..][0 .. v_g) are copied to rows
+//     block_off[me] * 64 + prefix(g) + 0, 1, ...; counts[me] = the total;
 //  c. expert me's sorted_expert blocks, tile_map and pair_map entries, and
 //     its padding rows (Ktot << 24) | T after its routes;
 //  d. a grid-stride share of the unused blocks: sorted_expert -1, every row
@@ -658,7 +693,7 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_sort_route_gfx950(
     const int32_t* __restrict__ hist, const int32_t* __restrict__ bucket, const int32_t* __restrict__ cslice,
     int32_t* __restrict__ counts, int32_t* __restrict__ sorted_ids, int32_t* __restrict__ sorted_expert,
     int32_t* __restrict__ tile_map, int32_t* __restrict__ pair_map, int32_t* __restrict__ num_valid,
-    uint32_t T, uint32_t Ktot, uint32_t Etot, uint32_t G, uint32_t W, uint32_t cap_blocks) {
+    uint32_t T, uint32_t Ktot, uint32_t Etot, uint32_t S, uint32_t G, uint32_t W, uint32_t cap_blocks) {
   extern __shared__ uint32_t lds[];
   uint32_t* cnt = lds;                        // [Etot]
   uint32_t* block_off = cnt + Etot;           // [Etot + 1]
@@ -670,14 +705,22 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_sort_route_gfx950(
   static_assert(kSlices == 8u, "two 16-byte loads per expert");
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, me = blockIdx.x;
   if (Etot == 0u || Etot > 1024u || me >= Etot || W == 0u || W > 8u) return;
-  // the first kRounds rounds of expert me's histogram row and the slice
+  // the first kRounds rounds of expert me's list offsets and the slice
   // counters of experts tid, tid + 256, ..., all requested before the first
   // wait
   constexpr uint32_t kRounds = 4;
-  const int32_t* row = hist + (size_t)me * G;
-  uint32_t vpre[kRounds];
+  const uint32_t hstride = Etot + 1u, dc = W * Ktot;  // a workgroup's offsets row, its list length
+  const int32_t* hcol = hist + me;                     // hist[g][me] at hcol + g * hstride
+  uint32_t plo[kRounds], phi[kRounds];
 #pragma unroll
-  for (uint32_t i = 0; i < kRounds; ++i) vpre[i] = tid + 256u * i < G ? (uint32_t)row[tid + 256u * i] : 0u;
+  for (uint32_t i = 0; i < kRounds; ++i) {
+    const uint32_t g = tid + 256u * i;
+    plo[i] = phi[i] = 0u;
+    if (g < G) {
+      plo[i] = (uint32_t)hcol[(size_t)g * hstride];
+      phi[i] = (uint32_t)hcol[(size_t)g * hstride + 1u];
+    }
+  }
   uint32_t cv[4];
 #pragma unroll
   for (uint32_t i = 0; i < 4u; ++i) {
@@ -740,26 +783,35 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_sort_route_gfx950(
     if (me == 0 && tid == 0) { num_valid[0] = 0; num_valid[1] = -1; num_valid[2] = 0; num_valid[3] = 0; }
     return;
   }
-  // b. expert me's routes, in route_select workgroup order (= token order)
+  // b. expert me's routes, in route_select workgroup order (= token order).
+  // The shared expert (S = 1, the last one) has every token once, in slot
+  // Ktot - 1: its rows are the tokens in order, written without the lists.
   const uint32_t rbase = block_off[me] * 64u;
   uint32_t carry = 0u;
-  for (uint32_t g0 = 0; g0 < G; g0 += 256u) {  // uniform trip count
+  const bool shared = S != 0u && me == Etot - 1u;
+  if (shared) {
+    const uint32_t slot = (Ktot - 1u) << 24;
+    for (uint32_t t = tid; t < T; t += 256u)
+      if (rbase + t < cap_rows) sorted_ids[rbase + t] = (int32_t)(slot | t);
+    carry = T;
+  }
+  for (uint32_t g0 = 0; g0 < (shared ? 0u : G); g0 += 256u) {  // uniform trip count
     const uint32_t g = g0 + tid;
-    uint32_t v = 0u;
+    uint32_t lo = 0u, hi = 0u;
     if (g0 < 256u * kRounds) {
 #pragma unroll
       for (uint32_t i = 0; i < kRounds; ++i)
-        if (g0 == 256u * i) v = vpre[i];
+        if (g0 == 256u * i) { lo = plo[i]; hi = phi[i]; }
     } else if (g < G) {
-      v = (uint32_t)row[g];
+      lo = (uint32_t)hcol[(size_t)g * hstride];
+      hi = (uint32_t)hcol[(size_t)g * hstride + 1u];
     }
-    // the round's bucket entries, requested before the scan's barrier
-    const int32_t* src = bucket + ((size_t)me * G + g) * W;
-    int4 q0 = make_int4(0, 0, 0, 0), q1 = make_int4(0, 0, 0, 0);
-    if (v != 0u) {  // the whole bucket (W <= 8 entries) in one or two 16-byte loads
-      q0 = *reinterpret_cast<const int4*>(src);
-      if (W > 4u) q1 = *reinterpret_cast<const int4*>(src + 4);
-    }
+    const uint32_t v = min(hi - lo, W);  // (hi >= lo for route_select's offsets)
+    // the round's list entries, requested before the scan's barrier
+    const int32_t* src = bucket + (size_t)g * dc + lo;
+    int32_t ent[8];
+#pragma unroll
+    for (uint32_t i = 0; i < 8u; ++i) ent[i] = i < v ? src[i] : 0;
     uint32_t inc = v;
 #pragma unroll
     for (uint32_t off = 1; off < 64u; off <<= 1) {
@@ -780,7 +832,6 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_sort_route_gfx950(
     }
     if (v != 0u) {
       const uint32_t dst = rbase + before + inc - v;
-      const int32_t ent[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
       for (uint32_t i = 0; i < 8u; ++i)
         if (i < v && dst + i < cap_rows) sorted_ids[dst + i] = ent[i];

@@ -261,9 +261,10 @@ def tensor_table(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> dic
     else:
         specs += [TensorSpec("screen", "f32", (screen_splits(cfg), T, screen_row_pad(cfg)), "temporary"),
                   TensorSpec("route_wsq", "f32", (screen_splits(cfg), screen_row_pad(cfg)), "temporary"),
-                  # per route_select workgroup: expert histogram, sorted-id buckets
-                  TensorSpec("route_hist", "i32", (cfg.Etot, screen_groups(cfg)), "temporary"),
-                  TensorSpec("route_bucket", "i32", (cfg.Etot, screen_groups(cfg), screen_tokens(cfg)), "temporary"),
+                  # per route_select workgroup: its routes' sorted-id entries grouped
+                  # by expert, and the groups' offsets (last entry the route count)
+                  TensorSpec("route_hist", "i32", (screen_groups(cfg), cfg.Etot + 1), "temporary"),
+                  TensorSpec("route_bucket", "i32", (screen_groups(cfg), screen_tokens(cfg) * cfg.Ktot), "temporary"),
                   # expert totals in ROUTE_SLICES atomic counters each (cleared by route_screen)
                   TensorSpec("route_slices", "i32", (cfg.Etot, ROUTE_SLICES), "temporary")]
     if path in ("stream", "fused"):
@@ -346,7 +347,7 @@ def _screen_front(cfg: MoEConfig) -> list[dict]:
              grid=(cfg.Etot, 1, 1), block=(256, 1, 1), lds=4 * 20, dyn=4 * (4 * cfg.Etot + 3),
              args=["route_hist", "route_bucket", "route_slices", "expert_counts", "sorted_ids", "sorted_expert",
                    "tile_map", "pair_map", "num_valid",
-                   u(T), u(cfg.Ktot), u(cfg.Etot), u(G), u(Wt), u(cfg.cap_blocks)],
+                   u(T), u(cfg.Ktot), u(cfg.Etot), u(cfg.S), u(G), u(Wt), u(cfg.cap_blocks)],
              reads=["route_hist", "route_bucket", "route_slices"],
              writes=["expert_counts", "sorted_ids", "sorted_expert", "tile_map", "pair_map", "num_valid"],
              refs=["kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112",

@@ -264,8 +264,8 @@ __device__ __forceinline__ void route_screen(const uint16_t* __restrict__ x, con
 //  5. per workgroup g: its routes' sorted-id entries (slot << 24) | token
 //     as one list bucket[g][..] grouped by expert (token order within an
 //     expert), the list's expert offsets hist[g][0 .. E + S] (an exclusive
-//     scan of the per-expert counts, last entry the total), and the nonzero
-//     counts added into cslice[e][g mod kSlices].
+//     scan of the per-expert counts, last entry the total), and the routed
+//     experts' nonzero counts added into cslice[e][g mod kSlices].
 template <uint32_t NJ, uint32_t EMAX, uint32_t W, uint32_t WPT>
 __device__ __forceinline__ void route_select(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
@@ -602,7 +602,9 @@ __device__ __forceinline__ void route_select(
       s_pre[e] = run;
       hrow[e] = (int32_t)run;
     }
-    if (e < rows && cnt[i] != 0u)
+    // a routed expert's count into its slice g mod kSlices (the shared
+    // expert's total is T, which sort_route knows)
+    if (e < E && cnt[i] != 0u)
       __hip_atomic_fetch_add(&cslice[e * kSlices + (blockIdx.x & (kSlices - 1u))], (int32_t)cnt[i],
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     run += cnt[i];
@@ -672,7 +674,8 @@ NK_ROUTE_SELECT(2048, 512, 8, 4)
 // ---------------------------------------------------------------------------
 // sort_route: workgroup me (256 threads) of a grid of exactly Etot, one per
 // expert:
-//  a. every expert's total = the sum of its kSlices slice counters, and the
+//  a. every routed expert's total = the sum of its kSlices slice counters
+//     (the shared expert's: T), and the
 //     expert layout from the totals (every workgroup computes the same one):
 //     experts in order get ceil(count / 64) 64-row blocks, ceil(count / 16)
 //     16-row tiles and ceil(blocks / 2) block pairs, an exclusive scan over
@@ -733,8 +736,10 @@ NK_KERNEL __launch_bounds__(256) void netra_moe_sort_route_gfx950(
     }
   }
 #pragma unroll
-  for (uint32_t i = 0; i < 4u; ++i)
-    if (tid + 256u * i < Etot) cnt[tid + 256u * i] = cv[i];
+  for (uint32_t i = 0; i < 4u; ++i) {
+    const uint32_t e = tid + 256u * i;
+    if (e < Etot) cnt[e] = S != 0u && e == Etot - 1u ? T : cv[i];  // the shared expert: every token
+  }
   __syncthreads();
   // a. layout
   const uint32_t ept = (Etot + 255u) / 256u, e0 = tid * ept;

@@ -176,6 +176,32 @@ def test_prefill_engines_use_the_screen_front_end(tmp_path):
     assert gate_up["launch"]["block"] == [512, 1, 1] and gate_up["launch"]["lds_bytes"] <= 160 * 1024
 
 
+@pytest.mark.parametrize("T,H,E,shape", [
+    (4096, 2048, 256, (8, 1)), (2048, 2048, 256, (8, 1)), (1024, 2048, 256, (8, 2)), (512, 2048, 256, (8, 4)),
+    (300, 2048, 256, (8, 4)), (512, 1024, 256, (8, 2)), (512, 512, 256, (4, 1)), (768, 2048, 384, (8, 2)),
+])
+def test_route_select_waves_per_token(T, H, E, shape):
+    """Waves per token: the most of 1, 2, 4 that keeps T * WPT <= 2048 and
+    WPT <= H / 512; the kernel symbol, block, grid and the per-workgroup list
+    tensors follow from (W, WPT)."""
+    from netra_moe.config import MoEConfig
+    from netra_moe.engine import screen_groups, screen_tokens, screen_waves, screen_waves_per_token, tensor_table
+    cfg = MoEConfig(f"wpt_t{T}_h{H}_e{E}", T=T, H=H, E=E, K=8, I=512, S=1, seed=1)
+    assert (screen_waves(cfg), screen_waves_per_token(cfg)) == shape
+    W, WPT = shape
+    sel = next(o for o in operations(cfg, "tile", "screen") if o["name"] == "moe.route_select")
+    emax = 256 if E <= 256 else 512
+    assert sel["symbol"] == f"netra_moe_route_select_h{H}_e{emax}_w{W}x{WPT}_gfx950"
+    assert sel["block"] == (64 * W, 1, 1) and sel["grid"] == (screen_groups(cfg), 1, 1)
+    assert screen_tokens(cfg) == W // WPT and screen_groups(cfg) == -(-T // (W // WPT))
+    tt = tensor_table(cfg, "tile", "screen")
+    assert tt["route_hist"].shape == (screen_groups(cfg), cfg.Etot + 1)
+    assert tt["route_bucket"].shape == (screen_groups(cfg), screen_tokens(cfg) * cfg.Ktot)
+    assert tt["route_slices"].shape == (cfg.Etot, 8)
+    sort = next(o for o in operations(cfg, "tile", "screen") if o["name"] == "moe.sort_route")
+    assert sort["grid"] == (cfg.Etot, 1, 1)  # the kernel's unused-block stride assumes exactly Etot
+
+
 def test_profiles_select_exact_shapes_and_refuse_neighbours():
     p64 = nm.profile_for(nm.BASELINE_CONFIGS["decode_t64"])
     p1 = nm.profile_for(nm.BASELINE_CONFIGS["decode_t1"])

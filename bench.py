@@ -199,7 +199,8 @@ def cpu_baseline(cfg, act_cpu, w_host, threads: int, min_seconds: float):
 # bridges on MI350X (docs/notes/gfx950-qwen36-fp8-kernels.md lines 78, 261,
 # 301, 563, 643), at the shapes they were quoted for. (Its SiLU-quant and
 # shared-gate notes also give kernel-trace figures: 2.742 us, line 80, and a
-# serving-trace median of 3.160 us, line 263.)
+# serving-trace median of 3.160 us, line 263.) The M768 prefill pair has no
+# published per-launch time (its notes give serving throughput only).
 REFERENCE_BRIDGE_US = {"router_m1": 6.24, "router_m16": 6.32, "shared_gate_m1": 5.96,
                        "silu_mul_quant_m1": 2.78, "gate_up_m1": 8.96, "down_reduce_m1": 10.28}
 
@@ -281,10 +282,36 @@ def bridge_timings(torch, dev, launches: int = 200, copies: int = 12) -> dict:
                            lambda w: B.launch("netra_qwen36_moe_down_reduce", P(hq), P(hs), P(w[2]), P(w[3]),
                                               P(wts9), P(ids9), P(out), 1, stream), True),
     }
+    # The M768 pair (producer + reducer) at its one shape: 768 tokens, their
+    # routing and AITER sorted format produced by this build's own screen front
+    # end (a T = 768 layer call with its routing tensors exposed).
+    from netra_moe.config import MoEConfig
+    from netra_moe.layer import MoELayer
+    m768 = MoEConfig("m768", T=768, H=H, E=E, K=K - 1, I=I, S=1, seed=1105)
+    rw = (torch.randn((E + 1, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    lay = MoELayer(m768, {"router_w": rw, "router_bias": torch.zeros(E, device=dev),
+                          "w13": fp8(E + 1, 2 * I, H), "w13_scale": w13s, "w2": fp8(E + 1, H, I), "w2_scale": w2s},
+                   graph=False, expose=("sorted_ids", "sorted_expert", "num_valid", "topk_weights", "x_q", "x_scale"))
+    lay.x.copy_(torch.randn((768, H), generator=g, device=dev).to(torch.bfloat16))
+    lay.forward()
+    torch.cuda.synchronize()
+    mb = {n: lay.buffer(n).clone() for n in ("sorted_ids", "sorted_expert", "num_valid", "topk_weights", "x_q",
+                                             "x_scale")}
+    lay.close()
+    half = 768 * K + m768.cap_blocks
+    m_sw = torch.zeros(m768.cap_rows, device=dev)  # sorted weights: unused by the producer, as in the reference
+    m_rs = torch.empty((m768.cap_rows, I // 128), device=dev)
+    m_parts = torch.empty((2, half, H), dtype=torch.float16, device=dev)
+    m_out = torch.empty((768, H), dtype=torch.bfloat16, device=dev)
+    cases["prefill_m768"] = (
+        "netra_moe_prefill_m768",
+        lambda w: B.launch("netra_moe_prefill_m768", P(mb["x_q"]), P(mb["x_scale"]), P(w[0]), P(w[1]), P(w[2]),
+                           P(w[3]), P(mb["sorted_ids"]), P(m_sw), P(mb["sorted_expert"]), P(mb["num_valid"]),
+                           P(mb["topk_weights"]), P(m_rs), P(m_parts), P(m_out), stream), True)
     res = {}
     for name, (fam, fn, streams_weights) in cases.items():
         B.check(fam, B.load(fam))
-        r = {"hot_us": batch_us(fn, hot_w), "reference_mi350x_us": REFERENCE_BRIDGE_US[name]}
+        r = {"hot_us": batch_us(fn, hot_w), "reference_mi350x_us": REFERENCE_BRIDGE_US.get(name)}
         if streams_weights:
             r["cold_us"] = batch_us(fn, cold_w)
         B.check(fam, B.unload(fam))

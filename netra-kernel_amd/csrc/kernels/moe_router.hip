@@ -107,37 +107,66 @@ __device__ __forceinline__ void router(const uint16_t* __restrict__ x, const uin
   }
   __syncthreads();
 
-  // The row slice is widened to fp32 once; each token is then one sequential
-  // fmaf chain over LDS reads (tokens one after another keeps the register
-  // footprint at the slice plus a few reads).
-  float wf[8 * NJ];
+  // Each token is one sequential fmaf chain over LDS reads; the NT tokens'
+  // chains run interleaved (independent accumulators), and each weight is
+  // widened from bf16 where the chains read it, once for all NT tokens (the
+  // slice stays packed: 64 VGPRs at H = 2048). The x values of block j + 1
+  // are read while block j's fmas run. With several tokens, empty asm
+  // statements pin the order: one claims to rewrite block j's packed weights
+  // (with a memory clobber, so no later block's reads or widenings move up),
+  // the others claim to rewrite every accumulator after block j (so the
+  // compiler cannot run the chains one after another, holding 128 widened
+  // weights: that spilled at NT = 4).
+  float acc[NT];
+  float4 lo[NT], hi[NT];
+#pragma unroll
+  for (uint32_t k = 0; k < NT; ++k) {
+    acc[k] = 0.0f;
+    lo[k] = s_x[k * (H / 4u) + s];  // lo at 32 j, hi at 32 j + 16 (the staging order)
+    hi[k] = s_x[k * (H / 4u) + s + 16u];
+  }
 #pragma unroll
   for (uint32_t j = 0; j < NJ; ++j) {
-    wf[8 * j + 0] = nk::bf16_lo(wv[j].x);
-    wf[8 * j + 1] = nk::bf16_hi(wv[j].x);
-    wf[8 * j + 2] = nk::bf16_lo(wv[j].y);
-    wf[8 * j + 3] = nk::bf16_hi(wv[j].y);
-    wf[8 * j + 4] = nk::bf16_lo(wv[j].z);
-    wf[8 * j + 5] = nk::bf16_hi(wv[j].z);
-    wf[8 * j + 6] = nk::bf16_lo(wv[j].w);
-    wf[8 * j + 7] = nk::bf16_hi(wv[j].w);
-  }
-#pragma unroll 1
-  for (uint32_t k = 0; k < NT; ++k) {
-    const float4* xk = s_x + k * (H / 4u) + s;  // lo at 32 j, hi at 32 j + 16 (the staging order)
-    float a = 0.0f;
+    float4 nlo[NT], nhi[NT];
+    if (j + 1u < NJ) {
 #pragma unroll
-    for (uint32_t j = 0; j < NJ; ++j) {
-      const float4 lo = xk[32u * j], hi = xk[32u * j + 16u];
-      a = fmaf(lo.x, wf[8 * j + 0], a);
-      a = fmaf(lo.y, wf[8 * j + 1], a);
-      a = fmaf(lo.z, wf[8 * j + 2], a);
-      a = fmaf(lo.w, wf[8 * j + 3], a);
-      a = fmaf(hi.x, wf[8 * j + 4], a);
-      a = fmaf(hi.y, wf[8 * j + 5], a);
-      a = fmaf(hi.z, wf[8 * j + 6], a);
-      a = fmaf(hi.w, wf[8 * j + 7], a);
+      for (uint32_t k = 0; k < NT; ++k) {
+        nlo[k] = s_x[k * (H / 4u) + s + 32u * (j + 1u)];
+        nhi[k] = s_x[k * (H / 4u) + s + 32u * (j + 1u) + 16u];
+      }
     }
+    uint4 wj = wv[j];
+    if constexpr (NT > 1) asm volatile("" : "+v"(wj.x), "+v"(wj.y), "+v"(wj.z), "+v"(wj.w) : : "memory");
+    const float w8[8] = {nk::bf16_lo(wj.x), nk::bf16_hi(wj.x), nk::bf16_lo(wj.y), nk::bf16_hi(wj.y),
+                         nk::bf16_lo(wj.z), nk::bf16_hi(wj.z), nk::bf16_lo(wj.w), nk::bf16_hi(wj.w)};
+#pragma unroll
+    for (uint32_t k = 0; k < NT; ++k) {
+      float a = acc[k];
+      a = fmaf(lo[k].x, w8[0], a);
+      a = fmaf(lo[k].y, w8[1], a);
+      a = fmaf(lo[k].z, w8[2], a);
+      a = fmaf(lo[k].w, w8[3], a);
+      a = fmaf(hi[k].x, w8[4], a);
+      a = fmaf(hi[k].y, w8[5], a);
+      a = fmaf(hi[k].z, w8[6], a);
+      a = fmaf(hi[k].w, w8[7], a);
+      acc[k] = a;
+    }
+    if (j + 1u < NJ) {
+#pragma unroll
+      for (uint32_t k = 0; k < NT; ++k) {
+        lo[k] = nlo[k];
+        hi[k] = nhi[k];
+      }
+    }
+    // every chain has taken block j here: the tokens stay interleaved
+    if constexpr (NT > 1)
+#pragma unroll
+      for (uint32_t k = 0; k < NT; ++k) asm volatile("" : "+v"(acc[k]));
+  }
+#pragma unroll
+  for (uint32_t k = 0; k < NT; ++k) {
+    float a = acc[k];
     a = a + __shfl_down(a, 8u, 16);
     a = a + __shfl_down(a, 4u, 16);
     a = a + __shfl_down(a, 2u, 16);

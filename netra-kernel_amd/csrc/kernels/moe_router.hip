@@ -250,6 +250,9 @@ __device__ __forceinline__ void topk_select(const uint16_t* __restrict__ lrow, c
     lg[j] = logit_f32<kCoherent>(lrow + e);
     bs[j] = bias[e];
   }
+  // the shared gate's logit (column E, present when S = 1) joins the same
+  // batch; with S = 0 the load reads column E - 1 and is not used
+  const float sg = logit_f32<kCoherent>(lrow + (E - 1u + (S != 0 ? 1u : 0u)));
   // Key of expert e = lane + 64 j: its code in the high word, ~e in the low
   // word (larger key: larger z, then lower expert index; 0: absent). Each
   // lane sorts its P keys once (descending; networks checked by the 0-1
@@ -303,7 +306,7 @@ __device__ __forceinline__ void topk_select(const uint16_t* __restrict__ lrow, c
   weight = ex / sum;
   if (S != 0 && lane == K) {
     id = E;
-    weight = nk::bf16_f32(nk::bf16_rne(nk::sigmoid(logit_f32<kCoherent>(lrow + E))));
+    weight = nk::bf16_f32(nk::bf16_rne(nk::sigmoid(sg)));
   }
 }
 

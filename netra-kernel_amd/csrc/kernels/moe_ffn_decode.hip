@@ -94,6 +94,14 @@ __device__ __forceinline__ uint32_t nth_bit(unsigned long long m, uint32_t j) {
   return m ? (uint32_t)__ffsll((long long)m) - 1u : 64u;
 }
 
+// nth_bit for a wave-uniform m and j, every lane active: lane l holds bit l
+// and counts the set bits below it, so one ballot finds the position.
+__device__ __forceinline__ uint32_t nth_bit_wave(unsigned long long m, uint32_t j, uint32_t lane) {
+  const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+  const unsigned long long hit = __ballot(((m >> lane) & 1ull) != 0ull && below == j);
+  return hit ? (uint32_t)__ffsll((long long)hit) - 1u : 64u;
+}
+
 // Slot of expert e in token t's route list, or Ktot.
 __device__ __forceinline__ uint32_t slot_of(const int32_t* s_ids, uint32_t t, uint32_t Ktot, uint32_t e) {
   for (uint32_t s = 0; s < Ktot; ++s)
@@ -174,7 +182,10 @@ __device__ __forceinline__ void ffn_gate_up(
     return;  // host-checked
 
   // ---- routes into LDS, routing bitmask ------------------------------------------------------
-  if (tid < Etot) s_mask[tid] = 0ull;
+  // (every entry cleared: the narrow presence ballots read all of them
+  // unconditionally, entries past Etot as zero)
+  static_assert(kMaxE == kThreads, "one mask entry per thread");
+  s_mask[tid] = 0ull;
   uint32_t topk_id = 0;  // narrow: wave t lane s < Ktot, token t's slot s
   float topk_wt = 0.0f;
   if constexpr (kStageAll) {
@@ -295,19 +306,34 @@ __device__ __forceinline__ void ffn_gate_up(
   constexpr uint32_t kChunks = kStageAll ? kMaxE / 64u : 1u;
   unsigned long long used[kChunks];
   uint32_t before[kChunks + 1];
-  auto used_expert = [&](uint32_t b) __attribute__((always_inline)) {  // the b-th expert with a route (uniform)
-    uint32_t e = 0;
+  // the b-th expert with a route (b < the count, uniform, every lane active):
+  // the last chunk c with before[c] <= b (before[] does not decrease, so the
+  // test holds for a prefix of the chunks) by a chain of scalar selects (the
+  // empty asm keeps it a chain rather than an indexed register read), then
+  // its bit by one ballot
+  auto used_expert = [&](uint32_t b) __attribute__((always_inline)) {
+    unsigned long long m = used[0];
+    uint32_t c0 = 0, b0 = 0;
 #pragma unroll
-    for (uint32_t c = 0; c < kChunks; ++c)
-      if (b >= before[c] && b < before[c + 1]) e = 64u * c + nth_bit(used[c], b - before[c]);
-    return e;
+    for (uint32_t c = 1; c < kChunks; ++c) {
+      const bool in = b >= before[c];
+      m = in ? used[c] : m;
+      c0 = in ? 64u * c : c0;
+      b0 = in ? before[c] : b0;
+      asm volatile("" : "+s"(m), "+s"(c0), "+s"(b0));
+    }
+    return c0 + nth_bit_wave(m, b - b0, lane);
   };
   uint32_t ntile = 0, e_pre = 0xffffffffu;
   if constexpr (kStageAll) {
+    // all chunks' mask entries read before the first ballot: one LDS wait
+    unsigned long long mv[kChunks];
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks; ++c) mv[c] = s_mask[64u * c + lane];
     before[0] = 0;
 #pragma unroll
     for (uint32_t c = 0; c < kChunks; ++c) {
-      used[c] = __ballot(64u * c + lane < Etot && s_mask[64u * c + lane] != 0ull);
+      used[c] = __ballot(mv[c] != 0ull);
       before[c + 1] = before[c] + (uint32_t)__popcll(used[c]);
     }
     ntile = before[kChunks];

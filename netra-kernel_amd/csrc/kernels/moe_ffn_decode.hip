@@ -181,6 +181,28 @@ __device__ __forceinline__ void ffn_gate_up(
       K > E)
     return;  // host-checked
 
+  // Step s of item `item` (tile expert e): 16-column item c0 + s / NA, K blocks
+  // kbw + ((s + rot) % NA) * kCH ..  Rotating the K order by the item spreads
+  // the workgroups running together over different offsets of their experts'
+  // weights (same-offset streams of 2 MiB-strided experts share HBM channels).
+  const uint32_t ca = wave % CA, sa = wave / CA;
+  const uint32_t kbw = sa * KBA;  // this wave's first K block
+  auto issue_at = [&](GateUpStep<kCH>& st, uint32_t e, uint32_t item, uint32_t s) __attribute__((always_inline)) {
+    const uint8_t* w13e = w13 + (size_t)e * 2u * I * H;
+    const float* w13se = w13s + (size_t)e * (2u * I / 128u) * KB;
+    const uint32_t c = ((item % GA) * CA + ca) * P + s / NA, rot = item % NA;
+#pragma unroll
+    for (uint32_t i = 0; i < kCH; ++i) {
+      const uint32_t kb = kbw + ((s + rot) % NA) * kCH + i;
+      st.g[i] = nk::load_tile_operand_once(nk::tile_base(w13e, 2u * c, kb, KB), lane);
+      st.u[i] = nk::load_tile_operand_once(nk::tile_base(w13e, 2u * c + 1u, kb, KB), lane);
+    }
+    const uint32_t sl = lane < 2u * KB ? lane : 0u;
+    st.ws = w13se[((sl < KB ? c : I / 16u + c) >> 3) * KB + (sl < KB ? sl : sl - KB)];
+  };
+  GateUpStep<kCH> b0, b1;
+  uint32_t e_pre = 0xffffffffu;  // the expert of the steps issued in the prologue
+
   // ---- routes into LDS, routing bitmask ------------------------------------------------------
   // (every entry cleared: the narrow presence ballots read all of them
   // unconditionally, entries past Etot as zero)
@@ -207,6 +229,15 @@ __device__ __forceinline__ void ffn_gate_up(
       nklds::copy4((uint32_t)__builtin_amdgcn_readfirstlane((int)nklds::lds_offset(&s_xs[64u * c])), rxs,
                    ((i & 15u) * KB + (i >> 4)) * 4u, 0u);
     }
+    // One token with a shared expert: the used experts are the K selected
+    // (distinct, below E) and E, so in ascending order E is tile Ktot - 1,
+    // known before the selection; that tile's first item steps go out now,
+    // under the logits loads (the waits below cover them too)
+    if (T == 1u && S != 0u && blockIdx.x / GA == Ktot - 1u) {  // uniform
+      e_pre = E;
+      issue_at(b0, E, blockIdx.x, 0u);
+      if constexpr (NS == 2) issue_at(b1, E, blockIdx.x, 1u);
+    }
     if (wave < T) {
       topk_select_any(logits + (size_t)wave * Etot, bias, E, K, S, lane, topk_id, topk_wt);
       if (lane < Ktot) s_ids[wave * Ktot + lane] = (int32_t)topk_id;
@@ -229,26 +260,6 @@ __device__ __forceinline__ void ffn_gate_up(
   }
   lds_barrier();
 
-  // Step s of item `item` (tile expert e): 16-column item c0 + s / NA, K blocks
-  // kbw + ((s + rot) % NA) * kCH ..  Rotating the K order by the item spreads
-  // the workgroups running together over different offsets of their experts'
-  // weights (same-offset streams of 2 MiB-strided experts share HBM channels).
-  const uint32_t ca = wave % CA, sa = wave / CA;
-  const uint32_t kbw = sa * KBA;  // this wave's first K block
-  auto issue_at = [&](GateUpStep<kCH>& st, uint32_t e, uint32_t item, uint32_t s) __attribute__((always_inline)) {
-    const uint8_t* w13e = w13 + (size_t)e * 2u * I * H;
-    const float* w13se = w13s + (size_t)e * (2u * I / 128u) * KB;
-    const uint32_t c = ((item % GA) * CA + ca) * P + s / NA, rot = item % NA;
-#pragma unroll
-    for (uint32_t i = 0; i < kCH; ++i) {
-      const uint32_t kb = kbw + ((s + rot) % NA) * kCH + i;
-      st.g[i] = nk::load_tile_operand_once(nk::tile_base(w13e, 2u * c, kb, KB), lane);
-      st.u[i] = nk::load_tile_operand_once(nk::tile_base(w13e, 2u * c + 1u, kb, KB), lane);
-    }
-    const uint32_t sl = lane < 2u * KB ? lane : 0u;
-    st.ws = w13se[((sl < KB ? c : I / 16u + c) >> 3) * KB + (sl < KB ? sl : sl - KB)];
-  };
-  GateUpStep<kCH> b0, b1;
   // wide: the x rows of sub-tile k of expert e, loaded into registers
   // (stage_load: rows past e's routes zero) and then stored into s_a in the
   // MFMA operand layout with their scales in s_xs (stage_store; the caller
@@ -324,7 +335,7 @@ __device__ __forceinline__ void ffn_gate_up(
     }
     return c0 + nth_bit_wave(m, b - b0, lane);
   };
-  uint32_t ntile = 0, e_pre = 0xffffffffu;
+  uint32_t ntile = 0;
   if constexpr (kStageAll) {
     // all chunks' mask entries read before the first ballot: one LDS wait
     unsigned long long mv[kChunks];
@@ -337,7 +348,7 @@ __device__ __forceinline__ void ffn_gate_up(
       before[c + 1] = before[c] + (uint32_t)__popcll(used[c]);
     }
     ntile = before[kChunks];
-    if (blockIdx.x / GA < ntile) {
+    if (e_pre == 0xffffffffu && blockIdx.x / GA < ntile) {
       e_pre = used_expert(blockIdx.x / GA);
       issue_at(b0, e_pre, blockIdx.x, 0u);
       if constexpr (NS == 2) issue_at(b1, e_pre, blockIdx.x, 1u);

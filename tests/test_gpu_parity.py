@@ -69,6 +69,14 @@ EXTRA_CONFIGS = {
                               seed=1114),
     # the single-token down with sixteen routes (two tiles per wave), no shared expert
     "single_k16": MoEConfig("single_k16", T=1, H=2048, E=256, K=16, I=512, S=0, seed=1111),
+    # one token with a shared expert on the other narrow shapes: its tile
+    # (Ktot - 1) issued before the selection, the shared gate's logit loaded
+    # with the expert logits at 16 (one per lane), 384 (eight per lane) and
+    # 32 experts
+    "single_t1_h512": MoEConfig("single_t1_h512", T=1, H=512, E=16, K=2, I=256, S=1, seed=1121),
+    "single_t1_e384_k12": MoEConfig("single_t1_e384_k12", T=1, H=1024, E=384, K=12, I=1024, S=1,
+                                    seed=1122),
+    "single_t1_h4096": MoEConfig("single_t1_h4096", T=1, H=4096, E=32, K=4, I=256, S=1, seed=1123),
     # expert tails on the tile path: every token on experts 0, 1 and the shared
     # expert, so each holds T rows; a last block of at most 16 rows after an
     # even number of full blocks is computed by the pair before it (1 and 16

@@ -1,7 +1,7 @@
 """ctypes binding of the engine C ABI (include/netra_engine.h).
 
 The reference's callers bind the same ABI from Python through ctypes (the
-SGLang adapter; SURVEY of runtime/gfx950/engine/netra_engine.h:60-108). Errors
+SGLang adapter; reference runtime/gfx950/engine/netra_engine.h:60-108). Errors
 raise NetraError carrying the status and the engine's last_error text.
 """
 from __future__ import annotations

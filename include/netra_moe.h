@@ -63,6 +63,10 @@
 //   netra_moe_ffn_down_h2048_i512_single_gfx950(the same arguments)   T = 1,
 //       grid H/16, block 512: a workgroup owns 16 output columns across all
 //       routes and writes out itself (partial for inspection; counters unused)
+//   netra_moe_ffn_down_h<H>_i<I>_rows_gfx950(the same arguments)   grid 2048,
+//       block 512: the narrow gate/up's bf16 rows (requantised per tile, hq / hs
+//       written for inspection) through the wide down's items; the partials go
+//       to netra_moe_combine_gfx950 (counters and out unused); used for 5 <= T <= 8
 //   decode ("stream") GEMMs, H in {512,1024,2048,4096}, I in {256,512,1024,2048}:
 //   (every w13 below is in the gate/up-interleaved tile16x128 layout of
 //   netra_moe_pack_tiles_gate_up)

@@ -8,14 +8,16 @@
 //       tile_map, pair_map, num_valid, counts, hrows, hq, hs; T, E, K, S, CAP)
 //     wide reads topk_ids (logits, bias and topk_weights unused); narrow
 //     selects from logits + bias and writes topk_ids / topk_weights
-//   netra_moe_ffn_down_h<H>_i<I>_<wide|narrow>_gfx950(topk_weights, w2, w2s,
+//   netra_moe_ffn_down_h<H>_i<I>_<wide|narrow|rows>_gfx950(topk_weights, w2, w2s,
 //       sorted_ids, sorted_expert, tile_map, num_valid, hrows, hq, hs, partial,
 //       counters, out; T, E, K, S)
 // The narrow down combines in the kernel (the hand-off below); the wide one
 // leaves the fp32 route partials to netra_moe_combine_gfx950: with tens of
 // tokens the hand-off's combine work lands in the kernel's tail (57.9 us
 // against 46.2 us without it at T = 64 on one MI355X, more than the separate
-// combine launch costs).
+// combine launch costs). The rows down takes the narrow gate/up's bf16 rows
+// through the wide down's items and leaves the combine to the same kernel;
+// from five tokens it is the faster of the two after the narrow gate/up.
 //   block 512 (8 waves), any grid
 // Weights are read with non-temporal loads: every tile is read by one
 // workgroup per launch (the tiles of an expert with more than 16 routes by
@@ -229,11 +231,11 @@ __device__ __forceinline__ void ffn_gate_up(
       nklds::copy4((uint32_t)__builtin_amdgcn_readfirstlane((int)nklds::lds_offset(&s_xs[64u * c])), rxs,
                    ((i & 15u) * KB + (i >> 4)) * 4u, 0u);
     }
-    // One token with a shared expert: the used experts are the K selected
-    // (distinct, below E) and E, so in ascending order E is tile Ktot - 1,
-    // known before the selection; that tile's first item steps go out now,
-    // under the logits loads (the waits below cover them too)
-    if (T == 1u && S != 0u && blockIdx.x / GA == Ktot - 1u) {  // uniform
+    // With a shared expert, items 0 .. GA - 1 are the shared expert's tile
+    // (narrow_tile below), whose expert E is known before the selection: its
+    // first item steps go out now, under the logits loads (the waits below
+    // cover them too)
+    if (S != 0u && blockIdx.x < GA) {  // uniform
       e_pre = E;
       issue_at(b0, E, blockIdx.x, 0u);
       if constexpr (NS == 2) issue_at(b1, E, blockIdx.x, 1u);
@@ -336,6 +338,13 @@ __device__ __forceinline__ void ffn_gate_up(
     return c0 + nth_bit_wave(m, b - b0, lane);
   };
   uint32_t ntile = 0;
+  // narrow: the tile of item q. The shared expert's tile is the last one (E
+  // is the largest used id); with S = 1 it takes items 0 .. GA - 1 and the
+  // routed tiles follow in order, so its weights can be requested before the
+  // selection whatever T is. (Positions in the outputs use the tile itself.)
+  auto narrow_tile = [&](uint32_t q) __attribute__((always_inline)) {
+    return S == 0u ? q / GA : (q < GA ? ntile - 1u : q / GA - 1u);
+  };
   if constexpr (kStageAll) {
     // all chunks' mask entries read before the first ballot: one LDS wait
     unsigned long long mv[kChunks];
@@ -348,8 +357,8 @@ __device__ __forceinline__ void ffn_gate_up(
       before[c + 1] = before[c] + (uint32_t)__popcll(used[c]);
     }
     ntile = before[kChunks];
-    if (e_pre == 0xffffffffu && blockIdx.x / GA < ntile) {
-      e_pre = used_expert(blockIdx.x / GA);
+    if (e_pre == 0xffffffffu && blockIdx.x < ntile * GA) {
+      e_pre = used_expert(narrow_tile(blockIdx.x));
       issue_at(b0, e_pre, blockIdx.x, 0u);
       if constexpr (NS == 2) issue_at(b1, e_pre, blockIdx.x, 1u);
     }
@@ -472,7 +481,7 @@ __device__ __forceinline__ void ffn_gate_up(
     } else if (item >= ntile * GA) {
       break;
     }
-    const uint32_t g = item / GA, grp = item % GA;
+    const uint32_t g = kStageAll ? narrow_tile(item) : item / GA, grp = item % GA;
     uint32_t e, k, row0;  // the tile's expert, its sub-tile among e's rows and its sorted position
     if constexpr (kStageAll) {
       e = used_expert(g);
@@ -1094,3 +1103,29 @@ NK_FFN_PAIR(2048, 512, wide, 1, 1, 2, 2, 4, 2, 4, 1)
 NK_FFN_PAIR(2048, 512, narrow, 8, 4, 1, 4, 1, 1, 4, 1)
 NK_FFN_PAIR(4096, 256, wide, 1, 1, 2, 2, 2, 2, 4, 1)
 NK_FFN_PAIR(4096, 256, narrow, 8, 2, 2, 2, 1, 1, 4, 1)
+
+// Symbols netra_moe_ffn_down_h<H>_i<I>_rows_gfx950: the down for the narrow
+// gate/up's bf16 h rows (requantised per tile, as the narrow down does) with
+// the wide down's item shape and no hand-off, leaving fp32 route partials to
+// the combine kernel: at 2 .. 8 tokens the hand-off's K-split sums, counters
+// and last-arriver combines cost more than a separate combine launch.
+#define NK_FFN_DOWN_ROWS(HV, IV, SBV, CHD, WPED, PDV)                                                \
+  NK_KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WPED)))                      \
+  void netra_moe_ffn_down_h##HV##_i##IV##_rows_gfx950(                                             \
+      const float* __restrict__ topk_weights, const uint8_t* __restrict__ w2,                      \
+      const float* __restrict__ w2s, const int32_t* __restrict__ sorted_ids,                       \
+      const int32_t* __restrict__ sorted_expert, const int32_t* __restrict__ tile_map,             \
+      const int32_t* __restrict__ num_valid, const uint16_t* __restrict__ hrows,                   \
+      uint8_t* __restrict__ hq, float* __restrict__ hs, float* __restrict__ partial,               \
+      uint32_t* __restrict__ counters, uint16_t* __restrict__ out, uint32_t T, uint32_t E,         \
+      uint32_t K, uint32_t S) {                                                                    \
+    nkffn::ffn_down<HV / 128, IV / 128, SBV, CHD, true, PDV, false>(topk_weights, w2, w2s, sorted_ids, \
+                                                                 sorted_expert, tile_map, num_valid, \
+                                                                 hrows, hq, hs, partial, counters, out, \
+                                                                 T, E, K, S);                    \
+  }
+// (the wide pairs' down parameters above)
+NK_FFN_DOWN_ROWS(512, 256, 1, 2, 4, 1)
+NK_FFN_DOWN_ROWS(1024, 1024, 1, 1, 4, 1)
+NK_FFN_DOWN_ROWS(2048, 512, 1, 2, 4, 1)
+NK_FFN_DOWN_ROWS(4096, 256, 1, 2, 4, 1)

@@ -54,6 +54,7 @@ GEMM_PATHS = ("fused", "stream", "tile")
 FUSED_HI = ((512, 256), (1024, 1024), (2048, 512), (4096, 256))  # netra_moe_ffn_{gate_up,down}_h<H>_i<I>_<v>_gfx950
 FUSED_MAX_T = 64                     # one bitmask word per expert in the gate/up prologue
 FFN_NARROW_T = 8                     # T at or below which the decode FFN splits K (the "narrow" variant)
+NARROW_ROWS_DOWN_T = 5               # narrow T at or above which down takes the wide item shape + combine kernel
 FFN_COUNTERS = 64 * 64               # combine hand-off counters [token][column group] (kCounters)
 FFN_WIDE_P = {(512, 256): 2, (1024, 1024): 4, (2048, 512): 4, (4096, 256): 2}  # wide gate/up items per wave (PG)
 STREAM_H = (512, 1024, 2048, 4096)   # netra_moe_gate_up_stream_h<H>_c<CH>_gfx950
@@ -286,7 +287,7 @@ def op_names(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> tuple[s
     """Engine operation names of one layer call, in launch order."""
     path = resolve_path(cfg, path)
     if path == "fused":
-        return ("route", "gate_up", "down") + (("combine",) if ffn_variant(cfg) == "wide" else ())
+        return ("route", "gate_up", "down") + (("combine",) if down_variant(cfg) in ("wide", "rows") else ())
     front_ops = EXACT_FRONT_OPS if resolve_front(cfg, path, front) == "exact" else SCREEN_FRONT_OPS
     return front_ops + PATH_OPS[path]
 ROUTER_H = (512, 1024, 2048, 4096)   # netra_moe_router_h<H>_t<NT>_gfx950
@@ -409,10 +410,15 @@ SINGLE_DOWN = {(2048, 512)}
 
 def down_variant(cfg: MoEConfig) -> str:
     """single (one workgroup per 16 output columns across all routes, the
-    combine in the workgroup) for one token, else the FFN variant."""
+    combine in the workgroup) for one token; rows (the narrow gate/up's bf16
+    rows, the wide down's items, the combine kernel after it) from
+    NARROW_ROWS_DOWN_T narrow tokens (measured at H 2048, I 512 with HBM-cold
+    weights: 38.4 / 41.4 / 44.8 / 49.0 against 39.7 / 43.8 / 49.1 / 53.1 µs
+    at T = 5 .. 8, 35.2 against 34.0 at T = 4); else the FFN variant."""
     if cfg.T == 1 and (cfg.H, cfg.I) in SINGLE_DOWN and cfg.Ktot <= 16:
         return "single"
-    return ffn_variant(cfg)
+    v = ffn_variant(cfg)
+    return "rows" if v == "narrow" and cfg.T >= NARROW_ROWS_DOWN_T else v
 
 
 def ffn_lds_bytes(cfg: MoEConfig) -> tuple[int, int]:
@@ -423,7 +429,7 @@ def ffn_lds_bytes(cfg: MoEConfig) -> tuple[int, int]:
     red = 8 * 8 * 64 * 4 if narrow else 0
     gu = max(kb * 2048, red, 1024 * 4 + 513 * 4) + 64 * kb + (8 if narrow else 16 * (128 * FFN_WIDE_P[(cfg.H, cfg.I)] + 8)) * 2
     gu += 64 * 16 * 4 + 512 * 8 + 2 * 513 * 4 + 48 * 4
-    dn = max(kbi * 2048, red) + 64 * kbi + 4
+    dn = max(kbi * 2048, 0 if down_variant(cfg) == "rows" else red) + 64 * kbi + 4
     if down_variant(cfg) == "single":
         dn = 8 * 2 * cfg.I + 16 * 16 * 4
     return (gu + 255) // 256 * 256, (dn + 255) // 256 * 256
@@ -446,7 +452,8 @@ def ffn_grid(cfg: MoEConfig, op: str) -> int:
 def _fused_decode(cfg: MoEConfig) -> list[dict]:
     """Route (router + top-k; narrow: router logits only), gate/up with the sort
     (narrow: top-k and sort) as its prologue, down with the combine folded in
-    (narrow) or followed by the combine kernel (wide)."""
+    (one token, and narrow below NARROW_ROWS_DOWN_T tokens) or followed by the
+    combine kernel (wide, and narrow's rows down)."""
     T, H, I = cfg.T, cfg.H, cfg.I
     u = lambda v: ("u32", int(v))  # noqa: E731
     v = ffn_variant(cfg)
@@ -471,7 +478,9 @@ def _fused_decode(cfg: MoEConfig) -> list[dict]:
                    "kernels/gfx950/templates/moe/prefill/fused_splitk2/entry_routing.inc:27-112"]
              + (["runtime/gfx950/routing/decode/qwen36_shared_gate_append_bridge.hip:76-112"] if narrow else [])),
         dict(name="moe.down", symbol=f"netra_moe_ffn_down_h{H}_i{I}_{down_variant(cfg)}_gfx950",
-             grid=(H // 16 if down_variant(cfg) == "single" else ffn_grid(cfg, "down"), 1, 1), block=(512, 1, 1),
+             grid=(H // 16 if down_variant(cfg) == "single" else
+                   FFN_GRID[("down", "wide")] if down_variant(cfg) == "rows" else ffn_grid(cfg, "down"), 1, 1),
+             block=(512, 1, 1),
              lds=lds_dn, dyn=0,
              args=["topk_weights", "w2", "w2_scale", "sorted_ids", "sorted_expert", "tile_map", "num_valid",
                    "h_rows", "h_q", "h_scale", "partial", "ffn_counters", "out",
@@ -481,11 +490,14 @@ def _fused_decode(cfg: MoEConfig) -> list[dict]:
              writes=["h_q", "h_scale", "partial", "ffn_counters", "out"],
              refs=["kernels/gfx950/templates/moe/decode/down_reduce_mfma_2wave.inc:14-291"]),
     ]
-    if down_variant(cfg) == "single":  # no hand-off: the combine counters stay untouched
+    if down_variant(cfg) in ("single", "rows"):  # no hand-off: the combine counters stay untouched
         ops[-1]["reads"].remove("ffn_counters")
         ops[-1]["writes"].remove("ffn_counters")
-    if v == "wide":  # the wide down leaves the fp32 partials to the combine kernel
-        ops[-1]["writes"] = ["partial"]
+    if down_variant(cfg) == "rows":  # h requantised from the rows (copies for inspection), partials out
+        ops[-1]["writes"] = ["h_q", "h_scale", "partial"]
+    if down_variant(cfg) in ("wide", "rows"):  # fp32 partials for the combine kernel
+        if v == "wide":
+            ops[-1]["writes"] = ["partial"]
         ops.append(dict(name="moe.combine", symbol="netra_moe_combine_gfx950",
                         grid=((H + 1023) // 1024, T, 1), block=(256, 1, 1), lds=0, dyn=0,
                         args=["partial", "topk_weights", "out", u(T), u(H), u(cfg.Ktot)],
@@ -697,7 +709,7 @@ def op_typing(cfg: MoEConfig, op: dict, path: str) -> dict:
                    numerical={**num, "output_rounding": "silu_mul_rne_bf16_then_e4m3_per_128",
                               "reduction_order": "k_block_ascending_fixed"})
     elif kind == "down":
-        combined = path == "fused" and ffn_variant(cfg) == "narrow"
+        combined = path == "fused" and down_variant(cfg) in ("narrow", "single")
         typ = dict(shape=[cfg.routes, H, I],
                    dtypes=["fp8_e4m3", "fp8_e4m3", "fp32", "bf16" if combined else partial_dtype],
                    layouts=[h_layout, "tile16x128", "row_major" if combined else "route_partials_row_major"],

@@ -52,8 +52,8 @@
 //       xq, xs, w13, w13s, sorted_ids, sorted_expert, tile_map, pair_map, num_valid,
 //       counts, hrows bf16[CAPT*16,I], hq, hs; T, E, K, S, CAP)
 //       block 512, grid 256 (wide, or H = 4096) / 512 (narrow); the sort rebuilt in
-//       the prologue (its outputs as netra_moe_sort_gfx950's); wide (8 < T) reads
-//       ids and requantises h to hq / hs; narrow (T <= 8) runs the top-k from
+//       the prologue (its outputs as netra_moe_sort_gfx950's); wide (16 < T) reads
+//       ids and requantises h to hq / hs; narrow (T <= 16) runs the top-k from
 //       logits + bias itself (writing ids / weights) and writes bf16 h rows
 //   netra_moe_ffn_down_h<H>_i<I>_<wide|narrow>_gfx950(weights, w2, w2s, sorted_ids,
 //       sorted_expert, tile_map, num_valid, hrows, hq, hs, partial f32[T*Ktot,H],
@@ -66,7 +66,7 @@
 //   netra_moe_ffn_down_h<H>_i<I>_rows_gfx950(the same arguments)   grid 2048,
 //       block 512: the narrow gate/up's bf16 rows (requantised per tile, hq / hs
 //       written for inspection) through the wide down's items; the partials go
-//       to netra_moe_combine_gfx950 (counters and out unused); used for 5 <= T <= 8
+//       to netra_moe_combine_gfx950 (counters and out unused); used for 5 <= T <= 16
 //   decode ("stream") GEMMs, H in {512,1024,2048,4096}, I in {256,512,1024,2048}:
 //   (every w13 below is in the gate/up-interleaved tile16x128 layout of
 //   netra_moe_pack_tiles_gate_up)

@@ -1,5 +1,5 @@
 // Decode FFN for T <= 64 tokens after the route kernel (wide) or the router
-// logits kernel (narrow, T <= 8): the sort rebuilt in the gate/up prologue,
+// logits kernel (narrow, T <= 16): the sort rebuilt in the gate/up prologue,
 // and (narrow) the top-k too, and the top-k weighted combine folded into down
 // through a hand-off between workgroups.
 //
@@ -25,8 +25,8 @@
 // at T = 64 against ordinary loads.
 //
 // gate/up prologue (every workgroup, redundantly; the inputs are a few KB in
-// L2): the route kernel's ids go to LDS (narrow: wave t runs token t's top-k
-// on the logits, the route kernel's selection, and puts its ids there, and
+// L2): the route kernel's ids go to LDS (narrow: wave w runs the top-k of tokens
+// w and w + 8 on the logits, the route kernel's selection, and puts its ids there, and
 // workgroup 0 writes topk_ids / topk_weights); the routing bitmask (bit t of word e:
 // token t routes to expert e) gives each expert's count and each route's rank
 // among its expert's tokens; a scan over experts gives block, tile and pair
@@ -88,7 +88,7 @@ constexpr uint32_t kMaxE = 512;      // experts incl. shared, one per thread in 
 constexpr uint32_t kMaxCap = 1024;   // capacity blocks
 constexpr uint32_t kMaxGroups = 64;  // down column groups per token (H / 64 at most)
 constexpr uint32_t kCounters = kMaxT * kMaxGroups;  // combine counters [token][group]
-constexpr uint32_t kNarrowT = 8;     // tokens the narrow variant serves (their x rows staged in LDS)
+constexpr uint32_t kNarrowT = 16;    // tokens the narrow variant serves (their x rows: one 16-row A tile)
 
 // Position of the j-th set bit (0-based) of m; 64 if there is none.
 __device__ __forceinline__ uint32_t nth_bit(unsigned long long m, uint32_t j) {
@@ -210,17 +210,18 @@ __device__ __forceinline__ void ffn_gate_up(
   // unconditionally, entries past Etot as zero)
   static_assert(kMaxE == kThreads, "one mask entry per thread");
   s_mask[tid] = 0ull;
-  uint32_t topk_id = 0;  // narrow: wave t lane s < Ktot, token t's slot s
-  float topk_wt = 0.0f;
+  constexpr uint32_t kTokW = kNarrowT / kWaves;  // narrow: tokens per wave
+  uint32_t topk_id[kTokW] = {};  // narrow: wave w lane s < Ktot, token w + 8 j's slot s
+  float topk_wt[kTokW] = {};
   if constexpr (kStageAll) {
     // narrow: the A operand of every item is the T token rows themselves
     // (row t = token t, rows T .. 15 zero), copied by DMA into the tile layout
     // of s_a (K block kb, half h: the 16-byte piece of row r at columns
     // 128 kb + 32 c + 16 h .. + 15 sits at 2048 kb + 1024 h + 16 (16 c + r))
     // with the scales s_xs[kb][r]; pieces past the T rows read as zeros. The
-    // copies use no registers and are in flight under the top-k; wave t
-    // selects token t's experts from the logits (the route kernel's top-k,
-    // one wave per token)
+    // copies use no registers and are in flight under the top-k; wave w
+    // selects the experts of tokens w and w + 8 from the logits (the route
+    // kernel's top-k, one wave per token and round)
     static_assert(KB % 4u == 0u, "scale copies of 64 floats");
     const nk::u32x4 rx = nklds::rsrc(xq, T * H), rxs = nklds::rsrc(xs, T * KB * 4u);
     for (uint32_t c = wave; c < 2u * KB; c += kWaves)  // copy c: K block c / 2, half c % 2
@@ -240,17 +241,25 @@ __device__ __forceinline__ void ffn_gate_up(
       issue_at(b0, E, blockIdx.x, 0u);
       if constexpr (NS == 2) issue_at(b1, E, blockIdx.x, 1u);
     }
-    if (wave < T) {
-      topk_select_any(logits + (size_t)wave * Etot, bias, E, K, S, lane, topk_id, topk_wt);
-      if (lane < Ktot) s_ids[wave * Ktot + lane] = (int32_t)topk_id;
+#pragma unroll
+    for (uint32_t j = 0; j < kTokW; ++j) {
+      const uint32_t tk = wave + kWaves * j;
+      if (tk < T) {  // uniform
+        topk_select_any(logits + (size_t)tk * Etot, bias, E, K, S, lane, topk_id[j], topk_wt[j]);
+        if (lane < Ktot) s_ids[tk * Ktot + lane] = (int32_t)topk_id[j];
+      }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the copies have landed
     lds_barrier();
     // workgroup 0 publishes the selection (after the barrier: no store is in
     // the wait above)
-    if (blockIdx.x == 0 && wave < T && lane < Ktot) {
-      topk_ids[wave * Ktot + lane] = (int32_t)topk_id;
-      topk_weights[wave * Ktot + lane] = topk_wt;
+#pragma unroll
+    for (uint32_t j = 0; j < kTokW; ++j) {
+      const uint32_t tk = wave + kWaves * j;
+      if (blockIdx.x == 0 && tk < T && lane < Ktot) {
+        topk_ids[tk * Ktot + lane] = (int32_t)topk_id[j];
+        topk_weights[tk * Ktot + lane] = topk_wt[j];
+      }
     }
   } else {
     for (uint32_t r = tid; r < routes; r += kThreads) s_ids[r] = topk_ids[r];
@@ -605,7 +614,7 @@ __device__ __forceinline__ void ffn_gate_up(
       for (uint32_t j = 0; j < 4; ++j) {
         const uint32_t q = (lane >> 4) * 4u + j;
         const uint32_t below = (uint32_t)__popcll(emask & ((1ull << q) - 1ull));
-        const bool routed = (emask >> q) & 1ull;  // q < T <= 8 for a set bit
+        const bool routed = (emask >> q) & 1ull;  // q < T <= 16 for a set bit
         const uint32_t r = routed ? below : cnt + q - below;
         hg[r * I + c0 * 16u + (lane & 15u)] = routed ? nk::bf16_rne(nk::silu(ag[j]) * au[j]) : (uint16_t)0u;
       }
@@ -1107,7 +1116,7 @@ NK_FFN_PAIR(4096, 256, narrow, 8, 2, 2, 2, 1, 1, 4, 1)
 // Symbols netra_moe_ffn_down_h<H>_i<I>_rows_gfx950: the down for the narrow
 // gate/up's bf16 h rows (requantised per tile, as the narrow down does) with
 // the wide down's item shape and no hand-off, leaving fp32 route partials to
-// the combine kernel: at 2 .. 8 tokens the hand-off's K-split sums, counters
+// the combine kernel: from 5 tokens on the hand-off's K-split sums, counters
 // and last-arriver combines cost more than a separate combine launch.
 #define NK_FFN_DOWN_ROWS(HV, IV, SBV, CHD, WPED, PDV)                                                \
   NK_KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WPED)))                      \

@@ -53,7 +53,7 @@ class TensorSpec:
 GEMM_PATHS = ("fused", "stream", "tile")
 FUSED_HI = ((512, 256), (1024, 1024), (2048, 512), (4096, 256))  # netra_moe_ffn_{gate_up,down}_h<H>_i<I>_<v>_gfx950
 FUSED_MAX_T = 64                     # one bitmask word per expert in the gate/up prologue
-FFN_NARROW_T = 8                     # T at or below which the decode FFN splits K (the "narrow" variant)
+FFN_NARROW_T = 16                    # T at or below which the decode FFN splits K (the "narrow" variant)
 NARROW_ROWS_DOWN_T = 5               # narrow T at or above which down takes the wide item shape + combine kernel
 FFN_COUNTERS = 64 * 64               # combine hand-off counters [token][column group] (kCounters)
 FFN_WIDE_P = {(512, 256): 2, (1024, 1024): 4, (2048, 512): 4, (4096, 256): 2}  # wide gate/up items per wave (PG)

@@ -48,9 +48,10 @@ EXTRA_CONFIGS = {
     # more than 256 experts: the 512-expert route_select / top-k / sort variants
     "shape_e384": MoEConfig("shape_e384", T=96, H=1024, E=384, K=6, I=256, S=1,
                             router_bias="zipf1.1", seed=1104),
-    # the narrow decode FFN (1 < T <= 8: top-k in the gate/up prologue, one
-    # A operand of every token row, the combine hand-off in down) on each of
-    # its shapes; hot: every token on the same experts, 8 rows per tile
+    # the narrow decode FFN (1 < T <= 16: top-k in the gate/up prologue, one
+    # A operand of every token row; down with the combine hand-off below five
+    # tokens, else the rows down and the combine kernel) on each of its
+    # shapes; hot: every token on the same experts, T rows per tile
     "narrow_t4": MoEConfig("narrow_t4", T=4, H=2048, E=256, K=8, I=512, S=1, seed=1106),
     "narrow_t8_hot": MoEConfig("narrow_t8_hot", T=8, H=2048, E=256, K=8, I=512, S=1,
                                router_bias="hot", seed=1107),
@@ -58,9 +59,15 @@ EXTRA_CONFIGS = {
     "narrow_t5_h1024_i1024": MoEConfig("narrow_t5_h1024_i1024", T=5, H=1024, E=24, K=3, I=1024, S=1,
                                        seed=1109),
     "narrow_t2_h512": MoEConfig("narrow_t2_h512", T=2, H=512, E=16, K=2, I=256, S=0, seed=1110),
-    # the wide decode FFN at the headline shape: full 16-row tiles (hot
-    # routing) and a ragged token count
-    "wide_t16_hot": MoEConfig("wide_t16_hot", T=16, H=2048, E=256, K=8, I=512, S=1, router_bias="hot",
+    # two tokens per selecting wave (T > 8), a full 16-row tile (hot)
+    "narrow_t12": MoEConfig("narrow_t12", T=12, H=2048, E=256, K=8, I=512, S=1, seed=1124),
+    "narrow_t16_hot": MoEConfig("narrow_t16_hot", T=16, H=2048, E=256, K=8, I=512, S=1,
+                                router_bias="hot", seed=1125),
+    "narrow_t9_h512": MoEConfig("narrow_t9_h512", T=9, H=512, E=16, K=2, I=256, S=1, seed=1126),
+    "narrow_t16_h4096": MoEConfig("narrow_t16_h4096", T=16, H=4096, E=32, K=4, I=256, S=1, seed=1127),
+    # the wide decode FFN at the headline shape: hot experts of 17 rows (a
+    # full tile and one row) and a ragged token count
+    "wide_t17_hot": MoEConfig("wide_t17_hot", T=17, H=2048, E=256, K=8, I=512, S=1, router_bias="hot",
                               seed=1112),
     "wide_t33": MoEConfig("wide_t33", T=33, H=2048, E=256, K=8, I=512, S=1, seed=1113),
     # every hot expert with 64 rows (four tiles each, as the shared expert):

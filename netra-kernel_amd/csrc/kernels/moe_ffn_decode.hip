@@ -558,11 +558,11 @@ __device__ __forceinline__ void ffn_gate_up(
     } else {
 #pragma unroll 1
       for (uint32_t s = 0; s < NS; s += 2u) {
-        issue(b1, s + 1u < NS ? s + 1u : NS - 1u);
+        if (s + 1u < NS) issue(b1, s + 1u);  // (no step issued past the last)
         __builtin_amdgcn_sched_barrier(0);
         compute(b0, s);
         if (s + 1u >= NS) break;
-        issue(b0, s + 2u < NS ? s + 2u : NS - 1u);
+        if (s + 2u < NS) issue(b0, s + 2u);
         __builtin_amdgcn_sched_barrier(0);
         compute(b1, s + 1u);
       }
@@ -887,11 +887,11 @@ __device__ __forceinline__ void ffn_down(
     } else {
 #pragma unroll 1
       for (uint32_t s = 0; s < NS; s += 2u) {
-        issue(e1, s + 1u < NS ? s + 1u : NS - 1u);
+        if (s + 1u < NS) issue(e1, s + 1u);  // (no step issued past the last)
         __builtin_amdgcn_sched_barrier(0);
         compute(e0, s);
         if (s + 1u >= NS) break;
-        issue(e0, s + 2u < NS ? s + 2u : NS - 1u);
+        if (s + 2u < NS) issue(e0, s + 2u);
         __builtin_amdgcn_sched_barrier(0);
         compute(e1, s + 1u);
       }

@@ -556,15 +556,27 @@ __device__ __forceinline__ void ffn_gate_up(
       compute(b0, 0u);
       compute(b1, 1u);
     } else {
+      // the last one or two steps peeled: no load is issued under a branch
+      // (the wait counts at a join would drain the step in flight) and none
+      // past the last step
+      uint32_t s = 0;
 #pragma unroll 1
-      for (uint32_t s = 0; s < NS; s += 2u) {
-        if (s + 1u < NS) issue(b1, s + 1u);  // (no step issued past the last)
+      for (; s + 2u < NS; s += 2u) {
+        issue(b1, s + 1u);
         __builtin_amdgcn_sched_barrier(0);
         compute(b0, s);
-        if (s + 1u >= NS) break;
-        if (s + 2u < NS) issue(b0, s + 2u);
+        issue(b0, s + 2u);
         __builtin_amdgcn_sched_barrier(0);
         compute(b1, s + 1u);
+      }
+      if constexpr (NS % 2u == 0u) {
+        issue(b1, s + 1u);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(b0, s);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(b1, s + 1u);
+      } else {
+        compute(b0, s);
       }
     }
     if constexpr (SA > 1) {  // add the K splits in split order (s_red has LDS of its own)
@@ -885,15 +897,27 @@ __device__ __forceinline__ void ffn_down(
     if constexpr (NS == 1) {
       compute(e0, 0u);
     } else {
+      // the last one or two steps peeled: no load is issued under a branch
+      // (the wait counts at a join would drain the step in flight) and none
+      // past the last step
+      uint32_t s = 0;
 #pragma unroll 1
-      for (uint32_t s = 0; s < NS; s += 2u) {
-        if (s + 1u < NS) issue(e1, s + 1u);  // (no step issued past the last)
+      for (; s + 2u < NS; s += 2u) {
+        issue(e1, s + 1u);
         __builtin_amdgcn_sched_barrier(0);
         compute(e0, s);
-        if (s + 1u >= NS) break;
-        if (s + 2u < NS) issue(e0, s + 2u);
+        issue(e0, s + 2u);
         __builtin_amdgcn_sched_barrier(0);
         compute(e1, s + 1u);
+      }
+      if constexpr (NS % 2u == 0u) {
+        issue(e1, s + 1u);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(e0, s);
+        if constexpr (!kFromRows) __builtin_amdgcn_sched_barrier(0);  // (rows: spills at 128 VGPRs)
+        compute(e1, s + 1u);
+      } else {
+        compute(e0, s);
       }
     }
     if constexpr (SB > 1) {

@@ -17,8 +17,9 @@ back to back on both rooflines (T=4096: a `roofline` object for gate/up against
 dense FP8).
 
 Prints ONE JSON line. Extra objects:
-  roofline      the dominant kernel (gate/up) on its binding roofline (HBM),
-                from HIP-event timing of back-to-back launches on the launch stream
+  roofline      the dominant kernel (gate/up; at T=64 the gate/up kernel that
+                runs each tile's down too) on its binding roofline (HBM), from
+                HIP-event timing of back-to-back launches on the launch stream
   cpu_baseline  the C oracle on the host cores over a bounded token sample
 """
 from __future__ import annotations
@@ -64,6 +65,14 @@ def down_bytes(cfg, touched: int, path: str) -> int:
         return w + h + 2 * cfg.T * cfg.H
     part = (2 if path == "tile" else 4) * cfg.routes * cfg.H  # bf16 / fp32 route partials
     return w + h + part
+
+
+def merged_bytes(cfg, touched: int, path: str) -> int:
+    """Algorithmic HBM bytes of one launch of the gate/up kernel that also runs
+    each tile's down (the fused path's merged variant): both GEMMs' bytes less
+    the h read-back, which stays in the workgroup's LDS."""
+    h = cfg.routes * cfg.I + 4 * cfg.routes * (cfg.I // 128)
+    return gate_up_bytes(cfg, touched, path) + down_bytes(cfg, touched, path) - h
 
 
 def gate_up_flops(cfg) -> int:
@@ -539,7 +548,8 @@ def main() -> int:
                 lay = MoELayer(c, w, graph=False, expose=inter)
                 lay.x.copy_(act["x"].to(dev))
                 xl.append(lay)
-            kern["isolated"] = {op: time_isolated(xl, op, max(50, steps // 2), torch) * 1e3 for op in ISOLATED_OPS}
+            kern["isolated"] = {op: time_isolated(xl, op, max(50, steps // 2), torch) * 1e3
+                                for op in ISOLATED_OPS if op in xl[0].op_names}
             for lay in xl:
                 lay.close()
         for lay in layers:
@@ -552,11 +562,15 @@ def main() -> int:
     main_res, kern, act = run_config(cfg, args.steps, args.warmup, True)
     touched = main_res["touched_experts"]
     iso = kern.pop("isolated")
+    from netra_moe.engine import down_variant
+    merged = path == "fused" and down_variant(cfg) == "merged"  # gate/up runs each tile's down too
     dom_op, dom_us = "gate_up", iso["gate_up"]
-    dom_bytes = gate_up_bytes(cfg, touched, path)
-    dn_us, dn_bytes = iso["down"], down_bytes(cfg, touched, path)
-    other = {"down": {"achieved_gbps": dn_bytes / (dn_us * 1e-6) / 1e9, "avg_us": dn_us,
-                      "algorithmic_bytes_per_launch": dn_bytes}}
+    dom_bytes = (merged_bytes if merged else gate_up_bytes)(cfg, touched, path)
+    other = {}
+    if not merged:
+        dn_us, dn_bytes = iso["down"], down_bytes(cfg, touched, path)
+        other["down"] = {"achieved_gbps": dn_bytes / (dn_us * 1e-6) / 1e9, "avg_us": dn_us,
+                         "algorithmic_bytes_per_launch": dn_bytes}
     gu_symbol = next(op["symbol"] for op in operations(cfg, path) if op["name"] == f"moe.{dom_op}")
     roof = {"kernel": gu_symbol, "bound": "hbm",
             "achieved": dom_bytes / (dom_us * 1e-6) / 1e9, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -573,6 +587,8 @@ def main() -> int:
         out = {}
         for op, fl, by in (("gate_up", gate_up_flops(c), gate_up_bytes(c, touched, p)),
                            ("down", down_flops(c), down_bytes(c, touched, p))):
+            if op not in iso:  # the merged decode variant: no down launch
+                continue
             us = iso[op]
             out[op] = {"kernel": syms[f"moe.{op}"], "avg_us": us, "flops": fl, "bytes": by,
                        "tflops": fl / (us * 1e-6) / 1e12, "gbps": by / (us * 1e-6) / 1e9}

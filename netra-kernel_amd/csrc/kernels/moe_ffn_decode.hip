@@ -136,8 +136,8 @@ __device__ __forceinline__ void quant_block(const uint32_t (&raw)[16], uint4& ql
 
 // ---------------------------------------------------------------------------
 // gate/up with the sort as its prologue
-template <uint32_t KB, uint32_t KBI, uint32_t SA, uint32_t CHM, uint32_t P>  // H / 128, I / 128, K splits,
-                                                                               // K blocks per step, items per wave
+template <uint32_t KB, uint32_t KBI, uint32_t SA, uint32_t CHM, uint32_t P,  // H / 128, I / 128, K splits,
+          bool kDown = false>  // K blocks per step, items per wave; kDown: the tile's down too
 __device__ __forceinline__ void ffn_gate_up(
     const uint16_t* __restrict__ logits, const float* __restrict__ bias, int32_t* __restrict__ topk_ids,
     float* __restrict__ topk_weights, const uint8_t* __restrict__ xq, const float* __restrict__ xs,
@@ -145,7 +145,8 @@ __device__ __forceinline__ void ffn_gate_up(
     int32_t* __restrict__ sorted_expert, int32_t* __restrict__ tile_map, int32_t* __restrict__ pair_map,
     int32_t* __restrict__ num_valid, int32_t* __restrict__ counts, uint16_t* __restrict__ hrows,
     uint8_t* __restrict__ hq, float* __restrict__ hs, uint32_t T, uint32_t E, uint32_t K, uint32_t S,
-    uint32_t cap_blocks) {
+    uint32_t cap_blocks, const uint8_t* __restrict__ w2 = nullptr, const float* __restrict__ w2s = nullptr,
+    float* __restrict__ partial = nullptr) {
   using nkstream::lds_barrier;
   constexpr uint32_t H = 128u * KB, I = 128u * KBI;
   constexpr uint32_t CA = kWaves / SA;                 // column items per gate/up item
@@ -160,10 +161,20 @@ __device__ __forceinline__ void ffn_gate_up(
   static_assert(I % (16u * CA * P) == 0 && H % kThreads == 0 && (P == 1 || SA == 1) && P <= kWaves, "shares");
   constexpr uint32_t kRed = SA > 1 ? kWaves * 8u * 64u * 4u : 0u;  // split sums
   constexpr bool kStageAll = SA > 1;  // narrow: one A operand (every token's row) for all items
+  // kDown: after its gate/up steps the workgroup runs the tile's down over all
+  // H output columns (wave w: 32-column items PDN w ..), its A operand the
+  // requantised h in LDS (s_big, scales in s_xs), and leaves fp32 route
+  // partials to the combine kernel
+  constexpr uint32_t PDN = H / (32u * kWaves);         // 32-column down items per wave
+  constexpr uint32_t kDCN = KBI >= 2u ? 2u : 1u;       // down K blocks per step
+  constexpr uint32_t NBN = KBI / kDCN;                 // down steps per 32-column item
+  constexpr uint32_t NSN = PDN * NBN;                  // down steps per wave
+  static_assert(!kDown || (SA == 1 && P == KBI && I == 128u * P && KBI <= KB && NSN >= 2u),
+                "kDown: one item per tile, the requantised h fits the x rows' LDS");
   constexpr uint32_t kBig = KB * 2048u > kRed || kStageAll ? KB * 2048u : kRed;
   // s_big: the tile's x rows | split sums
   __shared__ __align__(16) uint8_t s_big[kBig];
-  __shared__ float s_xs[16 * KB];                                 // x row scales [kb][row]
+  __shared__ __align__(16) float s_xs[16 * KB];                   // x row scales [kb][row] | kDown: h scales
   __shared__ __align__(16) uint16_t s_hb[kQuant ? 16u * kHb : 8u];  // the item's h rows (bf16)
   __shared__ int32_t s_ids[kMaxT * kMaxKtot];
   __shared__ unsigned long long s_mask[kMaxE];
@@ -597,6 +608,23 @@ __device__ __forceinline__ void ffn_gate_up(
       }
     }
     if constexpr (kQuant) {
+      // kDown: W2 step s of wave w covers 32-column item PDN w + s / NBN, K
+      // blocks ((s + g) % NBN) kDCN .. (rotated by the tile, as above)
+      const uint8_t* w2e = w2 + (size_t)e * H * I;
+      const float* w2se = w2s + (size_t)e * (H / 128u) * KBI;
+      const uint32_t rotn = g % NBN;
+      auto issue_dn = [&](DownStep<kDCN>& st, uint32_t s) __attribute__((always_inline)) {
+        const uint32_t d = wave * PDN + s / NBN, kb0 = ((s + rotn) % NBN) * kDCN;
+#pragma unroll
+        for (uint32_t i = 0; i < kDCN; ++i)
+#pragma unroll
+          for (uint32_t t2 = 0; t2 < 2; ++t2)
+            st.w[i][t2] = nk::load_tile_operand_once(nk::tile_base(w2e, d * 2u + t2, kb0 + i, KBI), lane);
+        const uint32_t li = (lane >> 1) < kDCN ? lane >> 1 : 0u;
+        st.ws = w2se[((d * 2u + (lane & 1u)) >> 3) * KBI + kb0 + li];
+      };
+      DownStep<kDCN> f0, f1;
+      if constexpr (kDown) issue_dn(f0, 0u);  // the weight stream goes on under the requant
       // the item's h rows are in LDS; waves 0 .. P - 1 requantise one 128-column block each
       lds_barrier();
       if (wave < P) {
@@ -614,6 +642,78 @@ __device__ __forceinline__ void ffn_gate_up(
         *reinterpret_cast<uint4*>(hq + blk * 2048u + lane * 16u) = qlo;
         *reinterpret_cast<uint4*>(hq + blk * 2048u + 1024u + lane * 16u) = qhi;
         if (lane < 16u) hs[blk * 16u + lane] = scale;
+        if constexpr (kDown) {  // and the down's A operand: K block `wave` (s_a is free)
+          *reinterpret_cast<uint4*>(&s_big[wave * 2048u + lane * 16u]) = qlo;
+          *reinterpret_cast<uint4*>(&s_big[wave * 2048u + 1024u + lane * 16u]) = qhi;
+          if (lane < 16u) s_xs[wave * 16u + lane] = scale;
+        }
+      }
+      if constexpr (kDown) {
+        // lane l: the route of the tile's row l & 15 (the rank among e's
+        // tokens, as staged), -1 for padding
+        int32_t route = -1;
+        {
+          const unsigned long long emask = s_mask[e];
+          const uint32_t j = 16u * k + (lane & 15u);
+          if (j < (uint32_t)__popcll(emask)) {
+            const uint32_t t = nth_bit(emask, j), sl = slot_of(s_ids, t, Ktot, e);
+            if (sl < Ktot) route = (int32_t)(t * Ktot + sl);  // (always: the mask comes from the ids)
+          }
+        }
+        lds_barrier();  // the h operand is in LDS
+        v4f acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        auto compute_dn = [&](const DownStep<kDCN>& st, uint32_t s) __attribute__((always_inline)) {
+#pragma unroll
+          for (uint32_t i = 0; i < kDCN; ++i) {
+            const uint32_t kb = ((s + rotn) % NBN) * kDCN + i;
+            const v8i a = nk::load_tile_operand(s_big + kb * 2048u, lane);
+            const float4 as4 = *reinterpret_cast<const float4*>(&s_xs[kb * 16u + (lane >> 4) * 4u]);
+            const float as[4] = {as4.x, as4.y, as4.z, as4.w};
+            const v4f d0v = nk::mfma_e4m3_16x16x128(a, st.w[i][0]);
+            const v4f d1v = nk::mfma_e4m3_16x16x128(a, st.w[i][1]);
+            const float s0 = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(st.ws), (int)(2u * i)));
+            const float s1 = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(st.ws), (int)(2u * i + 1u)));
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+              acc0[j] = acc0[j] + s0 * (as[j] * d0v[j]);
+              acc1[j] = acc1[j] + s1 * (as[j] * d1v[j]);
+            }
+          }
+          if (s % NBN == NBN - 1u) {  // 32-column item PDN w + s / NBN done: its route partials
+            const uint32_t d = wave * PDN + s / NBN;
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+              const int32_t r = __shfl(route, (lane >> 4) * 4u + j);
+              if (r >= 0) {
+                float* dst = partial + (size_t)r * H + d * 32u + (lane & 15u);
+                dst[0] = acc0[j];
+                dst[16] = acc1[j];
+              }
+            }
+            acc0 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            acc1 = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+          }
+        };
+        // two step buffers, the last one or two steps peeled (no load under a branch)
+        uint32_t s = 0;
+#pragma unroll 1
+        for (; s + 2u < NSN; s += 2u) {
+          issue_dn(f1, s + 1u);
+          __builtin_amdgcn_sched_barrier(0);
+          compute_dn(f0, s);
+          issue_dn(f0, s + 2u);
+          __builtin_amdgcn_sched_barrier(0);
+          compute_dn(f1, s + 1u);
+        }
+        if constexpr (NSN % 2u == 0u) {
+          issue_dn(f1, s + 1u);
+          __builtin_amdgcn_sched_barrier(0);
+          compute_dn(f0, s);
+          __builtin_amdgcn_sched_barrier(0);
+          compute_dn(f1, s + 1u);
+        } else {
+          compute_dn(f0, s);
+        }
       }
     } else if (sa == 0) {  // bf16 h of tile g, column 16 c0 + (l & 15) (P = 1)
       // lane l, j: MFMA row q = (l >> 4) * 4 + j is token q; the tile's row of
@@ -1136,6 +1236,30 @@ NK_FFN_PAIR(2048, 512, wide, 1, 1, 2, 2, 4, 2, 4, 1)
 NK_FFN_PAIR(2048, 512, narrow, 8, 4, 1, 4, 1, 1, 4, 1)
 NK_FFN_PAIR(4096, 256, wide, 1, 1, 2, 2, 2, 2, 4, 1)
 NK_FFN_PAIR(4096, 256, narrow, 8, 2, 2, 2, 1, 1, 4, 1)
+
+// Symbols netra_moe_ffn_gate_up_down_h<H>_i<I>_gfx950: the wide gate/up with each
+// tile's down in the same workgroup (the tile's h requantised into LDS, the
+// expert's W2 streamed right behind its W13, fp32 route partials left to the
+// combine kernel): one launch and one weight stream per tile instead of two.
+#define NK_FFN_MERGED(HV, IV, CHG, PG)                                                               \
+  NK_KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))                         \
+  void netra_moe_ffn_gate_up_down_h##HV##_i##IV##_gfx950(                                                  \
+      const uint16_t* __restrict__ logits, const float* __restrict__ bias,                         \
+      int32_t* __restrict__ topk_ids, float* __restrict__ topk_weights, const uint8_t* __restrict__ xq, \
+      const float* __restrict__ xs, const uint8_t* __restrict__ w13, const float* __restrict__ w13s, \
+      int32_t* __restrict__ sorted_ids, int32_t* __restrict__ sorted_expert,                       \
+      int32_t* __restrict__ tile_map, int32_t* __restrict__ pair_map, int32_t* __restrict__ num_valid, \
+      int32_t* __restrict__ counts, uint16_t* __restrict__ hrows, uint8_t* __restrict__ hq,        \
+      float* __restrict__ hs, const uint8_t* __restrict__ w2, const float* __restrict__ w2s,       \
+      float* __restrict__ partial, uint32_t T, uint32_t E, uint32_t K, uint32_t S, uint32_t cap_blocks) { \
+    nkffn::ffn_gate_up<HV / 128, IV / 128, 1, CHG, PG, true>(logits, bias, topk_ids, topk_weights, xq, xs, \
+                                                          w13, w13s, sorted_ids, sorted_expert,   \
+                                                          tile_map, pair_map, num_valid, counts,  \
+                                                          hrows, hq, hs, T, E, K, S, cap_blocks,  \
+                                                          w2, w2s, partial);                      \
+  }
+NK_FFN_MERGED(512, 256, 2, 2)
+NK_FFN_MERGED(2048, 512, 2, 4)
 
 // Symbols netra_moe_ffn_down_h<H>_i<I>_rows_gfx950: the down for the narrow
 // gate/up's bf16 h rows (requantised per tile, as the narrow down does) with

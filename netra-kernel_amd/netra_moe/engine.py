@@ -287,7 +287,9 @@ def op_names(cfg: MoEConfig, path: str = "auto", front: str = "auto") -> tuple[s
     """Engine operation names of one layer call, in launch order."""
     path = resolve_path(cfg, path)
     if path == "fused":
-        return ("route", "gate_up", "down") + (("combine",) if down_variant(cfg) in ("wide", "rows") else ())
+        dv = down_variant(cfg)
+        return (("route", "gate_up") + (() if dv == "merged" else ("down",))
+                + (("combine",) if dv in ("wide", "rows", "merged") else ()))
     front_ops = EXACT_FRONT_OPS if resolve_front(cfg, path, front) == "exact" else SCREEN_FRONT_OPS
     return front_ops + PATH_OPS[path]
 ROUTER_H = (512, 1024, 2048, 4096)   # netra_moe_router_h<H>_t<NT>_gfx950
@@ -406,6 +408,14 @@ def ffn_variant(cfg: MoEConfig) -> str:
 
 # (H, I) with a single-token down kernel (netra_moe_ffn_down_h<H>_i<I>_single)
 SINGLE_DOWN = {(2048, 512)}
+# (H, I) with a gate/up + down per tile kernel (netra_moe_ffn_gate_up_down_h<H>_i<I>;
+# one wide gate/up item per tile) -> the T from which it replaces the wide
+# down, layer times measured on one MI355X against gate/up + down: H 2048,
+# I 512: T=17 82.2 / 80.3 µs, 21: 85.2 / 84.6, 22: 86.2 / 87.0, 23: 86.8 /
+# 88.3, 32: 95.3 / 97.6, 64: 130.6 / 131.1; H 512, I 256: T=17 25.7 / 28.7,
+# 24: 26.9 / 30.7, 64: 32.0 / 35.0. (H 4096, I 256 measured no faster:
+# 139.0 / 138.8 µs at T=64.)
+MERGED_FFN_T = {(512, 256): 17, (2048, 512): 22}
 
 
 def down_variant(cfg: MoEConfig) -> str:
@@ -414,10 +424,14 @@ def down_variant(cfg: MoEConfig) -> str:
     rows, the wide down's items, the combine kernel after it) from
     NARROW_ROWS_DOWN_T narrow tokens (measured at H 2048, I 512 with HBM-cold
     weights: 38.4 / 41.4 / 44.8 / 49.0 against 39.7 / 43.8 / 49.1 / 53.1 µs
-    at T = 5 .. 8, 35.2 against 34.0 at T = 4); else the FFN variant."""
+    at T = 5 .. 8, 35.2 against 34.0 at T = 4); merged (the down of each tile
+    run by its wide gate/up workgroup, the combine kernel after it) from
+    MERGED_FFN_T tokens; else the FFN variant."""
     if cfg.T == 1 and (cfg.H, cfg.I) in SINGLE_DOWN and cfg.Ktot <= 16:
         return "single"
     v = ffn_variant(cfg)
+    if v == "wide" and cfg.T >= MERGED_FFN_T.get((cfg.H, cfg.I), cfg.T + 1):
+        return "merged"
     return "rows" if v == "narrow" and cfg.T >= NARROW_ROWS_DOWN_T else v
 
 
@@ -495,8 +509,17 @@ def _fused_decode(cfg: MoEConfig) -> list[dict]:
         ops[-1]["writes"].remove("ffn_counters")
     if down_variant(cfg) == "rows":  # h requantised from the rows (copies for inspection), partials out
         ops[-1]["writes"] = ["h_q", "h_scale", "partial"]
-    if down_variant(cfg) in ("wide", "rows"):  # fp32 partials for the combine kernel
-        if v == "wide":
+    if down_variant(cfg) == "merged":  # gate/up runs each tile's down: its partials out, no down launch
+        gu = ops[1]
+        gu["symbol"] = f"netra_moe_ffn_gate_up_down_h{H}_i{I}_gfx950"
+        i = gu["args"].index("h_scale") + 1
+        gu["args"][i:i] = ["w2", "w2_scale", "partial"]
+        gu["reads"] += ["w2", "w2_scale"]
+        gu["writes"] = [*sort_out, "h_q", "h_scale", "partial"]
+        gu["refs"] += ops[2]["refs"]
+        del ops[2]
+    if down_variant(cfg) in ("wide", "rows", "merged"):  # fp32 partials for the combine kernel
+        if v == "wide" and down_variant(cfg) == "wide":
             ops[-1]["writes"] = ["partial"]
         ops.append(dict(name="moe.combine", symbol="netra_moe_combine_gfx950",
                         grid=((H + 1023) // 1024, T, 1), block=(256, 1, 1), lds=0, dyn=0,

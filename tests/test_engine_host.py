@@ -88,7 +88,9 @@ def test_emitted_engine_passes_the_native_manifest_check(engine_dir):
     assert st == nm.Status.OK, msg
     doc = json.loads((engine_dir / "engine.json").read_text())
     assert [op["name"] for op in doc["operations"]] == [f"moe.{n}" for n in op_names(nm.BASELINE_CONFIGS["decode_t64"])]
-    assert op_names(nm.BASELINE_CONFIGS["decode_t64"]) == ("route", "gate_up", "down", "combine")
+    assert op_names(nm.BASELINE_CONFIGS["decode_t64"]) == ("route", "gate_up", "combine")  # down per tile in gate/up
+    wide17 = nm.MoEConfig("wide17", T=17, H=2048, E=256, K=8, I=512, S=1, seed=1)
+    assert op_names(wide17) == ("route", "gate_up", "down", "combine")
     assert op_names(nm.BASELINE_CONFIGS["decode_t1"]) == ("route", "gate_up", "down")
     assert op_names(nm.BASELINE_CONFIGS["decode_t64"], path="stream") == ("route", "sort", "gate_up", "down", "combine")
 

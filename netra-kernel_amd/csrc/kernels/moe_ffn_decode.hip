@@ -162,7 +162,7 @@ __device__ __forceinline__ void ffn_gate_up(
   constexpr uint32_t kRed = SA > 1 ? kWaves * 8u * 64u * 4u : 0u;  // split sums
   constexpr bool kStageAll = SA > 1;  // narrow: one A operand (every token's row) for all items
   // kDown: after its gate/up steps the workgroup runs the tile's down over all
-  // H output columns (wave w: 32-column items PDN w ..), its A operand the
+  // H output columns (wave w: 32-column items w, w + 8, ..), its A operand the
   // requantised h in LDS (s_big, scales in s_xs), and leaves fp32 route
   // partials to the combine kernel
   constexpr uint32_t PDN = H / (32u * kWaves);         // 32-column down items per wave
@@ -608,13 +608,16 @@ __device__ __forceinline__ void ffn_gate_up(
       }
     }
     if constexpr (kQuant) {
-      // kDown: W2 step s of wave w covers 32-column item PDN w + s / NBN, K
-      // blocks ((s + g) % NBN) kDCN .. (rotated by the tile, as above)
+      // kDown: W2 step s of wave w covers 32-column item 8 (s / NBN) + w, K
+      // blocks ((s + g) % NBN) kDCN .. (rotated by the tile, as above): the 8
+      // waves read neighbouring items, so the workgroup's reads advance through
+      // the expert's W2 as one front (items PDN w .. per wave, 8 fronts 128 KiB
+      // apart: 1.7 us slower at T=64)
       const uint8_t* w2e = w2 + (size_t)e * H * I;
       const float* w2se = w2s + (size_t)e * (H / 128u) * KBI;
       const uint32_t rotn = g % NBN;
       auto issue_dn = [&](DownStep<kDCN>& st, uint32_t s) __attribute__((always_inline)) {
-        const uint32_t d = wave * PDN + s / NBN, kb0 = ((s + rotn) % NBN) * kDCN;
+        const uint32_t d = (s / NBN) * kWaves + wave, kb0 = ((s + rotn) % NBN) * kDCN;
 #pragma unroll
         for (uint32_t i = 0; i < kDCN; ++i)
 #pragma unroll
@@ -680,7 +683,7 @@ __device__ __forceinline__ void ffn_gate_up(
             }
           }
           if (s % NBN == NBN - 1u) {  // 32-column item PDN w + s / NBN done: its route partials
-            const uint32_t d = wave * PDN + s / NBN;
+            const uint32_t d = (s / NBN) * kWaves + wave;
 #pragma unroll
             for (uint32_t j = 0; j < 4; ++j) {
               const int32_t r = __shfl(route, (lane >> 4) * 4u + j);

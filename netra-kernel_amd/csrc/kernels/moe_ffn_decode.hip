@@ -137,7 +137,8 @@ __device__ __forceinline__ void quant_block(const uint32_t (&raw)[16], uint4& ql
 // ---------------------------------------------------------------------------
 // gate/up with the sort as its prologue
 template <uint32_t KB, uint32_t KBI, uint32_t SA, uint32_t CHM, uint32_t P,  // H / 128, I / 128, K splits,
-          bool kDown = false>  // K blocks per step, items per wave; kDown: the tile's down too
+          bool kDown = false, bool kKSplit = false>  // K blocks per step, items per wave; kDown: the
+                                                     // tile's down too; kKSplit: gate/up K over the waves
 __device__ __forceinline__ void ffn_gate_up(
     const uint16_t* __restrict__ logits, const float* __restrict__ bias, int32_t* __restrict__ topk_ids,
     float* __restrict__ topk_weights, const uint8_t* __restrict__ xq, const float* __restrict__ xs,
@@ -171,11 +172,17 @@ __device__ __forceinline__ void ffn_gate_up(
   constexpr uint32_t NSN = PDN * NBN;                  // down steps per wave
   static_assert(!kDown || (SA == 1 && P == KBI && I == 128u * P && KBI <= KB && NSN >= 2u),
                 "kDown: one item per tile, the requantised h fits the x rows' LDS");
+  // kKS (kDown, H = 2048): gate/up step s is 16-column item s for every wave,
+  // wave w taking K blocks kCH w .. (the workgroup reads the item's 64 KiB of
+  // W13 together); the waves' split sums are added in wave order in LDS
+  constexpr bool kKS = kKSplit;
+  static_assert(!kKS || (kDown && KB == kWaves * kCH && NS == I / 16u && kQuant), "kKS: one step per 16-column item");
   constexpr uint32_t kBig = KB * 2048u > kRed || kStageAll ? KB * 2048u : kRed;
   // s_big: the tile's x rows | split sums
   __shared__ __align__(16) uint8_t s_big[kBig];
   __shared__ __align__(16) float s_xs[16 * KB];                   // x row scales [kb][row] | kDown: h scales
   __shared__ __align__(16) uint16_t s_hb[kQuant ? 16u * kHb : 8u];  // the item's h rows (bf16)
+  __shared__ float s_ksred[kKS ? 2u * kWaves * 8u * 64u : 1u];     // kKS: split sums, two steps
   __shared__ int32_t s_ids[kMaxT * kMaxKtot];
   __shared__ unsigned long long s_mask[kMaxE];
   __shared__ uint32_t s_boff[kMaxE + 1], s_toff[kMaxE + 1];
@@ -203,10 +210,10 @@ __device__ __forceinline__ void ffn_gate_up(
   auto issue_at = [&](GateUpStep<kCH>& st, uint32_t e, uint32_t item, uint32_t s) __attribute__((always_inline)) {
     const uint8_t* w13e = w13 + (size_t)e * 2u * I * H;
     const float* w13se = w13s + (size_t)e * (2u * I / 128u) * KB;
-    const uint32_t c = ((item % GA) * CA + ca) * P + s / NA, rot = item % NA;
+    const uint32_t c = kKS ? s : ((item % GA) * CA + ca) * P + s / NA, rot = item % NA;
 #pragma unroll
     for (uint32_t i = 0; i < kCH; ++i) {
-      const uint32_t kb = kbw + ((s + rot) % NA) * kCH + i;
+      const uint32_t kb = kKS ? wave * kCH + i : kbw + ((s + rot) % NA) * kCH + i;
       st.g[i] = nk::load_tile_operand_once(nk::tile_base(w13e, 2u * c, kb, KB), lane);
       st.u[i] = nk::load_tile_operand_once(nk::tile_base(w13e, 2u * c + 1u, kb, KB), lane);
     }
@@ -537,7 +544,7 @@ __device__ __forceinline__ void ffn_gate_up(
     auto compute = [&](const GateUpStep<kCH>& st, uint32_t s) __attribute__((always_inline)) {
 #pragma unroll
       for (uint32_t i = 0; i < kCH; ++i) {
-        const uint32_t kb = kbw + ((s + rot) % NA) * kCH + i;
+        const uint32_t kb = kKS ? wave * kCH + i : kbw + ((s + rot) % NA) * kCH + i;
         const v8i a = nk::load_tile_operand(s_a + kb * 2048u, lane);
         const v4f dg = nk::mfma_e4m3_16x16x128(a, st.g[i]);
         const v4f du = nk::mfma_e4m3_16x16x128(a, st.u[i]);
@@ -550,7 +557,29 @@ __device__ __forceinline__ void ffn_gate_up(
           au[j] = au[j] + su * (as * du[j]);
         }
       }
-      if constexpr (kQuant) {
+      if constexpr (kKS) {  // item s's split sums -> LDS; wave s % 8 adds them in wave order
+        float* const red = s_ksred + (s & 1u) * (kWaves * 8u * 64u);
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+          red[(wave * 8u + j) * 64u + lane] = ag[j];
+          red[(wave * 8u + 4u + j) * 64u + lane] = au[j];
+        }
+        ag = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        au = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        lds_barrier();  // (the buffer of step s - 2 was read before step s - 1's barrier)
+        if (wave == s % kWaves) {
+#pragma unroll
+          for (uint32_t j = 0; j < 4; ++j) {
+            float gs = 0.0f, us = 0.0f;
+#pragma unroll
+            for (uint32_t w = 0; w < kWaves; ++w) {
+              gs += red[(w * 8u + j) * 64u + lane];
+              us += red[(w * 8u + 4u + j) * 64u + lane];
+            }
+            s_hb[((lane >> 4) * 4u + j) * kHb + s * 16u + (lane & 15u)] = nk::bf16_rne(nk::silu(gs) * us);
+          }
+        }
+      } else if constexpr (kQuant) {
         if (s % NA == NA - 1u) {  // item c0 + s / NA done: its 16 x 16 h block -> LDS
 #pragma unroll
           for (uint32_t j = 0; j < 4; ++j)
@@ -1240,13 +1269,14 @@ NK_FFN_PAIR(2048, 512, narrow, 8, 4, 1, 4, 1, 1, 4, 1)
 NK_FFN_PAIR(4096, 256, wide, 1, 1, 2, 2, 2, 2, 4, 1)
 NK_FFN_PAIR(4096, 256, narrow, 8, 2, 2, 2, 1, 1, 4, 1)
 
-// Symbols netra_moe_ffn_gate_up_down_h<H>_i<I>_gfx950: the wide gate/up with each
-// tile's down in the same workgroup (the tile's h requantised into LDS, the
-// expert's W2 streamed right behind its W13, fp32 route partials left to the
-// combine kernel): one launch and one weight stream per tile instead of two.
-#define NK_FFN_MERGED(HV, IV, CHG, PG)                                                               \
+// Symbols netra_moe_ffn_gate_up_down_h<H>_i<I>[_ksplit]_gfx950: the wide gate/up
+// with each tile's down in the same workgroup (the tile's h requantised into
+// LDS, the expert's W2 streamed right behind its W13, fp32 route partials left
+// to the combine kernel): one launch and one weight stream per tile instead of
+// two. _ksplit: gate/up K split over the waves, one 16-column item per step.
+#define NK_FFN_MERGED(HV, IV, CHG, PG, KSV, SFX)                                                    \
   NK_KERNEL __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))                         \
-  void netra_moe_ffn_gate_up_down_h##HV##_i##IV##_gfx950(                                                  \
+  void netra_moe_ffn_gate_up_down_h##HV##_i##IV##SFX##_gfx950(                                     \
       const uint16_t* __restrict__ logits, const float* __restrict__ bias,                         \
       int32_t* __restrict__ topk_ids, float* __restrict__ topk_weights, const uint8_t* __restrict__ xq, \
       const float* __restrict__ xs, const uint8_t* __restrict__ w13, const float* __restrict__ w13s, \
@@ -1255,14 +1285,15 @@ NK_FFN_PAIR(4096, 256, narrow, 8, 2, 2, 2, 1, 1, 4, 1)
       int32_t* __restrict__ counts, uint16_t* __restrict__ hrows, uint8_t* __restrict__ hq,        \
       float* __restrict__ hs, const uint8_t* __restrict__ w2, const float* __restrict__ w2s,       \
       float* __restrict__ partial, uint32_t T, uint32_t E, uint32_t K, uint32_t S, uint32_t cap_blocks) { \
-    nkffn::ffn_gate_up<HV / 128, IV / 128, 1, CHG, PG, true>(logits, bias, topk_ids, topk_weights, xq, xs, \
+    nkffn::ffn_gate_up<HV / 128, IV / 128, 1, CHG, PG, true, KSV>(logits, bias, topk_ids, topk_weights, xq, xs, \
                                                           w13, w13s, sorted_ids, sorted_expert,   \
                                                           tile_map, pair_map, num_valid, counts,  \
                                                           hrows, hq, hs, T, E, K, S, cap_blocks,  \
                                                           w2, w2s, partial);                      \
   }
-NK_FFN_MERGED(512, 256, 2, 2)
-NK_FFN_MERGED(2048, 512, 2, 4)
+NK_FFN_MERGED(512, 256, 2, 2, false, )
+NK_FFN_MERGED(2048, 512, 2, 4, false, )
+NK_FFN_MERGED(2048, 512, 2, 4, true, _ksplit)
 
 // Symbols netra_moe_ffn_down_h<H>_i<I>_rows_gfx950: the down for the narrow
 // gate/up's bf16 h rows (requantised per tile, as the narrow down does) with

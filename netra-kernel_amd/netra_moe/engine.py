@@ -416,6 +416,12 @@ SINGLE_DOWN = {(2048, 512)}
 # 24: 26.9 / 30.7, 64: 32.0 / 35.0. (H 4096, I 256 measured no faster:
 # 139.0 / 138.8 µs at T=64.)
 MERGED_FFN_T = {(512, 256): 17, (2048, 512): 22}
+# (H, I) -> the T from which the merged kernel splits gate/up's K over its
+# waves (netra_moe_ffn_gate_up_down_h<H>_i<I>_ksplit: the workgroup reads one
+# 16-column item's 64 KiB of W13 per step, split sums added in LDS), layer µs
+# against the unsplit merged kernel: T=24 88.9 / 88.4, 32 94.5 / 95.1, 64
+# 128.5 / 129.5
+MERGED_KSPLIT_T = {(2048, 512): 28}
 
 
 def down_variant(cfg: MoEConfig) -> str:
@@ -443,6 +449,8 @@ def ffn_lds_bytes(cfg: MoEConfig) -> tuple[int, int]:
     red = 8 * 8 * 64 * 4 if narrow else 0
     gu = max(kb * 2048, red, 1024 * 4 + 513 * 4) + 64 * kb + (8 if narrow else 16 * (128 * FFN_WIDE_P[(cfg.H, cfg.I)] + 8)) * 2
     gu += 64 * 16 * 4 + 512 * 8 + 2 * 513 * 4 + 48 * 4
+    if down_variant(cfg) == "merged" and cfg.T >= MERGED_KSPLIT_T.get((cfg.H, cfg.I), cfg.T + 1):
+        gu += 2 * 8 * 8 * 64 * 4  # the K split's sums, two steps
     dn = max(kbi * 2048, 0 if down_variant(cfg) == "rows" else red) + 64 * kbi + 4
     if down_variant(cfg) == "single":
         dn = 8 * 2 * cfg.I + 16 * 16 * 4
@@ -511,7 +519,8 @@ def _fused_decode(cfg: MoEConfig) -> list[dict]:
         ops[-1]["writes"] = ["h_q", "h_scale", "partial"]
     if down_variant(cfg) == "merged":  # gate/up runs each tile's down: its partials out, no down launch
         gu = ops[1]
-        gu["symbol"] = f"netra_moe_ffn_gate_up_down_h{H}_i{I}_gfx950"
+        ks = "_ksplit" if T >= MERGED_KSPLIT_T.get((H, I), T + 1) else ""
+        gu["symbol"] = f"netra_moe_ffn_gate_up_down_h{H}_i{I}{ks}_gfx950"
         i = gu["args"].index("h_scale") + 1
         gu["args"][i:i] = ["w2", "w2_scale", "partial"]
         gu["reads"] += ["w2", "w2_scale"]

@@ -70,11 +70,13 @@ EXTRA_CONFIGS = {
     "wide_t17_hot": MoEConfig("wide_t17_hot", T=17, H=2048, E=256, K=8, I=512, S=1, router_bias="hot",
                               seed=1112),
     "wide_t33": MoEConfig("wide_t33", T=33, H=2048, E=256, K=8, I=512, S=1, seed=1113),
-    # the gate/up + down per tile kernel: at H 512 with and without the shared
-    # expert, and with more tiles than workgroups (two rounds: ~330 experts)
-    "tile_t40_h512": MoEConfig("tile_t40_h512", T=40, H=512, E=16, K=2, I=256, S=1, seed=1128),
-    "tile_t23_h512_s0": MoEConfig("tile_t23_h512_s0", T=23, H=512, E=16, K=2, I=256, S=0, seed=1129),
-    "tile_t64_e384_k12": MoEConfig("tile_t64_e384_k12", T=64, H=2048, E=384, K=12, I=512, S=1, seed=1130),
+    # the merged gate/up + down per tile kernel: at H 512 with and without the
+    # shared expert, at H 2048 unsplit (T < 28) and K-split with more tiles than
+    # workgroups (two rounds: ~330 experts)
+    "merged_t40_h512": MoEConfig("merged_t40_h512", T=40, H=512, E=16, K=2, I=256, S=1, seed=1128),
+    "merged_t23_h512_s0": MoEConfig("merged_t23_h512_s0", T=23, H=512, E=16, K=2, I=256, S=0, seed=1129),
+    "merged_t25": MoEConfig("merged_t25", T=25, H=2048, E=256, K=8, I=512, S=1, seed=1131),
+    "merged_t64_e384_k12": MoEConfig("merged_t64_e384_k12", T=64, H=2048, E=384, K=12, I=512, S=1, seed=1130),
     # every hot expert with 64 rows (four tiles each, as the shared expert):
     # multi-tile experts throughout the wide decode FFN
     "wide_t64_hot": MoEConfig("wide_t64_hot", T=64, H=2048, E=256, K=8, I=512, S=1, router_bias="hot",

@@ -63,11 +63,13 @@
 //   netra_moe_ffn_down_h2048_i512_single_gfx950(the same arguments)   T = 1,
 //       grid H/16, block 512: a workgroup owns 16 output columns across all
 //       routes and writes out itself (partial for inspection; counters unused)
-//   netra_moe_ffn_gate_up_down_h<H>_i<I>_gfx950(the gate/up arguments, with w2, w2s and
-//       partial f32[T*Ktot,H] after hs)   (H, I) in {(512,256), (2048,512)}, grid 256,
-//       block 512: the wide gate/up, each workgroup then running its tile's down over
-//       all H columns from the requantised h in its LDS; the partials go to
-//       netra_moe_combine_gfx950 (used from T = 22 at H = 2048, T = 17 at H = 512)
+//   netra_moe_ffn_gate_up_down_h<H>_i<I>[_ksplit]_gfx950(the gate/up arguments, with w2,
+//       w2s and partial f32[T*Ktot,H] after hs)   (H, I) in {(512,256), (2048,512)}
+//       (_ksplit: (2048,512) only), grid 256, block 512: the wide gate/up (_ksplit: K
+//       split over the waves), each workgroup then running its tile's down over all H
+//       columns from the requantised h in its LDS; the partials go to
+//       netra_moe_combine_gfx950 (used from T = 22 at H = 2048, _ksplit from T = 28;
+//       from T = 17 at H = 512)
 //   netra_moe_ffn_down_h<H>_i<I>_rows_gfx950(the same arguments)   grid 2048,
 //       block 512: the narrow gate/up's bf16 rows (requantised per tile, hq / hs
 //       written for inspection) through the wide down's items; the partials go

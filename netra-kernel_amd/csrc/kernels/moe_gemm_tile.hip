@@ -519,12 +519,18 @@ __device__ __forceinline__ void down_rows(
     }
   };
 
-  auto run = [&](auto ntc) __attribute__((always_inline)) {
+  // One output group; kRefill: the next group's weight tiles and scales load
+  // under this one's MFMAs (the last group of the item, peeled, loads none:
+  // no load under a branch, whose join would make the compiler's wait counts
+  // drain the group in flight). kSplitF16 keeps one loop whose last refill
+  // repeats its group: peeled, it needs more than the 128 VGPRs of two
+  // workgroups per CU.
+  auto group = [&](auto ntc, auto refc, uint32_t q) __attribute__((always_inline)) {
     constexpr uint32_t NT = decltype(ntc)::value;
-#pragma unroll 1
-    for (uint32_t q = 0; q < NBC; ++q) {
-      const uint32_t nb = nb0 + q, nbn = nb0 + (q + 1u < NBC ? q + 1u : q);  // the last refill repeats nb
-      const float wsn = wse[nbn * KB + (lane & (KB - 1u))];
+    constexpr bool kRefill = decltype(refc)::value;
+    {
+      const uint32_t nb = nb0 + q, nbn = nb0 + (kRefill && q + 1u < NBC ? q + 1u : q);
+      const float wsn = kRefill ? wse[nbn * KB + (lane & (KB - 1u))] : 0.0f;
       v4f acc[NT];
 #pragma unroll
       for (uint32_t rt = 0; rt < NT; ++rt) acc[rt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
@@ -535,7 +541,8 @@ __device__ __forceinline__ void down_rows(
 #pragma unroll
         for (uint32_t rt = 0; rt < NT; ++rt)
           d[rt] = nk::mfma_e4m3_16x16x128(bq[kb], nk::load_tile_operand(&s_a[(rt * KB + kb) * 2048u], lane));
-        bq[kb] = nk::load_tile_operand<kAiter>(wt, ((nbn * 8u + wave) * KB + kb) * 2048u, lane);  // next group's tile
+        if constexpr (kRefill)  // the next group's tile
+          bq[kb] = nk::load_tile_operand<kAiter>(wt, ((nbn * 8u + wave) * KB + kb) * 2048u, lane);
 #pragma unroll
         for (uint32_t rt = 0; rt < NT; ++rt) {
           const float sc = ws * s_hs[kb * kRows + rt * 16u + (lane & 15u)];  // this lane's route row
@@ -558,9 +565,19 @@ __device__ __forceinline__ void down_rows(
           }
         }
       }
-      wsv = wsn;
+      if constexpr (kRefill) wsv = wsn;
       if constexpr (kSplitF16) emit(ntc, acc, 2u * q + 1u, nb, half_bytes);
       else emit(ntc, acc, q, nb, 0u);
+    }
+  };
+  auto run = [&](auto ntc) __attribute__((always_inline)) {
+    if constexpr (kSplitF16) {
+#pragma unroll 1
+      for (uint32_t q = 0; q < NBC; ++q) group(ntc, std::true_type{}, q);
+    } else {
+#pragma unroll 1
+      for (uint32_t q = 0; q + 1u < NBC; ++q) group(ntc, std::true_type{}, q);
+      group(ntc, std::false_type{}, NBC - 1u);
     }
   };
   switch (ntiles) {

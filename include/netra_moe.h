@@ -68,8 +68,8 @@
 //       (_ksplit: (2048,512) only), grid 256, block 512: the wide gate/up (_ksplit: K
 //       split over the waves), each workgroup then running its tile's down over all H
 //       columns from the requantised h in its LDS; the partials go to
-//       netra_moe_combine_gfx950 (used from T = 22 at H = 2048, _ksplit from T = 28;
-//       from T = 17 at H = 512)
+//       netra_moe_combine_gfx950 (used at H = 2048 from 128 expected tiles, _ksplit from
+//       150; at H = 512 for every T > 16)
 //   netra_moe_ffn_down_h<H>_i<I>_rows_gfx950(the same arguments)   grid 2048,
 //       block 512: the narrow gate/up's bf16 rows (requantised per tile, hq / hs
 //       written for inspection) through the wide down's items; the partials go

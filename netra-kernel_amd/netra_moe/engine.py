@@ -409,19 +409,32 @@ def ffn_variant(cfg: MoEConfig) -> str:
 # (H, I) with a single-token down kernel (netra_moe_ffn_down_h<H>_i<I>_single)
 SINGLE_DOWN = {(2048, 512)}
 # (H, I) with a gate/up + down per tile kernel (netra_moe_ffn_gate_up_down_h<H>_i<I>;
-# one wide gate/up item per tile) -> the T from which it replaces the wide
-# down, layer times measured on one MI355X against gate/up + down: H 2048,
-# I 512: T=17 82.2 / 80.3 µs, 21: 85.2 / 84.6, 22: 86.2 / 87.0, 23: 86.8 /
-# 88.3, 32: 95.3 / 97.6, 64: 130.6 / 131.1; H 512, I 256: T=17 25.7 / 28.7,
-# 24: 26.9 / 30.7, 64: 32.0 / 35.0. (H 4096, I 256 measured no faster:
-# 139.0 / 138.8 µs at T=64.)
-MERGED_FFN_T = {(512, 256): 17, (2048, 512): 22}
-# (H, I) -> the T from which the merged kernel splits gate/up's K over its
-# waves (netra_moe_ffn_gate_up_down_h<H>_i<I>_ksplit: the workgroup reads one
-# 16-column item's 64 KiB of W13 per step, split sums added in LDS), layer µs
-# against the unsplit merged kernel: T=24 88.9 / 88.4, 32 94.5 / 95.1, 64
-# 128.5 / 129.5
-MERGED_KSPLIT_T = {(2048, 512): 28}
+# one wide gate/up item per tile) -> the expected tile count (expected_tiles)
+# from which it replaces the wide down. The merged kernel streams each tile's
+# W13 and W2 from one workgroup, so it wants enough tiles to keep the chip
+# streaming; the separate down spreads each tile over many workgroups. Layer
+# times measured on one MI355X against gate/up + down (µs, merged / separate):
+# H 2048, I 512, E 256, K 8: T=21 (126.6 tiles) 85.2 / 84.6, 22 (130.7) 86.2 /
+# 87.0, 23 86.8 / 88.3, 32 95.3 / 97.6, 64 130.6 / 131.1; E 64: T=64 K=4 (67.0)
+# 82.4 / 72.1, T=48 K=6 (66.4) 80.9 / 71.7. H 512, I 256, from 19 tiles on:
+# E 16 K 2 T=40 (18.9) 23.5 / 25.2, E 64 K 4 T=32 (57.9) 24.1 / 25.7, E 128
+# K 8 T=24 25.6 / 28.0, E 256 T=17 25.7 / 28.7, T=64 32.0 / 35.0. (H 4096, I
+# 256: 138.0 / 138.6 at T=64, 97.6 / 96.8 at T=24, 85.2 / 70.2 with E 32 at
+# T=48: left out.)
+MERGED_MIN_TILES = {(512, 256): 0, (2048, 512): 128}
+# (H, I) -> the expected tile count from which the merged kernel splits
+# gate/up's K over its waves (netra_moe_ffn_gate_up_down_h<H>_i<I>_ksplit: the
+# workgroup reads one 16-column item's 64 KiB of W13 per step, split sums
+# added in LDS), layer µs against the unsplit merged kernel at E 256, K 8:
+# T=24 (137 tiles) 88.9 / 88.4, 32 (166) 94.5 / 95.1, 64 (226) 128.5 / 129.5
+MERGED_KSPLIT_MIN_TILES = {(2048, 512): 150}
+
+
+def expected_tiles(cfg: MoEConfig) -> float:
+    """16-row tiles of a decode call under uniform routing: the routed experts
+    a call is expected to touch, plus the shared experts' tiles."""
+    touched = cfg.E * (1.0 - (1.0 - cfg.K / cfg.E) ** cfg.T) if cfg.E else 0.0
+    return touched + cfg.S * ((cfg.T + 15) // 16)
 
 
 def down_variant(cfg: MoEConfig) -> str:
@@ -432,11 +445,11 @@ def down_variant(cfg: MoEConfig) -> str:
     weights: 38.4 / 41.4 / 44.8 / 49.0 against 39.7 / 43.8 / 49.1 / 53.1 µs
     at T = 5 .. 8, 35.2 against 34.0 at T = 4); merged (the down of each tile
     run by its wide gate/up workgroup, the combine kernel after it) from
-    MERGED_FFN_T tokens; else the FFN variant."""
+    MERGED_MIN_TILES expected tiles; else the FFN variant."""
     if cfg.T == 1 and (cfg.H, cfg.I) in SINGLE_DOWN and cfg.Ktot <= 16:
         return "single"
     v = ffn_variant(cfg)
-    if v == "wide" and cfg.T >= MERGED_FFN_T.get((cfg.H, cfg.I), cfg.T + 1):
+    if v == "wide" and expected_tiles(cfg) >= MERGED_MIN_TILES.get((cfg.H, cfg.I), float("inf")):
         return "merged"
     return "rows" if v == "narrow" and cfg.T >= NARROW_ROWS_DOWN_T else v
 
@@ -449,7 +462,7 @@ def ffn_lds_bytes(cfg: MoEConfig) -> tuple[int, int]:
     red = 8 * 8 * 64 * 4 if narrow else 0
     gu = max(kb * 2048, red, 1024 * 4 + 513 * 4) + 64 * kb + (8 if narrow else 16 * (128 * FFN_WIDE_P[(cfg.H, cfg.I)] + 8)) * 2
     gu += 64 * 16 * 4 + 512 * 8 + 2 * 513 * 4 + 48 * 4
-    if down_variant(cfg) == "merged" and cfg.T >= MERGED_KSPLIT_T.get((cfg.H, cfg.I), cfg.T + 1):
+    if down_variant(cfg) == "merged" and expected_tiles(cfg) >= MERGED_KSPLIT_MIN_TILES.get((cfg.H, cfg.I), float("inf")):
         gu += 2 * 8 * 8 * 64 * 4  # the K split's sums, two steps
     dn = max(kbi * 2048, 0 if down_variant(cfg) == "rows" else red) + 64 * kbi + 4
     if down_variant(cfg) == "single":
@@ -519,7 +532,7 @@ def _fused_decode(cfg: MoEConfig) -> list[dict]:
         ops[-1]["writes"] = ["h_q", "h_scale", "partial"]
     if down_variant(cfg) == "merged":  # gate/up runs each tile's down: its partials out, no down launch
         gu = ops[1]
-        ks = "_ksplit" if T >= MERGED_KSPLIT_T.get((H, I), T + 1) else ""
+        ks = "_ksplit" if expected_tiles(cfg) >= MERGED_KSPLIT_MIN_TILES.get((H, I), float("inf")) else ""
         gu["symbol"] = f"netra_moe_ffn_gate_up_down_h{H}_i{I}{ks}_gfx950"
         i = gu["args"].index("h_scale") + 1
         gu["args"][i:i] = ["w2", "w2_scale", "partial"]

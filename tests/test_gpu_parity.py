@@ -76,6 +76,8 @@ EXTRA_CONFIGS = {
     "merged_t40_h512": MoEConfig("merged_t40_h512", T=40, H=512, E=16, K=2, I=256, S=1, seed=1128),
     "merged_t23_h512_s0": MoEConfig("merged_t23_h512_s0", T=23, H=512, E=16, K=2, I=256, S=0, seed=1129),
     "merged_t25": MoEConfig("merged_t25", T=25, H=2048, E=256, K=8, I=512, S=1, seed=1131),
+    # too few tiles for the merged kernel at H 2048 (~67): the wide gate/up and down
+    "wide_t64_e64_k4": MoEConfig("wide_t64_e64_k4", T=64, H=2048, E=64, K=4, I=512, S=1, seed=1132),
     "merged_t64_e384_k12": MoEConfig("merged_t64_e384_k12", T=64, H=2048, E=384, K=12, I=512, S=1, seed=1130),
     # every hot expert with 64 rows (four tiles each, as the shared expert):
     # multi-tile experts throughout the wide decode FFN

@@ -240,3 +240,42 @@ def test_op_bridges_declare_the_reference_bridge_abis():
     names = declared(REPO / "include" / "netra_qwen36_bridges.h")
     assert sorted(names) == sorted(bridges.BRIDGE_SYMBOLS)
     assert len(names) == 24
+
+
+def test_merged_decode_ffn_follows_the_expected_tile_count():
+    """The fused path merges each tile's down into gate/up only when a call is
+    expected to have enough 16-row tiles to keep the chip streaming (the
+    expected count under uniform routing: E (1 - (1 - K/E)^T) + S ceil(T/16),
+    checked against a direct sum over experts), and splits gate/up's K over
+    the waves from a larger count; few-expert shapes keep the separate down."""
+    from netra_moe.engine import (MERGED_KSPLIT_MIN_TILES, MERGED_MIN_TILES, down_variant,
+                                  expected_tiles)
+
+    import numpy as np
+
+    def sampled(T, E, K, S, trials=400):  # touched experts of random uniform top-K routings
+        rng = np.random.default_rng(T * 1000 + E)
+        touched = [len(np.unique(np.argsort(rng.random((T, E)), axis=1)[:, :K])) for _ in range(trials)]
+        return float(np.mean(touched)) + S * ((T + 15) // 16)
+
+    def cfg(T, H, E, K, I, S=1):
+        return nm.MoEConfig(f"t{T}_h{H}_e{E}", T=T, H=H, E=E, K=K, I=I, S=S, seed=7)
+
+    for T, E, K, S in ((21, 256, 8, 1), (64, 64, 4, 1), (40, 16, 2, 0), (64, 384, 12, 1)):
+        assert expected_tiles(cfg(T, 2048, E, K, 512, S)) == pytest.approx(sampled(T, E, K, S), rel=0.01)
+    assert MERGED_MIN_TILES[(2048, 512)] < MERGED_KSPLIT_MIN_TILES[(2048, 512)]
+    sym = lambda c: next(op["symbol"] for op in operations(c) if op["name"] == "moe.gate_up")  # noqa: E731
+    # H 2048, E 256, K 8: wide at T = 21 (126.6 tiles), merged from T = 22 (130.7), K split from T = 28
+    assert down_variant(cfg(21, 2048, 256, 8, 512)) == "wide"
+    assert op_names(cfg(21, 2048, 256, 8, 512)) == ("route", "gate_up", "down", "combine")
+    assert sym(cfg(22, 2048, 256, 8, 512)) == "netra_moe_ffn_gate_up_down_h2048_i512_gfx950"
+    assert op_names(cfg(22, 2048, 256, 8, 512)) == ("route", "gate_up", "combine")
+    assert sym(cfg(27, 2048, 256, 8, 512)) == "netra_moe_ffn_gate_up_down_h2048_i512_gfx950"
+    assert sym(cfg(28, 2048, 256, 8, 512)) == "netra_moe_ffn_gate_up_down_h2048_i512_ksplit_gfx950"
+    # few experts at H 2048 (~67 tiles): the separate down
+    assert down_variant(cfg(64, 2048, 64, 4, 512)) == "wide"
+    # H 512: merged at every wide T; H 4096 and (1024, 1024): never; narrow T: never
+    assert down_variant(cfg(17, 512, 16, 2, 256, 0)) == "merged"
+    assert down_variant(cfg(64, 4096, 256, 8, 256)) == "wide"
+    assert down_variant(cfg(40, 1024, 24, 3, 1024)) == "wide"
+    assert down_variant(cfg(16, 2048, 256, 8, 512)) == "rows"

@@ -18,6 +18,12 @@
 // combine launch costs). The rows down takes the narrow gate/up's bf16 rows
 // through the wide down's items and leaves the combine to the same kernel;
 // from five tokens it is the faster of the two after the narrow gate/up.
+//   netra_moe_ffn_gate_up_down_h<H>_i<I>[_ksplit]_gfx950(the gate/up arguments
+//       with w2, w2s and partial after hs)
+//     the wide gate/up with each tile's down run by the same workgroup from the
+//     requantised h in its LDS (fp32 partials to the combine kernel); _ksplit
+//     splits gate/up's K over the waves. Chosen when a call has enough tiles
+//     to keep the chip streaming.
 //   block 512 (8 waves), any grid
 // Weights are read with non-temporal loads: every tile is read by one
 // workgroup per launch (the tiles of an expert with more than 16 routes by
